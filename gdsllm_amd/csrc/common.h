@@ -1,0 +1,112 @@
+// Shared helpers for the gfx950 kernels and the C ABI around them.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "gdsllm_amd.h"
+
+namespace gdsllm {
+
+// ----------------------------------------------------------------- host side
+
+// Records `msg` as this thread's last error and returns `code`.
+int set_error(int code, const std::string& msg);
+// Clears the thread's last error and returns GDSLLM_OK.
+int ok();
+// Checks the result of a HIP call or launch; on failure records
+// "<what>: <hip error string>" and returns GDSLLM_ERR_HIP.
+int check_hip(hipError_t err, const char* what);
+// Number of compute units of the current device (cached per device).
+int cu_count();
+// Maximum dynamic LDS bytes a workgroup may use on the current device.
+int max_lds_bytes();
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ---------------------------------------------------------------- device side
+
+typedef _Float16 half_t;
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming (non-temporal) global load.
+__device__ __forceinline__ uint4 load_nt16(const void* p) {
+    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ float h2f(uint32_t bits16) {
+    return static_cast<float>(__builtin_bit_cast(half_t, static_cast<uint16_t>(bits16)));
+}
+// Returns `v` as a materialized fp32 register value.  Without it the compiler
+// folds "fp32 multiply(-add), then convert to fp16" into one v_fma_mixlo_f16,
+// which rounds once (the reference rounds to fp32 first) and adds +0 to a
+// plain product (turning an IEEE -0 into +0).  Bit-exact paths need both
+// roundings and the sign of zero, so they pass through this barrier.
+__device__ __forceinline__ float fp32_rounded(float v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+__device__ __forceinline__ uint16_t f2h_bits(float v) {
+    return __builtin_bit_cast(uint16_t, static_cast<half_t>(v));
+}
+__device__ __forceinline__ uint32_t pack_h2(half_t lo, half_t hi) {
+    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, lo)) |
+           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hi)) << 16);
+}
+
+// fp32 += a.lo*b.lo + a.hi*b.hi with a, b packed fp16 pairs (v_dot2_f32_f16).
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, a),
+                                  __builtin_bit_cast(half2_t, b), c, false);
+}
+
+// Bytes [2, 6) of the little-endian pair (lo, hi): re-aligns a dword stream
+// that starts on a 2-byte boundary.
+__device__ __forceinline__ uint32_t align2(uint32_t lo, uint32_t hi) {
+    return __builtin_amdgcn_alignbyte(hi, lo, 2);
+}
+
+// Two fp16 weights from two 4-bit fields of `v`.  Fields at bits [0,4) and
+// [16,20) become 1024+q (exponent 2^10, ulp 1); fields at bits [4,8) and
+// [20,24) become 64+q (exponent 2^6, ulp 1/16 so bits 4..7 weigh 1).
+__device__ __forceinline__ uint32_t nib_lo_pair(uint32_t v) {
+    return (v & 0x000F000Fu) | 0x64006400u;
+}
+__device__ __forceinline__ uint32_t nib_hi_pair(uint32_t v) {
+    return (v & 0x00F000F0u) | 0x54005400u;
+}
+
+// Sum over the 16 lanes of each DPP row (lanes 16r .. 16r+15).
+__device__ __forceinline__ float row16_sum(float v) {
+    v += __shfl_xor(v, 8, 16);
+    v += __shfl_xor(v, 4, 16);
+    v += __shfl_xor(v, 2, 16);
+    v += __shfl_xor(v, 1, 16);
+    return v;
+}
+// Sum over groups of `width` lanes (power of two <= 64).
+template <int WIDTH>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int o = WIDTH / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, WIDTH);
+    return v;
+}
+
+// Orders this wave's earlier LDS writes before its later LDS reads.  LDS
+// requests of one wavefront are served in issue order; the waitcnt and the
+// memory clobber keep the compiler from moving reads above the writes.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
+}
+
+}  // namespace gdsllm

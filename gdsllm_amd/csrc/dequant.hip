@@ -1,0 +1,269 @@
+// Bit-exact fp16 dequantization of GGUF Q4_0 / Q8_0 blocks and affine-Q4
+// groups (the reference's runtime/gguf_dequant.cu and the dequant half of
+// runtime/affine_q4_dequant.cu).
+//
+// Each output element is ONE round-to-nearest-even to fp16 of the fp32 value
+// the reference forms: d*(q-8) and d*q are exact in fp32 (11-bit by 5/8-bit
+// products), nib*s+b is an exact product plus one fp32 rounding.  HBM-bound:
+// 18 (or 34) bytes in and 64 bytes out per 32 weights, so the kernels are
+// shaped for write coalescing: a thread owns two consecutive blocks (a
+// 4-byte-aligned 36 / 68 byte span), and the 128 output bytes it produces
+// leave as eight 16-byte stores.
+
+#include "common.h"
+
+namespace gdsllm {
+namespace {
+
+constexpr int kThreads = 256;
+
+// ---- Q4_0 -------------------------------------------------------------------
+// Block: fp16 d, then 16 bytes qs; element j = d*((qs[j] & 15) - 8),
+// element j+16 = d*((qs[j] >> 4) - 8)  (runtime/gguf_dequant.cu:84-107).
+__device__ __forceinline__ void q4_block_to_fp16(uint32_t d_bits, const uint32_t q[4], uint32_t out[16]) {
+    const float d = h2f(d_bits);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        uint32_t lo2[2], hi2[2];
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const uint32_t b0 = (q[w] >> (16 * p)) & 0xFFu;
+            const uint32_t b1 = (q[w] >> (16 * p + 8)) & 0xFFu;
+            const uint16_t l0 = f2h_bits(fp32_rounded(d * static_cast<float>(static_cast<int>(b0 & 15u) - 8)));
+            const uint16_t l1 = f2h_bits(fp32_rounded(d * static_cast<float>(static_cast<int>(b1 & 15u) - 8)));
+            const uint16_t h0 = f2h_bits(fp32_rounded(d * static_cast<float>(static_cast<int>(b0 >> 4) - 8)));
+            const uint16_t h1 = f2h_bits(fp32_rounded(d * static_cast<float>(static_cast<int>(b1 >> 4) - 8)));
+            lo2[p] = static_cast<uint32_t>(l0) | (static_cast<uint32_t>(l1) << 16);
+            hi2[p] = static_cast<uint32_t>(h0) | (static_cast<uint32_t>(h1) << 16);
+        }
+        out[2 * w] = lo2[0];
+        out[2 * w + 1] = lo2[1];
+        out[8 + 2 * w] = hi2[0];
+        out[8 + 2 * w + 1] = hi2[1];
+    }
+}
+
+// Two blocks (36 bytes = 9 dwords) per thread.  `src` must be 4-byte aligned.
+__global__ __launch_bounds__(kThreads) void dequant_q4_0_pairs(const uint32_t* __restrict__ src,
+                                                                uint4* __restrict__ dst,
+                                                                int64_t num_pairs) {
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (p >= num_pairs) return;
+    const uint32_t* s = src + p * 9;
+    uint32_t v[9];
+#pragma unroll
+    for (int i = 0; i < 9; ++i) v[i] = __builtin_nontemporal_load(s + i);
+    // block 0: d = bytes 0-1, qs = bytes 2..17; block 1: d = bytes 18-19, qs = 20..35
+    uint32_t q0[4] = {align2(v[0], v[1]), align2(v[1], v[2]), align2(v[2], v[3]), align2(v[3], v[4])};
+    uint32_t q1[4] = {v[5], v[6], v[7], v[8]};
+    uint32_t o[16];
+    uint4* out = dst + p * 8;
+    q4_block_to_fp16(v[0] & 0xFFFFu, q0, o);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+    q4_block_to_fp16(v[4] >> 16, q1, o);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[4 + i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+}
+
+// One block per thread, byte loads: any alignment, any count (tail / odd cases).
+__global__ __launch_bounds__(kThreads) void dequant_q4_0_bytes(const uint8_t* __restrict__ src,
+                                                                uint16_t* __restrict__ dst,
+                                                                int64_t first, int64_t num_blocks) {
+    const int64_t b = first + static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (b >= num_blocks) return;
+    const uint8_t* s = src + b * 18;
+    const float d = h2f(static_cast<uint32_t>(s[0]) | (static_cast<uint32_t>(s[1]) << 8));
+    uint16_t* o = dst + b * 32;
+    for (int j = 0; j < 16; ++j) {
+        const int byte = s[2 + j];
+        o[j] = f2h_bits(fp32_rounded(d * static_cast<float>((byte & 15) - 8)));
+        o[j + 16] = f2h_bits(fp32_rounded(d * static_cast<float>((byte >> 4) - 8)));
+    }
+}
+
+// ---- Q8_0 -------------------------------------------------------------------
+// Block: fp16 d, then int8 qs[32]; element i = d*qs[i] (runtime/gguf_dequant.cu:40-57).
+__device__ __forceinline__ void q8_block_to_fp16(uint32_t d_bits, const uint32_t q[8], uint4* out) {
+    const float d = h2f(d_bits);
+#pragma unroll
+    for (int w = 0; w < 8; w += 2) {
+        uint32_t o[4];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t v = q[w + h];
+            const float a = fp32_rounded(d * static_cast<float>(static_cast<int8_t>(v & 0xFFu)));
+            const float b = fp32_rounded(d * static_cast<float>(static_cast<int8_t>((v >> 8) & 0xFFu)));
+            const float c = fp32_rounded(d * static_cast<float>(static_cast<int8_t>((v >> 16) & 0xFFu)));
+            const float e = fp32_rounded(d * static_cast<float>(static_cast<int8_t>(v >> 24)));
+            o[2 * h] = static_cast<uint32_t>(f2h_bits(a)) | (static_cast<uint32_t>(f2h_bits(b)) << 16);
+            o[2 * h + 1] = static_cast<uint32_t>(f2h_bits(c)) | (static_cast<uint32_t>(f2h_bits(e)) << 16);
+        }
+        out[w / 2] = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+}
+
+// Two blocks (68 bytes = 17 dwords) per thread.  `src` must be 4-byte aligned.
+__global__ __launch_bounds__(kThreads) void dequant_q8_0_pairs(const uint32_t* __restrict__ src,
+                                                                uint4* __restrict__ dst,
+                                                                int64_t num_pairs) {
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (p >= num_pairs) return;
+    const uint32_t* s = src + p * 17;
+    uint32_t v[17];
+#pragma unroll
+    for (int i = 0; i < 17; ++i) v[i] = __builtin_nontemporal_load(s + i);
+    // block 0: d = bytes 0-1, qs = bytes 2..33; block 1: d = bytes 34-35, qs = 36..67
+    uint32_t q0[8], q1[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        q0[i] = align2(v[i], v[i + 1]);
+        q1[i] = v[9 + i];
+    }
+    uint4* out = dst + p * 8;
+    q8_block_to_fp16(v[0] & 0xFFFFu, q0, out);
+    q8_block_to_fp16(v[8] >> 16, q1, out + 4);
+}
+
+__global__ __launch_bounds__(kThreads) void dequant_q8_0_bytes(const uint8_t* __restrict__ src,
+                                                                uint16_t* __restrict__ dst,
+                                                                int64_t first, int64_t num_blocks) {
+    const int64_t b = first + static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (b >= num_blocks) return;
+    const uint8_t* s = src + b * 34;
+    const float d = h2f(static_cast<uint32_t>(s[0]) | (static_cast<uint32_t>(s[1]) << 8));
+    uint16_t* o = dst + b * 32;
+    for (int j = 0; j < 32; ++j) o[j] = f2h_bits(fp32_rounded(d * static_cast<float>(static_cast<int8_t>(s[2 + j]))));
+}
+
+// ---- affine Q4 --------------------------------------------------------------
+// Word w holds elements 8w..8w+7, nibble n = (word >> 4n) & 15 (LSB first);
+// group = element / group_size over the flat index; value = nib*s + b in fp32,
+// then one fp16 rounding (runtime/affine_q4_dequant.cu:28-59).  One thread per
+// word: coalesced dword loads and 16-byte stores.
+__global__ __launch_bounds__(kThreads) void dequant_affine_words(const uint32_t* __restrict__ w,
+                                                                  const uint16_t* __restrict__ scales,
+                                                                  const uint16_t* __restrict__ biases,
+                                                                  uint4* __restrict__ dst,
+                                                                  int64_t num_words, int words_per_group) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (i >= num_words) return;
+    const int64_t g = i / words_per_group;
+    const float s = h2f(scales[g]);
+    const float b = h2f(biases[g]);
+    const uint32_t v = __builtin_nontemporal_load(w + i);
+    uint32_t o[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float lo = fp32_rounded(static_cast<float>((v >> (8 * k)) & 15u) * s + b);
+        const float hi = fp32_rounded(static_cast<float>((v >> (8 * k + 4)) & 15u) * s + b);
+        o[k] = static_cast<uint32_t>(f2h_bits(lo)) | (static_cast<uint32_t>(f2h_bits(hi)) << 16);
+    }
+    dst[i] = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// Destination not 16-byte aligned: one thread per element.
+__global__ __launch_bounds__(kThreads) void dequant_affine_elems(const uint32_t* __restrict__ w,
+                                                                  const uint16_t* __restrict__ scales,
+                                                                  const uint16_t* __restrict__ biases,
+                                                                  uint16_t* __restrict__ dst,
+                                                                  int64_t num_elements, int group_size) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (i >= num_elements) return;
+    const int64_t g = i / group_size;
+    const uint32_t nib = (w[i >> 3] >> (4 * (i & 7))) & 15u;
+    dst[i] = f2h_bits(fp32_rounded(static_cast<float>(nib) * h2f(scales[g]) + h2f(biases[g])));
+}
+
+int grid_for(int64_t n) { return static_cast<int>((n + kThreads - 1) / kThreads); }
+
+}  // namespace
+}  // namespace gdsllm
+
+using namespace gdsllm;
+
+extern "C" int gdsllm_dequant_q4_0(const void* src, void* dst, int64_t num_blocks, void* stream) {
+    if (num_blocks < 0) return set_error(GDSLLM_ERR_INVALID_ARGUMENT, "dequant_q4_0: negative block count");
+    if (num_blocks == 0) return ok();
+    if (!src || !dst) return set_error(GDSLLM_ERR_INVALID_ARGUMENT, "dequant_q4_0: null pointer");
+    if (num_blocks > (int64_t(1) << 40)) return set_error(GDSLLM_ERR_INVALID_ARGUMENT, "dequant_q4_0: block count too large");
+    hipStream_t s = as_stream(stream);
+    const bool aligned = (reinterpret_cast<uintptr_t>(src) % 4 == 0) && (reinterpret_cast<uintptr_t>(dst) % 16 == 0);
+    int64_t done = 0;
+    if (aligned) {
+        const int64_t pairs = num_blocks / 2;
+        if (pairs > 0) {
+            hipLaunchKernelGGL(dequant_q4_0_pairs, dim3(grid_for(pairs)), dim3(kThreads), 0, s,
+                               static_cast<const uint32_t*>(src), static_cast<uint4*>(dst), pairs);
+            done = pairs * 2;
+        }
+    }
+    if (done < num_blocks) {
+        hipLaunchKernelGGL(dequant_q4_0_bytes, dim3(grid_for(num_blocks - done)), dim3(kThreads), 0, s,
+                           static_cast<const uint8_t*>(src), static_cast<uint16_t*>(dst), done, num_blocks);
+    }
+    if (int rc = check_hip(hipGetLastError(), "dequant_q4_0 launch")) return rc;
+    return ok();
+}
+
+extern "C" int gdsllm_dequant_q8_0(const void* src, void* dst, int64_t num_blocks, void* stream) {
+    if (num_blocks < 0) return set_error(GDSLLM_ERR_INVALID_ARGUMENT, "dequant_q8_0: negative block count");
+    if (num_blocks == 0) return ok();
+    if (!src || !dst) return set_error(GDSLLM_ERR_INVALID_ARGUMENT, "dequant_q8_0: null pointer");
+    if (num_blocks > (int64_t(1) << 40)) return set_error(GDSLLM_ERR_INVALID_ARGUMENT, "dequant_q8_0: block count too large");
+    hipStream_t s = as_stream(stream);
+    const bool aligned = (reinterpret_cast<uintptr_t>(src) % 4 == 0) && (reinterpret_cast<uintptr_t>(dst) % 16 == 0);
+    int64_t done = 0;
+    if (aligned) {
+        const int64_t pairs = num_blocks / 2;
+        if (pairs > 0) {
+            hipLaunchKernelGGL(dequant_q8_0_pairs, dim3(grid_for(pairs)), dim3(kThreads), 0, s,
+                               static_cast<const uint32_t*>(src), static_cast<uint4*>(dst), pairs);
+            done = pairs * 2;
+        }
+    }
+    if (done < num_blocks) {
+        hipLaunchKernelGGL(dequant_q8_0_bytes, dim3(grid_for(num_blocks - done)), dim3(kThreads), 0, s,
+                           static_cast<const uint8_t*>(src), static_cast<uint16_t*>(dst), done, num_blocks);
+    }
+    if (int rc = check_hip(hipGetLastError(), "dequant_q8_0 launch")) return rc;
+    return ok();
+}
+
+extern "C" int gdsllm_dequant_affine_q4(const void* weight, const void* scales, const void* biases,
+                                        void* dst, int64_t num_elements, int64_t in_dim,
+                                        int64_t group_size, void* stream) {
+    if (num_elements < 0) return set_error(GDSLLM_ERR_INVALID_ARGUMENT, "dequant_affine_q4: negative element count");
+    if (num_elements == 0) return ok();
+    if (group_size <= 0) return set_error(GDSLLM_ERR_INVALID_ARGUMENT, "dequant_affine_q4: group_size must be positive");
+    if (group_size > (int64_t(1) << 30)) return set_error(GDSLLM_ERR_INVALID_ARGUMENT, "dequant_affine_q4: group_size too large");
+    // The format stores whole words per group (the reference kernel indexes
+    // weight + group * (group_size / 8), runtime/affine_q4_dequant.cu:42-46).
+    if (group_size % 8 != 0)
+        return set_error(GDSLLM_ERR_UNSUPPORTED, "dequant_affine_q4: group_size must be a multiple of 8");
+    if (in_dim <= 0 || in_dim % group_size != 0)
+        return set_error(GDSLLM_ERR_INVALID_ARGUMENT, "dequant_affine_q4: in_dim must be a positive multiple of group_size");
+    if (num_elements % 8 != 0 || num_elements % group_size != 0)
+        return set_error(GDSLLM_ERR_INVALID_ARGUMENT,
+                         "dequant_affine_q4: element count must be a multiple of 8 and of group_size");
+    if (!weight || !scales || !biases || !dst)
+        return set_error(GDSLLM_ERR_INVALID_ARGUMENT, "dequant_affine_q4: null pointer");
+    if (reinterpret_cast<uintptr_t>(weight) % 4 != 0 || reinterpret_cast<uintptr_t>(scales) % 2 != 0 ||
+        reinterpret_cast<uintptr_t>(biases) % 2 != 0 || reinterpret_cast<uintptr_t>(dst) % 2 != 0)
+        return set_error(GDSLLM_ERR_INVALID_ARGUMENT, "dequant_affine_q4: misaligned pointer");
+    hipStream_t s = as_stream(stream);
+    if (reinterpret_cast<uintptr_t>(dst) % 16 == 0) {
+        const int64_t words = num_elements / 8;
+        hipLaunchKernelGGL(dequant_affine_words, dim3(grid_for(words)), dim3(kThreads), 0, s,
+                           static_cast<const uint32_t*>(weight), static_cast<const uint16_t*>(scales),
+                           static_cast<const uint16_t*>(biases), static_cast<uint4*>(dst), words,
+                           static_cast<int>(group_size / 8));
+    } else {
+        hipLaunchKernelGGL(dequant_affine_elems, dim3(grid_for(num_elements)), dim3(kThreads), 0, s,
+                           static_cast<const uint32_t*>(weight), static_cast<const uint16_t*>(scales),
+                           static_cast<const uint16_t*>(biases), static_cast<uint16_t*>(dst), num_elements,
+                           static_cast<int>(group_size));
+    }
+    if (int rc = check_hip(hipGetLastError(), "dequant_affine_q4 launch")) return rc;
+    return ok();
+}

@@ -1,0 +1,60 @@
+"""GGUF projection dispatch of the LLaMA forward pass, over the gfx950 kernels.
+
+Mirrors runtime/llama.py:106-166 of the reference: same function names,
+arguments and weight-metadata dicts ({"buffer", "shape", "gguf_type",
+"offset"}, built at runtime/torch_bridge.py:125-132), same decode/prefill rule
+(x.shape[1] == 1 -> fused dequant+GEMV).  Differences, all on the fast side of
+the same contract:
+  * decode with batch > 1 (x [B, 1, K], B <= 8) runs one batched fused GEMV
+    instead of failing the reference's x.view(-1) size check;
+  * Q4_0 prefill runs the fused MFMA dequant-GEMM instead of dequant + GEMM.
+Q8_0 prefill keeps the reference's dequant -> F.linear route.
+"""
+
+from __future__ import annotations
+
+from typing import Dict, Optional
+
+import torch
+import torch.nn.functional as F
+
+from . import ext
+
+
+def _dequant_gguf(meta: dict, scratch: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """fp16 dequantization of a GGUF tensor (runtime/llama.py:106-119)."""
+    return ext().dequant_gguf(meta["buffer"], meta["shape"], meta["gguf_type"], meta["offset"], scratch)
+
+
+def _fused_dequant_gemv(x: torch.Tensor, meta: dict) -> torch.Tensor:
+    """Fused dequant + GEMV for decode (runtime/llama.py:122-141).
+
+    x: (batch, 1, in_dim) fp16 -> (batch, 1, out_dim) fp16.
+    """
+    batch = x.shape[0] if x.dim() == 3 else 1
+    out = ext().fused_dequant_gemv(
+        meta["buffer"], x.reshape(batch, -1), meta["shape"], meta["gguf_type"], meta["offset"]
+    )
+    return out.unsqueeze(1)
+
+
+def _fused_dequant_gemm(x: torch.Tensor, meta: dict) -> torch.Tensor:
+    """Prefill Q4_0 projection on the MFMA dequant-GEMM: (B, S, K) -> (B, S, M)."""
+    return ext().fused_dequant_gemm(meta["buffer"], x, meta["shape"], meta["gguf_type"], meta["offset"])
+
+
+def dequant_linear(
+    x: torch.Tensor, weights: Dict[str, torch.Tensor], name: str, scratch: Optional[torch.Tensor] = None
+) -> torch.Tensor:
+    """F.linear with on-the-fly dequantization (runtime/llama.py:144-166)."""
+    w = weights[f"{name}.weight"]
+    if isinstance(w, dict) and "gguf_type" in w:
+        if x.shape[1] == 1 and x.shape[0] <= 8:
+            return _fused_dequant_gemv(x, w)
+        if w["gguf_type"] == "q4_0" and w["shape"][1] % 64 == 0:
+            return _fused_dequant_gemm(x, w)
+        w = _dequant_gguf(w, scratch)
+    elif w.dtype == torch.int8:
+        scale = weights[f"{name}.scale"]
+        w = (w.float() * scale).half()
+    return F.linear(x, w)

@@ -1,0 +1,158 @@
+"""Affine-Q4 projection dispatch and the MoE MLP of the Qwen-MoE forward pass.
+
+Mirrors runtime/qwen_moe.py:20-73 and :386-513 of the reference (same names,
+arguments and metadata dicts {"buffer", "shape", "quant_type",
+"weight_offset", "scale_offset", "bias_offset", "group_size"}).
+
+The decode MoE path changes shape, not contract: instead of syncing the
+selected expert ids to the host and running 3 GEMV launches per expert over
+per-expert buffers (runtime/qwen_moe.py:455-474), the stacked [E, N, K]
+expert tensors stay resident and one gather kernel pair reads the selected
+experts by index on the device (`moe_gather`).  The reference's per-expert
+route (expert_tensors from load_experts) is still accepted.
+"""
+
+from __future__ import annotations
+
+from typing import Dict, Optional, Tuple
+
+import torch
+import torch.nn.functional as F
+
+from . import ext
+
+
+def _dequant_affine_q4(meta: dict, scratch: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """runtime/qwen_moe.py:20-35."""
+    return ext().dequant_affine_q4(
+        meta["buffer"], meta["shape"], meta["weight_offset"], meta["scale_offset"], meta["bias_offset"],
+        meta["group_size"], scratch,
+    )
+
+
+def _fused_affine_q4_gemv(x: torch.Tensor, meta: dict) -> torch.Tensor:
+    """runtime/qwen_moe.py:38-55: (batch, 1, in_dim) -> (batch, 1, out_dim)."""
+    batch = x.shape[0] if x.dim() == 3 else 1
+    out = ext().fused_affine_q4_gemv(
+        meta["buffer"], x.reshape(batch, -1), meta["shape"], meta["weight_offset"], meta["scale_offset"],
+        meta["bias_offset"], meta["group_size"],
+    )
+    return out.unsqueeze(1)
+
+
+def affine_q4_linear(x: torch.Tensor, weights: Dict, name: str, scratch: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """runtime/qwen_moe.py:58-73: fused GEMV for decode, dequant + F.linear otherwise."""
+    w = weights[f"{name}.weight"]
+    if isinstance(w, dict) and w.get("quant_type") == "affine_q4":
+        if x.shape[1] == 1 and x.shape[0] <= 8:
+            return _fused_affine_q4_gemv(x, w)
+        w = _dequant_affine_q4(w, scratch)
+    return F.linear(x, w)
+
+
+def moe_route(
+    x: torch.Tensor, weights: Dict, num_experts_per_token: int, scratch: Optional[torch.Tensor] = None
+) -> Tuple[torch.Tensor, torch.Tensor, list]:
+    """runtime/qwen_moe.py:386-416: router logits -> top-k -> softmax (fp32) -> fp16."""
+    router_w = weights["mlp.gate.weight"]
+    if isinstance(router_w, dict):
+        router_w = _dequant_affine_q4(router_w, scratch)
+    logits = F.linear(x, router_w)
+    top_logits, top_idx = torch.topk(logits, num_experts_per_token, dim=-1)
+    top_w = F.softmax(top_logits.float(), dim=-1).type_as(x)
+    return top_idx, top_w, top_idx.unique().tolist()
+
+
+_EXPERT_PROJ = ("mlp.switch_mlp.gate_proj", "mlp.switch_mlp.up_proj", "mlp.switch_mlp.down_proj")
+
+
+def moe_gather(x: torch.Tensor, weights: Dict, top_k_indices: torch.Tensor, top_k_weights: torch.Tensor) -> torch.Tensor:
+    """Decode expert MLP over resident stacked experts: sum_k w_k * down_k(silu(gate_k x) * up_k x).
+
+    x: (1, 1, hidden); weights holds the three stacked affine_q4 entries
+    (shape [E, N, K]).  Returns (1, 1, hidden) fp16.
+    """
+    g, u, d = (weights[f"{p}.weight"] for p in _EXPERT_PROJ)
+    out = ext().moe_gather_affine_q4(
+        x.reshape(-1),
+        g["buffer"], g["shape"], g["weight_offset"], g["scale_offset"], g["bias_offset"],
+        u["buffer"], u["shape"], u["weight_offset"], u["scale_offset"], u["bias_offset"],
+        d["buffer"], d["shape"], d["weight_offset"], d["scale_offset"], d["bias_offset"],
+        g["group_size"], top_k_indices.reshape(-1), top_k_weights.reshape(-1),
+    )
+    return out.view(1, 1, -1)
+
+
+def _expert_meta(stacked: dict, e: int) -> dict:
+    """One expert's slice of a stacked [E, N, K] affine_q4 entry (runtime/torch_bridge.py:326-337)."""
+    E, N, K = stacked["shape"]
+    g = stacked["group_size"]
+    return {
+        "buffer": stacked["buffer"],
+        "shape": [N, K],
+        "quant_type": "affine_q4",
+        "weight_offset": stacked["weight_offset"] + e * N * (K // 8) * 4,
+        "scale_offset": stacked["scale_offset"] + e * N * (K // g) * 2,
+        "bias_offset": stacked["bias_offset"] + e * N * (K // g) * 2,
+        "group_size": g,
+    }
+
+
+def moe_mlp_selective(
+    x: torch.Tensor,
+    weights: Dict,
+    expert_tensors: Optional[Dict[str, dict]],
+    top_k_indices: torch.Tensor,
+    top_k_weights: torch.Tensor,
+    num_experts_per_token: int,
+    scratch: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """runtime/qwen_moe.py:419-513.  expert_tensors=None selects the resident
+    stacked experts in `weights` (decode: one on-device gather)."""
+    batch, seq_len, hidden = x.shape
+    x_flat = x.view(-1, hidden)
+    n_tok = x_flat.shape[0]
+    resident = expert_tensors is None
+    if resident and n_tok == 1:
+        expert_output = moe_gather(x, weights, top_k_indices, top_k_weights).view(1, hidden)
+    else:
+        def meta(proj: str, e: int) -> dict:
+            if resident:
+                return _expert_meta(weights[f"mlp.switch_mlp.{proj}.weight"], e)
+            return expert_tensors[f"{proj}.{e}"]
+
+        expert_output = torch.zeros(n_tok, hidden, device=x.device, dtype=x.dtype)
+        idx = top_k_indices.view(n_tok, num_experts_per_token)
+        wts = top_k_weights.view(n_tok, num_experts_per_token)
+        for k in range(num_experts_per_token):
+            ids, ew = idx[:, k], wts[:, k]
+            if n_tok == 1:
+                e = int(ids[0].item())
+                gate = _fused_affine_q4_gemv(x_flat.view(1, 1, -1), meta("gate_proj", e))
+                up = _fused_affine_q4_gemv(x_flat.view(1, 1, -1), meta("up_proj", e))
+                down = _fused_affine_q4_gemv(F.silu(gate) * up, meta("down_proj", e))
+                expert_output += ew.unsqueeze(-1) * down.view(n_tok, -1)
+            else:
+                for e_t in ids.unique():
+                    e = int(e_t.item())
+                    mask = ids == e
+                    xs = x_flat[mask]
+                    gw = _dequant_affine_q4(meta("gate_proj", e), scratch)
+                    gate = F.linear(xs, gw)
+                    uw = _dequant_affine_q4(meta("up_proj", e), scratch)
+                    up = F.linear(xs, uw)
+                    dw = _dequant_affine_q4(meta("down_proj", e), scratch)
+                    down = F.linear(F.silu(gate) * up, dw)
+                    expert_output[mask] += ew[mask].unsqueeze(-1) * down
+    expert_output = expert_output.view(batch, seq_len, hidden)
+
+    if "mlp.shared_expert.gate_proj.weight" not in weights:
+        return expert_output.clamp(min=-65504.0, max=65504.0)
+    shared_gate = affine_q4_linear(x, weights, "mlp.shared_expert.gate_proj", scratch)
+    shared_up = affine_q4_linear(x, weights, "mlp.shared_expert.up_proj", scratch)
+    shared_out = affine_q4_linear(F.silu(shared_gate) * shared_up, weights, "mlp.shared_expert.down_proj", scratch)
+    sg = weights["mlp.shared_expert_gate.weight"]
+    if isinstance(sg, dict):
+        sg = _dequant_affine_q4(sg, scratch)
+    shared_out = torch.sigmoid(F.linear(x, sg)) * shared_out
+    return (expert_output + shared_out).clamp(min=-65504.0, max=65504.0)

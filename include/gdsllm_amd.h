@@ -1,0 +1,155 @@
+/*
+ * gdsllm_amd — C ABI of the MI355X (gfx950) quantized-weight matvec library.
+ *
+ * Every entry point takes raw device pointers, 64-bit sizes and a HIP stream
+ * (passed as `void*`, 0 = the null stream), enqueues its kernels asynchronously
+ * on that stream and returns a status code.  A non-zero status leaves a
+ * human-readable message in gdsllm_last_error() (thread-local).  Argument
+ * validation happens before any HIP call, so a rejected call never touches
+ * the device.
+ *
+ * Weight formats (byte layouts are the ones the reference's converters write
+ * and its kernels read):
+ *   Q4_0   row-major [rows][cols/32] blocks of 18 bytes: fp16 d (LE) + 16 bytes
+ *          qs; element 32b+j = d*((qs[j]&15)-8), element 32b+j+16 = d*((qs[j]>>4)-8)
+ *          (runtime/gguf_dequant.cu:84-107, runtime/fused_gemv.cu:63-71)
+ *   Q8_0   row-major blocks of 34 bytes: fp16 d + int8 qs[32]; element = d*qs[i]
+ *          (runtime/gguf_dequant.cu:40-57)
+ *   affine uint32 words [rows][cols/8], 8 nibbles LSB-first, fp16 scale and bias
+ *          per group of `group_size` consecutive elements of a row;
+ *          element = nib*scale + bias (runtime/affine_q4_dequant.cu:28-59)
+ * Activations and outputs are fp16; every reduction accumulates in fp32.
+ */
+#ifndef GDSLLM_AMD_H
+#define GDSLLM_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum gdsllm_status {
+    GDSLLM_OK = 0,
+    GDSLLM_ERR_INVALID_ARGUMENT = 1, /* shape / size / pointer rejected          */
+    GDSLLM_ERR_UNSUPPORTED = 2,      /* valid request this build cannot serve    */
+    GDSLLM_ERR_HIP = 3,              /* a HIP runtime call or launch failed      */
+    GDSLLM_ERR_IO = 4,               /* file open / read failed                  */
+    GDSLLM_ERR_OUT_OF_MEMORY = 5     /* device allocation failed                 */
+};
+
+/* Message of the last failing call on this host thread ("" if none). */
+const char* gdsllm_last_error(void);
+/* Library version string. */
+const char* gdsllm_version(void);
+
+/* ---------------------------------------------------------------- buffers --
+ * HBM-resident weight buffers.  Replace the cuFile buffer lifecycle
+ * gds_alloc / gds_free / gds_read (runtime/gds_io.cu:93-118, 120-131,
+ * 135-191) behind the same GdsBufferHandle shape (runtime/gds_bindings.cpp:51-76):
+ * sizes round up to 4 KiB like gds_alloc (runtime/gds_io.cu:97-99), reads are
+ * pread() into pinned host staging followed by hipMemcpy into the buffer.  */
+int gdsllm_buffer_alloc(size_t size, int device_id, void** dev_ptr, size_t* rounded_size);
+int gdsllm_buffer_free(void* dev_ptr, int device_id);
+/* Read `size` bytes of `path` starting at `file_offset` into dev_ptr+buf_offset.
+ * `buf_size` is the buffer's size, checked like gds_read (runtime/gds_io.cu:140-142).
+ * *bytes_read receives the count copied (short only at end of file).        */
+int gdsllm_buffer_read_file(void* dev_ptr, size_t buf_size, const char* path,
+                            size_t size, int64_t file_offset, int64_t buf_offset,
+                            int device_id, int64_t* bytes_read);
+
+/* ---------------------------------------------------------------- dequant --
+ * Bit-exact fp16 dequantization: every element is one IEEE round-to-nearest-even
+ * of the exact fp32 value the reference computes.                            */
+
+/* Replaces launch_dequant_q4_0 (runtime/gguf_dequant.h:25-26,
+ * runtime/gguf_dequant.cu:110-118).  dst: fp16[num_blocks*32].            */
+int gdsllm_dequant_q4_0(const void* src, void* dst, int64_t num_blocks, void* stream);
+/* Replaces launch_dequant_q8_0 (runtime/gguf_dequant.h:19-20,
+ * runtime/gguf_dequant.cu:60-68).  dst: fp16[num_blocks*32].              */
+int gdsllm_dequant_q8_0(const void* src, void* dst, int64_t num_blocks, void* stream);
+/* Replaces launch_dequant_affine_q4 (runtime/affine_q4_dequant.h:29-32,
+ * runtime/affine_q4_dequant.cu:61-73).  Elements are grouped by flat index
+ * (group = i / group_size) exactly as the reference does; `in_dim` is checked
+ * to be a multiple of group_size and otherwise unused, as in the reference.  */
+int gdsllm_dequant_affine_q4(const void* weight, const void* scales, const void* biases,
+                             void* dst, int64_t num_elements, int64_t in_dim,
+                             int64_t group_size, void* stream);
+
+/* ------------------------------------------------------------ fused GEMV --
+ * y[b][r] = fp16( sum_k W[r][k] * x[b][k] ), b < batch (1..8), fp32 accumulate.
+ * x row b starts at x + b*ldx elements, y row b at y + b*ldy elements.
+ * out_dim == 0 or in_dim == 0 is a no-op, as in the reference launchers.      */
+
+/* Replaces launch_fused_q4_0_gemv (runtime/fused_gemv.h:23-25,
+ * runtime/fused_gemv.cu:107-135); batch > 1 is an extension.                 */
+int gdsllm_fused_q4_0_gemv(const void* weight, const void* x, void* y,
+                           int64_t out_dim, int64_t in_dim, int64_t batch,
+                           int64_t ldx, int64_t ldy, void* stream);
+/* Replaces launch_fused_q8_0_gemv (runtime/fused_gemv.h:29-31,
+ * runtime/fused_gemv.cu:207-231).                                            */
+int gdsllm_fused_q8_0_gemv(const void* weight, const void* x, void* y,
+                           int64_t out_dim, int64_t in_dim, int64_t batch,
+                           int64_t ldx, int64_t ldy, void* stream);
+/* Replaces launch_fused_affine_q4_gemv (runtime/affine_q4_dequant.h:41-44,
+ * runtime/affine_q4_dequant.cu:160-187).                                     */
+int gdsllm_fused_affine_q4_gemv(const void* weight, const void* scales, const void* biases,
+                                const void* x, void* y, int64_t out_dim, int64_t in_dim,
+                                int64_t group_size, int64_t batch, int64_t ldx,
+                                int64_t ldy, void* stream);
+
+/* ------------------------------------------------------ MoE expert gather --
+ * One projection of a stacked affine-Q4 expert tensor as the Qwen-MoE layer
+ * file stores it: words [E][out_dim][in_dim/8], then scales and biases
+ * [E][out_dim][in_dim/group_size], each region at its own offset
+ * (tools/convert_qwen_moe.py:216-233).  Expert e's slices start at
+ * weight + e*weight_stride, scales + e*scale_stride, biases + e*bias_stride
+ * (bytes; runtime/torch_bridge.py:326-337).                                   */
+typedef struct gdsllm_affine_experts {
+    const void* weight;
+    const void* scales;
+    const void* biases;
+    int64_t weight_stride;
+    int64_t scale_stride;
+    int64_t bias_stride;
+    int64_t num_experts;
+    int64_t out_dim;
+    int64_t in_dim;
+    int64_t group_size;
+} gdsllm_affine_experts;
+
+/* Bytes of device workspace gdsllm_moe_gather_affine_q4 needs. */
+size_t gdsllm_moe_gather_workspace_size(int64_t top_k, int64_t ffn_dim);
+
+/* Top-k expert-gather MLP for one token (decode):
+ *   y = fp16( sum_k w[k] * down[idx[k]] . h_k ),
+ *   h_k = fp16( fp16(silu(fp16(gate[idx[k]] . x))) * fp16(up[idx[k]] . x) )
+ * i.e. the decode branch of moe_mlp_selective (runtime/qwen_moe.py:455-474)
+ * with the routing weights combined in fp32.  idx: int32[top_k] on device,
+ * routing_weights: fp16[top_k] on device, x: fp16[hidden], y: fp16[hidden].
+ * gate/up: out_dim = ffn_dim, in_dim = hidden; down: out_dim = hidden,
+ * in_dim = ffn_dim.  Expert indices outside [0, num_experts) contribute
+ * nothing.  No counterpart kernel exists in the reference, which loops over
+ * fused_affine_q4_gemv launches in Python.                                   */
+int gdsllm_moe_gather_affine_q4(const gdsllm_affine_experts* gate,
+                                const gdsllm_affine_experts* up,
+                                const gdsllm_affine_experts* down,
+                                const void* x, const int32_t* idx,
+                                const void* routing_weights, int64_t top_k,
+                                void* y, void* workspace, size_t workspace_bytes,
+                                void* stream);
+
+/* ---------------------------------------------------- prefill dequant-GEMM --
+ * Y[t][r] = fp16( sum_k X[t][k] * W[r][k] ), t < tokens, on MFMA.  Replaces
+ * the prefill branch dequant -> F.linear (runtime/llama.py:160-166).
+ * X row t at x + t*ldx, Y row t at y + t*ldy (elements).                     */
+int gdsllm_dequant_gemm_q4_0(const void* weight, const void* x, void* y,
+                             int64_t out_dim, int64_t in_dim, int64_t tokens,
+                             int64_t ldx, int64_t ldy, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GDSLLM_AMD_H */

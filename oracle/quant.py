@@ -1,0 +1,147 @@
+"""Numpy restatement of the reference's quantized-matvec arithmetic.
+
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py): the checker for the HIP
+kernels, never called by the product.
+
+Every function cites the reference code it restates.  Dequantization is
+bit-exact (same fp32 operations, same single round-to-nearest-even to fp16 as
+the CUDA kernels); matrix-vector products are computed in float64 over those
+exact fp16 weights, and kernels are compared against them under the stated
+tolerance (GEMV_REL_L2 / GEMV_MAX_NORM).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+Q4_0_BLOCK_BYTES = 18  # runtime/gguf_dequant.cu:73-74
+Q8_0_BLOCK_BYTES = 34  # runtime/gguf_dequant.cu:29-30
+QK = 32                # weights per GGUF block
+
+# GEMV / GEMM acceptance: relative L2 over the whole output, and the largest
+# per-row error normalized by that row's ||w_r * x||_2.
+GEMV_REL_L2 = 2e-3
+GEMV_MAX_NORM = 1e-2
+
+
+def _blocks(raw, block_bytes: int) -> np.ndarray:
+    a = np.frombuffer(raw, dtype=np.uint8) if isinstance(raw, (bytes, bytearray)) else np.asarray(raw, dtype=np.uint8)
+    if a.size % block_bytes:
+        raise ValueError(f"byte count {a.size} is not a multiple of {block_bytes}")
+    return a.reshape(-1, block_bytes)
+
+
+def dequant_q4_0(raw) -> np.ndarray:
+    """kernel_dequant_q4_0 (runtime/gguf_dequant.cu:76-108).
+
+    Block = fp16 d (little endian) + 16 bytes qs.  out[32b+j] = fp16(f32(d) *
+    f32((qs[j] & 15) - 8)), out[32b+j+16] = fp16(f32(d) * f32((qs[j] >> 4) - 8))
+    (the code's j / j+16 order, :105-106 — not the even/odd wording of its
+    header comment, :18-19).  The fp32 product is exact, so one RNE rounding.
+    """
+    b = _blocks(raw, Q4_0_BLOCK_BYTES)
+    d = np.ascontiguousarray(b[:, :2]).view(np.float16)[:, 0].astype(np.float32)[:, None]
+    qs = b[:, 2:]
+    lo = (qs & 15).astype(np.float32) - 8.0
+    hi = (qs >> 4).astype(np.float32) - 8.0
+    out = np.empty((b.shape[0], QK), dtype=np.float16)
+    out[:, :16] = (d * lo).astype(np.float16)
+    out[:, 16:] = (d * hi).astype(np.float16)
+    return out.reshape(-1)
+
+
+def dequant_q8_0(raw) -> np.ndarray:
+    """kernel_dequant_q8_0 (runtime/gguf_dequant.cu:32-58): out[32b+i] = fp16(f32(d) * f32(qs[i]))."""
+    b = _blocks(raw, Q8_0_BLOCK_BYTES)
+    d = np.ascontiguousarray(b[:, :2]).view(np.float16)[:, 0].astype(np.float32)[:, None]
+    qs = np.ascontiguousarray(b[:, 2:]).view(np.int8).astype(np.float32)
+    return (d * qs).astype(np.float16).reshape(-1)
+
+
+def unpack_affine_nibbles(words: np.ndarray) -> np.ndarray:
+    """uint32 words -> nibbles, element 8w+n = (word >> 4n) & 15 (LSB first;
+    runtime/affine_q4_dequant.cu:50-58, tools/convert_qwen_moe.py:170-179)."""
+    w = np.asarray(words, dtype=np.uint32).reshape(-1)
+    shifts = (4 * np.arange(8, dtype=np.uint32))[None, :]
+    return ((w[:, None] >> shifts) & np.uint32(15)).astype(np.uint8).reshape(-1)
+
+
+def dequant_affine_q4(words, scales, biases, num_elements: int, group_size: int) -> np.ndarray:
+    """kernel_dequant_affine_q4 (runtime/affine_q4_dequant.cu:28-59).
+
+    Group G = flat_index // group_size; out = fp16(f32(nib) * f32(s[G]) + f32(b[G])):
+    the product is exact, the add rounds once in fp32, the cast once to fp16
+    (two roundings, as the kernel does — restated in fp32, not fp64).  The two
+    roundings differ from one when nib*s sits exactly on an fp16 tie and a bias
+    below half an fp32 ulp of it nudges the exact sum off the tie.
+    """
+    nib = unpack_affine_nibbles(words)[:num_elements].astype(np.float32)
+    g = np.arange(num_elements) // group_size
+    s = np.asarray(scales, dtype=np.float16).reshape(-1)[g].astype(np.float32)
+    b = np.asarray(biases, dtype=np.float16).reshape(-1)[g].astype(np.float32)
+    v = (nib * s).astype(np.float32) + b
+    return v.astype(np.float32).astype(np.float16)
+
+
+def gemv(w_fp16: np.ndarray, x_fp16: np.ndarray) -> np.ndarray:
+    """y[b, r] = sum_k W[r, k] * x[b, k] in float64 over the exact fp16 values.
+
+    The fused kernels (runtime/fused_gemv.cu:27-105, 142-205;
+    runtime/affine_q4_dequant.cu:79-158) accumulate the same products in fp32
+    and round once to fp16; this is the exact value they approximate.
+    """
+    w = np.asarray(w_fp16, dtype=np.float16).astype(np.float64)
+    x = np.atleast_2d(np.asarray(x_fp16, dtype=np.float16)).astype(np.float64)
+    return x @ w.T
+
+
+def row_norms(w_fp16: np.ndarray, x_fp16: np.ndarray) -> np.ndarray:
+    """||w_r * x_b||_2 for every (b, r): the scale of the fp32 accumulation error of row r."""
+    w = np.asarray(w_fp16, dtype=np.float16).astype(np.float64)
+    x = np.atleast_2d(np.asarray(x_fp16, dtype=np.float16)).astype(np.float64)
+    return np.sqrt((x * x) @ (w * w).T)
+
+
+def gemv_errors(y_test, y_ref: np.ndarray, norms: np.ndarray) -> tuple[float, float]:
+    """(relative L2 error, max |y - y_ref| / ||w_r * x||) of a kernel result."""
+    y = np.asarray(y_test, dtype=np.float64).reshape(y_ref.shape)
+    diff = y - y_ref
+    rel = float(np.linalg.norm(diff) / max(np.linalg.norm(y_ref), 1e-30))
+    mx = float(np.max(np.abs(diff) / np.maximum(norms, 1e-30))) if diff.size else 0.0
+    return rel, mx
+
+
+def silu_fp16(g_fp16: np.ndarray) -> np.ndarray:
+    """torch F.silu on an fp16 tensor: x / (1 + exp(-x)) in fp32, rounded to fp16."""
+    g = np.asarray(g_fp16, dtype=np.float16).astype(np.float32)
+    with np.errstate(over="ignore"):
+        return (g / (np.float32(1.0) + np.exp(-g))).astype(np.float16)
+
+
+def moe_gather(x, gate, up, down, idx, routing_weights):
+    """Decode branch of moe_mlp_selective (runtime/qwen_moe.py:455-474).
+
+    gate/up/down: callables e -> fp16 dequantized [out, in] matrix of expert e.
+    For each k: g = fp16(gate_e . x), u = fp16(up_e . x) (the fused GEMV outputs),
+    h = fp16(fp16(silu(g)) * u), then sum_k w_k * (down_e . h).  Returns
+    (float64 exact weighted sum given the fp16 intermediates, the intermediates h).
+    Indices outside the expert range contribute nothing.
+    """
+    x = np.asarray(x, dtype=np.float16).reshape(-1)
+    acc = None
+    hs = []
+    for k, e in enumerate(np.asarray(idx).reshape(-1)):
+        e = int(e)
+        wg, wu, wd = gate(e), up(e), down(e)
+        if wg is None:
+            hs.append(None)
+            continue
+        g = gemv(wg, x)[0].astype(np.float16)
+        u = gemv(wu, x)[0].astype(np.float16)
+        h = (silu_fp16(g).astype(np.float32) * u.astype(np.float32)).astype(np.float16)
+        hs.append(h)
+        y = gemv(wd, h)[0] * float(np.float16(np.asarray(routing_weights).reshape(-1)[k]))
+        acc = y if acc is None else acc + y
+    if acc is None:
+        acc = np.zeros(0)
+    return acc, hs

@@ -1,0 +1,131 @@
+"""Shared helpers for the parity tests: seeded inputs, calls through the C ABI,
+oracle comparisons."""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+
+from gdsllm_amd import AffineExperts, capi, check
+from gdsllm_amd import synthetic as syn
+from oracle import quant as oq
+
+
+def gen(seed: int) -> torch.Generator:
+    g = torch.Generator()
+    g.manual_seed(seed)
+    return g
+
+
+def stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def ptr(t: torch.Tensor) -> int:
+    return t.data_ptr()
+
+
+def to_np(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().numpy()
+
+
+def on_gpu(t: torch.Tensor, dev, pad_front: int = 0) -> torch.Tensor:
+    """Copy to the GPU; with pad_front > 0 the data starts pad_front bytes into
+    a larger allocation (to exercise misaligned entry paths).  Returns a view
+    whose data_ptr() is the shifted start."""
+    if pad_front == 0:
+        return t.contiguous().to(dev)
+    raw = t.contiguous().view(torch.uint8).reshape(-1)
+    buf = torch.zeros(raw.numel() + pad_front + 64, dtype=torch.uint8, device=dev)
+    buf[pad_front:pad_front + raw.numel()] = raw.to(dev)
+    return buf[pad_front:pad_front + raw.numel()]
+
+
+def assert_gemv_close(y_test: np.ndarray, w_fp16: np.ndarray, x_fp16: np.ndarray, what: str = "") -> tuple:
+    y_ref = oq.gemv(w_fp16, x_fp16)
+    norms = oq.row_norms(w_fp16, x_fp16)
+    rel, mx = oq.gemv_errors(y_test.astype(np.float64), y_ref, norms)
+    assert np.all(np.isfinite(y_test)), f"{what}: non-finite output"
+    assert rel <= oq.GEMV_REL_L2, f"{what}: rel L2 {rel:.3e} > {oq.GEMV_REL_L2}"
+    assert mx <= oq.GEMV_MAX_NORM, f"{what}: max normalized error {mx:.3e} > {oq.GEMV_MAX_NORM}"
+    return rel, mx
+
+
+def gguf_gemv(fmt: str, w_dev: torch.Tensor, x_dev: torch.Tensor, M: int, K: int) -> torch.Tensor:
+    """y [B, M] via gdsllm_fused_{fmt}_gemv; x_dev is [B, K] contiguous."""
+    B = x_dev.shape[0]
+    y = torch.empty(B, M, dtype=torch.float16, device=x_dev.device)
+    fn = capi().gdsllm_fused_q4_0_gemv if fmt == "q4_0" else capi().gdsllm_fused_q8_0_gemv
+    check(fn(ptr(w_dev), ptr(x_dev), ptr(y), M, K, B, K, M, stream()))
+    torch.cuda.synchronize()
+    return y
+
+
+def affine_gemv(words, scales, biases, x_dev, M, K, g) -> torch.Tensor:
+    B = x_dev.shape[0]
+    y = torch.empty(B, M, dtype=torch.float16, device=x_dev.device)
+    check(capi().gdsllm_fused_affine_q4_gemv(ptr(words), ptr(scales), ptr(biases), ptr(x_dev), ptr(y), M, K, g, B, K, M,
+                                             stream()))
+    torch.cuda.synchronize()
+    return y
+
+
+def experts_struct(words: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, group_size: int) -> AffineExperts:
+    E, N, kw = words.shape
+    K = kw * 8
+    return AffineExperts(ptr(words), ptr(scales), ptr(biases), N * kw * 4, N * (K // group_size) * 2,
+                         N * (K // group_size) * 2, E, N, K, group_size)
+
+
+def moe_gather(gate, up, down, x_dev, idx_dev, w_dev, group_size, return_workspace: bool = False):
+    """y [hidden] via gdsllm_moe_gather_affine_q4; optionally also the fp16
+    workspace [top_k][2][ffn] holding the phase-1 gate/up outputs."""
+    g, u, d = (experts_struct(*p, group_size) for p in (gate, up, down))
+    top_k = idx_dev.numel()
+    ws_bytes = capi().gdsllm_moe_gather_workspace_size(top_k, g.out_dim)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x_dev.device)
+    y = torch.empty(d.out_dim, dtype=torch.float16, device=x_dev.device)
+    check(capi().gdsllm_moe_gather_affine_q4(ctypes.byref(g), ctypes.byref(u), ctypes.byref(d), ptr(x_dev), ptr(idx_dev),
+                                             ptr(w_dev), top_k, ptr(y), ptr(ws), ws_bytes, stream()))
+    torch.cuda.synchronize()
+    if return_workspace:
+        return y, ws[: top_k * 2 * g.out_dim * 2].view(torch.float16).view(top_k, 2, g.out_dim)
+    return y
+
+
+def affine_dequant_np(words: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, group_size: int) -> np.ndarray:
+    n = words.numel() * 8
+    return oq.dequant_affine_q4(to_np(words).view(np.uint32), to_np(scales), to_np(biases), n, group_size)
+
+
+def double_rounding_cases(n: int, seed: int):
+    """(nib, scale, bias) triples for which fp16(nib*s+b) rounded once differs
+    from rounding to fp32 first (nib*s on an fp16 tie, |b| below half an fp32
+    ulp of it).  Found by vectorized sampling; every returned case is checked
+    with exact float64 arithmetic (the sums below are exact in float64)."""
+    rng = np.random.default_rng(seed)
+    found = []
+    while sum(len(f[0]) for f in found) < n:
+        m = 1 << 20
+        s = rng.integers(0x3C00, 0x7000, m, dtype=np.uint16).view(np.float16)  # 1 .. 8192
+        nib = rng.integers(1, 16, m)
+        b = (rng.integers(0x0400, 0x1C00, m, dtype=np.uint16) | (rng.integers(0, 2, m, dtype=np.uint16) << 15))
+        b = b.view(np.float16)  # |b| in [2^-14, 2^-6)
+        exact = nib * s.astype(np.float64) + b.astype(np.float64)
+        with np.errstate(over="ignore"):
+            once = exact.astype(np.float16)
+            twice = exact.astype(np.float32).astype(np.float16)
+        sel = np.isfinite(once) & (once.view(np.uint16) != twice.view(np.uint16))
+        found.append((nib[sel], s[sel], b[sel]))
+    nib = np.concatenate([f[0] for f in found])[:n]
+    s = np.concatenate([f[1] for f in found])[:n]
+    b = np.concatenate([f[2] for f in found])[:n]
+    return nib.astype(np.uint32), s, b
+
+
+__all__ = [
+    "gen", "stream", "ptr", "to_np", "on_gpu", "assert_gemv_close", "gguf_gemv", "affine_gemv", "moe_gather",
+    "experts_struct", "affine_dequant_np", "double_rounding_cases", "syn", "oq", "capi", "check",
+]

@@ -1,0 +1,130 @@
+"""Parity of the fused GEMV kernels (Q4_0, Q8_0, affine-Q4) with the oracle,
+through the C ABI.  Tolerance: relative L2 <= 2e-3 and per-row error /
+||w_r * x||_2 <= 1e-2 (oracle.quant.GEMV_REL_L2 / GEMV_MAX_NORM)."""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import (affine_dequant_np, affine_gemv, assert_gemv_close, capi, check, gen, gguf_gemv, on_gpu, oq, ptr,
+                     stream, syn, to_np)
+
+pytestmark = pytest.mark.gpu
+
+GGUF_SHAPES = [
+    (1, 256), (5, 256), (64, 512), (33, 4096), (4096, 4096), (300, 11008), (130, 8192), (17, 28672),
+    # in_dim % 256 != 0: generic path
+    (10, 32), (7, 96), (9, 4128),
+]
+
+
+def _gguf_case(fmt, M, K, B, seed):
+    make = syn.q4_0_weights if fmt == "q4_0" else syn.q8_0_weights
+    w = make(M, K, gen(seed))
+    x = syn.activations(B, K, gen(seed + 1))
+    deq = (oq.dequant_q4_0 if fmt == "q4_0" else oq.dequant_q8_0)(to_np(w)).reshape(M, K)
+    return w, x, deq
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("M,K", GGUF_SHAPES, ids=[f"{m}x{k}" for m, k in GGUF_SHAPES])
+def test_gguf_gemv_b1(gpu, fmt, M, K):
+    w, x, deq = _gguf_case(fmt, M, K, 1, 1000 + M + K)
+    y = gguf_gemv(fmt, w.to(gpu), x.to(gpu), M, K)
+    assert_gemv_close(to_np(y), deq, to_np(x), f"{fmt} {M}x{K}")
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("B", [2, 3, 4, 8])
+@pytest.mark.parametrize("M,K", [(70, 4096), (33, 11008), (20, 96)])
+def test_gguf_gemv_batched(gpu, fmt, B, M, K):
+    w, x, deq = _gguf_case(fmt, M, K, B, 2000 + B + M)
+    y = gguf_gemv(fmt, w.to(gpu), x.to(gpu), M, K)
+    assert_gemv_close(to_np(y), deq, to_np(x), f"{fmt} B={B} {M}x{K}")
+
+
+def test_q4_0_gemv_cfg0_full(gpu):
+    """The headline shape: LLaMA-7B gate_proj 11008x4096 at batch 1."""
+    w, x, deq = _gguf_case("q4_0", 11008, 4096, 1, 1000)
+    y = gguf_gemv("q4_0", w.to(gpu), x.to(gpu), 11008, 4096)
+    rel, mx = assert_gemv_close(to_np(y), deq, to_np(x), "cfg0")
+    print(f"cfg0 rel_l2={rel:.2e} max_norm={mx:.2e}")
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+def test_gguf_gemv_misaligned_inputs(gpu, fmt):
+    """Weights off the 16-byte grid take the generic kernel; x off the 8-byte grid
+    takes the element-wise staging; both must agree with the oracle."""
+    M, K = 40, 512
+    w, x, deq = _gguf_case(fmt, M, K, 2, 77)
+    wd = on_gpu(w, gpu, pad_front=2)
+    xbuf = torch.zeros(2 * K + 8, dtype=torch.float16, device=gpu)
+    xd = xbuf[1:1 + 2 * K]
+    xd.copy_(x.reshape(-1).to(gpu))
+    y = torch.empty(2, M, dtype=torch.float16, device=gpu)
+    fn = capi().gdsllm_fused_q4_0_gemv if fmt == "q4_0" else capi().gdsllm_fused_q8_0_gemv
+    check(fn(ptr(wd), ptr(xd), ptr(y), M, K, 2, K, M, stream()))
+    torch.cuda.synchronize()
+    assert_gemv_close(to_np(y), deq, to_np(x), f"{fmt} misaligned")
+
+
+def test_gguf_gemv_strided_batch(gpu):
+    """ldx / ldy larger than the row: rows of x and y taken from wider buffers."""
+    M, K, B = 50, 256, 3
+    w, x, deq = _gguf_case("q4_0", M, K, B, 91)
+    xw = torch.zeros(B, K + 64, dtype=torch.float16)
+    xw[:, :K] = x
+    xd = xw.to(gpu)
+    y = torch.full((B, M + 10), 7.0, dtype=torch.float16, device=gpu)
+    check(capi().gdsllm_fused_q4_0_gemv(ptr(w.to(gpu)), ptr(xd), ptr(y), M, K, B, K + 64, M + 10, stream()))
+    torch.cuda.synchronize()
+    yn = to_np(y)
+    assert np.all(yn[:, M:] == 7.0), "wrote outside the output rows"
+    assert_gemv_close(yn[:, :M], deq, to_np(x), "strided")
+
+
+def test_gguf_gemv_closed_forms(gpu):
+    """All nibbles 8 -> y = 0 up to the fp32 cancellation of the nibble-offset
+    correction (1032*sum(x) per block, |err| ~ 2^-24 * 1032 * |sum x| * d, far
+    below one fp16 ulp of a real output); one-hot x -> y = column k of the fp16
+    weights exactly (every term is an exact small integer times d)."""
+    M, K = 64, 1024
+    w = syn.q4_0_weights(M, K, gen(5)).view(-1, 18).clone()
+    w[:, 2:] = 0x88
+    x = syn.activations(1, K, gen(6))
+    y = gguf_gemv("q4_0", w.reshape(M, -1).to(gpu), x.to(gpu), M, K)
+    bound = 1e-5 * float(np.abs(to_np(x).astype(np.float64)).sum())
+    assert np.max(np.abs(to_np(y).astype(np.float64))) <= bound
+    w2 = syn.q4_0_weights(M, K, gen(8))
+    deq = oq.dequant_q4_0(to_np(w2)).reshape(M, K)
+    for k in (0, 15, 16, 31, 517, K - 1):
+        e = torch.zeros(1, K, dtype=torch.float16)
+        e[0, k] = 1.0
+        y = gguf_gemv("q4_0", w2.to(gpu), e.to(gpu), M, K)
+        assert np.array_equal(to_np(y)[0], deq[:, k]), f"column {k}"
+
+
+AFFINE_SHAPES = [(1024, 4096, 64), (4096, 1024, 64), (64, 4096, 128), (33, 256, 32), (7, 2048, 64), (5, 96, 32),
+                 # generic path: in_dim % 32 != 0 or group_size % 32 != 0
+                 (9, 104, 8), (6, 128, 16)]
+
+
+@pytest.mark.parametrize("M,K,g", AFFINE_SHAPES, ids=[f"{m}x{k}g{g}" for m, k, g in AFFINE_SHAPES])
+@pytest.mark.parametrize("B", [1, 3, 8])
+def test_affine_gemv(gpu, M, K, g, B):
+    w, s, b = syn.affine_q4_weights([M, K], g, gen(3000 + M + K + g))
+    x = syn.activations(B, K, gen(3001 + B))
+    deq = affine_dequant_np(w, s, b, g).reshape(M, K)
+    y = affine_gemv(w.to(gpu), s.to(gpu), b.to(gpu), x.to(gpu), M, K, g)
+    assert_gemv_close(to_np(y), deq, to_np(x), f"affine {M}x{K} g{g} B{B}")
+
+
+def test_capi_rejects_bad_shapes_before_launch(gpu):
+    lib = capi()
+    y = torch.empty(4, dtype=torch.float16, device=gpu)
+    assert lib.gdsllm_fused_q4_0_gemv(ptr(y), ptr(y), ptr(y), 4, 48, 1, 48, 4, stream()) == 1
+    assert b"multiple of 32" in lib.gdsllm_last_error()
+    assert lib.gdsllm_fused_q8_0_gemv(ptr(y), ptr(y), ptr(y), 4, 64, 9, 64, 4, stream()) == 1
+    assert lib.gdsllm_fused_affine_q4_gemv(ptr(y), ptr(y), ptr(y), ptr(y), ptr(y), 4, 96, 64, 1, 96, 4, stream()) == 1
+    # zero-sized problems are no-ops, as in the reference launchers
+    assert lib.gdsllm_fused_q4_0_gemv(None, None, None, 0, 64, 1, 64, 0, stream()) == 0

@@ -1,0 +1,125 @@
+"""Parity of the top-k expert-gather MLP and the MFMA prefill dequant-GEMM."""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import (affine_dequant_np, assert_gemv_close, capi, check, gen, moe_gather, oq, ptr, stream, syn, to_np)
+
+pytestmark = pytest.mark.gpu
+
+
+def _moe_pool(E, H, F, g, seed, device="cpu"):
+    gg = gen(seed) if device == "cpu" else torch.Generator(device=device).manual_seed(seed)
+    gate = syn.affine_q4_weights([E, F, H], g, gg)
+    up = syn.affine_q4_weights([E, F, H], g, gg)
+    down = syn.affine_q4_weights([E, H, F], g, gg)
+    return gate, up, down
+
+
+def _expert_fn(pool, g, E):
+    def f(e):
+        if e < 0 or e >= E:
+            return None
+        w, s, b = (t[e].cpu() for t in pool)
+        N = w.shape[0]
+        return affine_dequant_np(w, s, b, g).reshape(N, -1)
+    return f
+
+
+def _check_moe(y, ws, gate, up, down, x, idx, wts, g, E):
+    """Three checks.  (1) phase 1: the fp16 gate/up rows in the workspace match
+    the oracle GEMVs under the GEMV tolerance.  (2) phase 2: y matches the
+    oracle's weighted down-projection of h = fp16(fp16(silu(g)) * u) built from
+    the kernel's own fp16 g/u, under the GEMV tolerance.  (3) end to end: y
+    matches the all-oracle result in relative L2 (one-ulp fp16 differences in
+    g/u move h, so the per-row bound is not applied end to end)."""
+    xn = to_np(x).reshape(-1)
+    gf, uf, dn = _expert_fn(gate, g, E), _expert_fn(up, g, E), _expert_fn(down, g, E)
+    wsn = to_np(ws)
+    for k, e in enumerate(idx):
+        e = int(e)
+        if gf(e) is None:
+            assert np.all(wsn[k] == 0), "rows of an out-of-range expert must be zero"
+            continue
+        assert_gemv_close(wsn[k, 0][None, :], gf(e), xn[None, :], f"gate k={k}")
+        assert_gemv_close(wsn[k, 1][None, :], uf(e), xn[None, :], f"up k={k}")
+    ref2 = None
+    norm2 = 0.0
+    for k, e in enumerate(idx):
+        e = int(e)
+        if gf(e) is None:
+            continue
+        h = (oq.silu_fp16(wsn[k, 0]).astype(np.float32) * wsn[k, 1].astype(np.float32)).astype(np.float16)
+        wk = float(np.float16(to_np(wts)[k]))
+        part = oq.gemv(dn(e), h)[0] * wk
+        ref2 = part if ref2 is None else ref2 + part
+        norm2 = norm2 + (wk ** 2) * oq.row_norms(dn(e), h)[0] ** 2
+    rel2, mx2 = oq.gemv_errors(to_np(y).astype(np.float64), ref2, np.sqrt(norm2))
+    assert rel2 <= oq.GEMV_REL_L2, f"moe phase-2 rel L2 {rel2:.3e}"
+    assert mx2 <= oq.GEMV_MAX_NORM, f"moe phase-2 max normalized {mx2:.3e}"
+    ref, _ = oq.moe_gather(xn, gf, uf, dn, idx, to_np(wts))
+    rel = float(np.linalg.norm(to_np(y).astype(np.float64) - ref) / np.linalg.norm(ref))
+    assert rel <= oq.GEMV_REL_L2, f"moe end-to-end rel L2 {rel:.3e}"
+    print(f"moe phase2 rel={rel2:.2e} max={mx2:.2e} end-to-end rel={rel:.2e}")
+    return rel2, mx2
+
+
+@pytest.mark.parametrize("E,H,F,g,top_k", [(16, 4096, 1024, 64, 10), (8, 512, 256, 32, 3), (12, 1024, 512, 128, 1)])
+def test_moe_gather(gpu, E, H, F, g, top_k):
+    gate, up, down = _moe_pool(E, H, F, g, 4000 + E + top_k)
+    x = syn.activations(1, H, gen(4100 + E))
+    idx = torch.randperm(E, generator=gen(4200 + E))[:top_k].to(torch.int32)
+    wts = torch.softmax(torch.randn(top_k, generator=gen(4300)), 0).to(torch.float16)
+    y, ws = moe_gather(tuple(t.to(gpu) for t in gate), tuple(t.to(gpu) for t in up),
+                       tuple(t.to(gpu) for t in down), x.to(gpu), idx.to(gpu), wts.to(gpu), g, return_workspace=True)
+    _check_moe(y, ws, gate, up, down, x, to_np(idx), wts, g, E)
+
+
+def test_moe_gather_skips_out_of_range_experts(gpu):
+    E, H, F, g = 6, 512, 256, 64
+    gate, up, down = _moe_pool(E, H, F, g, 77)
+    x = syn.activations(1, H, gen(78))
+    idx = torch.tensor([2, -1, 5, 6, 0], dtype=torch.int32)
+    wts = torch.tensor([0.3, 0.2, 0.2, 0.2, 0.1], dtype=torch.float16)
+    y, ws = moe_gather(tuple(t.to(gpu) for t in gate), tuple(t.to(gpu) for t in up),
+                       tuple(t.to(gpu) for t in down), x.to(gpu), idx.to(gpu), wts.to(gpu), g, return_workspace=True)
+    _check_moe(y, ws, gate, up, down, x, to_np(idx), wts, g, E)
+
+
+def test_moe_gather_cfg2_full_pool(gpu):
+    """512-expert pool (3.6 GB) generated on the device; the oracle sees only the 10 picked experts."""
+    E, H, F, g, top_k = 512, 4096, 1024, 64, 10
+    gate, up, down = _moe_pool(E, H, F, g, 1002, device=gpu)
+    x = syn.activations(1, H, gen(1003))
+    idx = torch.randperm(E, generator=gen(1004))[:top_k].to(torch.int32)
+    wts = torch.softmax(torch.randn(top_k, generator=gen(1005)), 0).to(torch.float16)
+    y, ws = moe_gather(gate, up, down, x.to(gpu), idx.to(gpu), wts.to(gpu), g, return_workspace=True)
+    sel = sorted(set(int(e) for e in idx))
+    remap = {e: i for i, e in enumerate(sel)}
+    small = [tuple(t[sel].cpu() for t in pool) for pool in (gate, up, down)]
+    _check_moe(y, ws, *small, x, np.array([remap[int(e)] for e in idx]), wts, g, len(sel))
+    del gate, up, down
+    torch.cuda.empty_cache()
+
+
+GEMM_CASES = [(1, 128, 64), (7, 300, 256), (64, 128, 4096), (100, 260, 1024), (512, 4096, 4096), (33, 11008, 4096),
+              (512, 512, 11008)]
+
+
+@pytest.mark.parametrize("T,M,K", GEMM_CASES, ids=[f"T{t}_{m}x{k}" for t, m, k in GEMM_CASES])
+def test_dequant_gemm_q4_0(gpu, T, M, K):
+    w = syn.q4_0_weights(M, K, gen(5000 + M))
+    x = syn.activations(T, K, gen(5001 + T))
+    deq = oq.dequant_q4_0(to_np(w)).reshape(M, K)
+    xd = x.to(gpu)
+    y = torch.empty(T, M, dtype=torch.float16, device=gpu)
+    check(capi().gdsllm_dequant_gemm_q4_0(ptr(w.to(gpu)), ptr(xd), ptr(y), M, K, T, K, M, stream()))
+    torch.cuda.synchronize()
+    assert_gemv_close(to_np(y), deq, to_np(x), f"gemm T{T} {M}x{K}")
+
+
+def test_dequant_gemm_rejects_unsupported(gpu):
+    y = torch.empty(8, dtype=torch.float16, device=gpu)
+    assert capi().gdsllm_dequant_gemm_q4_0(ptr(y), ptr(y), ptr(y), 4, 96, 2, 96, 4, stream()) == 2
+    assert b"multiple of 64" in capi().gdsllm_last_error()

@@ -1,0 +1,310 @@
+"""Pins the CPU oracle (oracle/quant.py) before it is trusted as the checker.
+
+The reference ships no tests or golden vectors for this path, so the oracle is
+pinned by: known-answer blocks worked out by hand from the CUDA source,
+an independent exact-arithmetic restatement (Python Fractions + a hand-written
+round-to-nearest-even, no numpy casts) over random blocks including special
+values, brute-force loops for the products, closed forms, and planted
+mistakes that the acceptance tolerance must reject.
+"""
+
+from fractions import Fraction
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import quant as oq
+from gdsllm_amd import synthetic as syn
+
+
+# ---------------------------------------------------------------- exact rounding
+
+
+def round_rne(x: Fraction, mant_bits: int, emin: int, emax: int) -> Fraction:
+    """Round an exact rational to the nearest IEEE binary value with `mant_bits`
+    significand bits (incl. the hidden bit), min normal exponent emin, max emax;
+    ties to even; overflow -> +-inf (returned as float)."""
+    if x == 0:
+        return x
+    sign = -1 if x < 0 else 1
+    a = abs(x)
+    e = math.floor(math.log2(a.numerator) - math.log2(a.denominator))
+    while Fraction(2) ** e > a:
+        e -= 1
+    while Fraction(2) ** (e + 1) <= a:
+        e += 1
+    e = max(e, emin)  # subnormals share the minimum exponent's ulp
+    ulp = Fraction(2) ** (e - mant_bits + 1)
+    q, r = divmod(a, ulp)
+    q = int(q)
+    if r * 2 > ulp or (r * 2 == ulp and q % 2 == 1):
+        q += 1
+    v = q * ulp
+    max_finite = (2 - Fraction(2) ** (1 - mant_bits)) * Fraction(2) ** emax
+    if v > max_finite:
+        return sign * math.inf
+    return sign * v
+
+
+def to_f16_bits(v) -> int:
+    """Bits of an exactly representable fp16 value (Fraction / float / inf)."""
+    return int(np.array([float(v)], dtype=np.float64).astype(np.float16).view(np.uint16)[0])
+
+
+def f16(bits: int) -> Fraction:
+    return Fraction(float(np.array([bits], dtype=np.uint16).view(np.float16)[0]))
+
+
+def exact_q4_0(raw: np.ndarray) -> list:
+    """Independent restatement of runtime/gguf_dequant.cu:84-107 with exact math."""
+    out = []
+    for blk in raw.reshape(-1, 18):
+        d = f16(int(blk[0]) | (int(blk[1]) << 8))
+        vals = [None] * 32
+        for j in range(16):
+            vals[j] = d * ((int(blk[2 + j]) & 15) - 8)
+            vals[j + 16] = d * ((int(blk[2 + j]) >> 4) - 8)
+        for j, v in enumerate(vals):
+            # fp32 product is exact (11 x 4 bits), then one RNE to fp16
+            r = round_rne(v, 11, -14, 15)
+            neg_zero = v == 0 and (d < 0 or (d == 0 and str(float(d)).startswith("-"))) != (
+                (((int(blk[2 + j % 16]) >> (4 * (j // 16))) & 15) - 8) < 0)
+            out.append(0x8000 if (r == 0 and neg_zero) else to_f16_bits(r))
+    return out
+
+
+def _sign_bit(bits: int) -> bool:
+    return bool(bits & 0x8000)
+
+
+# ------------------------------------------------------------------ known answers
+
+
+def test_q4_0_known_answer_block():
+    """d = 1, qs[j] = (15-j) << 4 | j: element j = j-8 (low nibble), element
+    j+16 = 7-j (high nibble) — the j / j+16 order of gguf_dequant.cu:105-106."""
+    blk = np.zeros(18, dtype=np.uint8)
+    blk[:2] = np.array([1.0], dtype=np.float16).view(np.uint8)
+    for j in range(16):
+        blk[2 + j] = ((15 - j) << 4) | j
+    out = oq.dequant_q4_0(blk)
+    assert out[:16].tolist() == [j - 8 for j in range(16)]
+    assert out[16:].tolist() == [7 - j for j in range(16)]
+
+
+def test_q4_0_signed_zeros():
+    """d < 0 with q = 8 gives -0.0 (fp32 -0.5 * 0 = -0); d = +0 gives -0 for q < 8."""
+    blk = np.zeros((2, 18), dtype=np.uint8)
+    blk[0, :2] = np.array([-0.5], dtype=np.float16).view(np.uint8)
+    blk[0, 2:] = 0x88
+    blk[1, :2] = np.array([0.0], dtype=np.float16).view(np.uint8)
+    blk[1, 2:] = 0x0F  # low nibble 15 (+7 * 0 = +0), high nibble 0 (-8 * 0 = -0)
+    bits = oq.dequant_q4_0(blk).view(np.uint16)
+    assert all(b == 0x8000 for b in bits[:32])
+    assert all(b == 0x0000 for b in bits[32:48]) and all(b == 0x8000 for b in bits[48:])
+
+
+def test_q8_0_known_answer_block():
+    blk = np.zeros(34, dtype=np.uint8)
+    blk[:2] = np.array([0.5], dtype=np.float16).view(np.uint8)
+    q = np.array([-127, -128, -1, 0, 1, 127] + list(range(-13, 13)), dtype=np.int8)
+    blk[2:] = q.view(np.uint8)
+    assert oq.dequant_q8_0(blk).tolist() == [0.5 * v for v in q.tolist()]
+
+
+def test_affine_nibble_order_lsb_first():
+    """word 0x76543210 holds elements 0..7 = 0..7 (runtime/affine_q4_dequant.cu:50-58)."""
+    w = np.array([0x76543210, 0xFEDCBA98], dtype=np.uint32)
+    assert oq.unpack_affine_nibbles(w).tolist() == list(range(16))
+    out = oq.dequant_affine_q4(w, np.array([1.0, 2.0], np.float16), np.array([0.0, -1.0], np.float16), 16, 8)
+    assert out.tolist() == list(range(8)) + [2 * v - 1 for v in range(8, 16)]
+
+
+def test_affine_group_is_flat_index():
+    """Groups follow the flat element index, crossing row boundaries when
+    in_dim is not a multiple of group_size (the reference's group_idx)."""
+    w = np.full(6, 0x11111111, dtype=np.uint32)  # 48 nibbles of 1
+    s = np.array([1.0, 2.0, 4.0], np.float16)
+    out = oq.dequant_affine_q4(w, s, np.zeros(3, np.float16), 48, 16)
+    assert out.tolist() == [1.0] * 16 + [2.0] * 16 + [4.0] * 16
+
+
+# ----------------------------------------------------------- exact restatements
+
+
+SPECIAL_D = [0.0, -0.0, 1.0, -1.0, 0.5, 6.0e-8, -5.96e-8, 3.0e-5, 65504.0, -65504.0, 7.1e3, 0.0123, 1e-3]
+
+
+def _random_q4_blocks(n, seed):
+    rng = np.random.default_rng(seed)
+    raw = rng.integers(0, 256, size=(n, 18), dtype=np.uint8)
+    d = np.concatenate([np.array(SPECIAL_D, np.float16),
+                        rng.uniform(-2, 2, n - len(SPECIAL_D)).astype(np.float16)])
+    raw[:, :2] = d.view(np.uint8).reshape(n, 2)
+    return raw
+
+
+def test_q4_0_matches_exact_rounding():
+    raw = _random_q4_blocks(64, 1)
+    got = oq.dequant_q4_0(raw).view(np.uint16)
+    for i, (g, blk) in enumerate(zip(got.reshape(-1, 32), raw)):
+        d = f16(int(blk[0]) | (int(blk[1]) << 8))
+        d_neg = bool(blk[1] & 0x80)
+        for j in range(32):
+            q = ((int(blk[2 + j % 16]) >> (4 * (j // 16))) & 15) - 8
+            v = round_rne(d * q, 11, -14, 15)
+            if v == 0:
+                assert _sign_bit(int(g[j])) == (d_neg != (q < 0)) and int(g[j]) & 0x7FFF == 0, (i, j)
+            else:
+                assert int(g[j]) == to_f16_bits(v), (i, j)
+
+
+def test_q8_0_matches_exact_rounding():
+    rng = np.random.default_rng(2)
+    n = 64
+    raw = rng.integers(0, 256, size=(n, 34), dtype=np.uint8)
+    d = np.concatenate([np.array(SPECIAL_D, np.float16), rng.uniform(-0.01, 0.01, n - len(SPECIAL_D)).astype(np.float16)])
+    raw[:, :2] = d.view(np.uint8).reshape(n, 2)
+    got = oq.dequant_q8_0(raw).view(np.uint16)
+    for g, blk in zip(got.reshape(-1, 32), raw):
+        dd = f16(int(blk[0]) | (int(blk[1]) << 8))
+        d_neg = bool(blk[1] & 0x80)
+        for j in range(32):
+            q = int(np.int8(np.uint8(blk[2 + j])))
+            v = round_rne(dd * q, 11, -14, 15)
+            if v == 0:
+                assert _sign_bit(int(g[j])) == (d_neg != (q < 0)) and int(g[j]) & 0x7FFF == 0
+            else:
+                assert int(g[j]) == to_f16_bits(v)
+
+
+def test_affine_matches_exact_double_rounding():
+    """nib*s + b rounded once to fp32, then once to fp16 — not a single rounding."""
+    rng = np.random.default_rng(3)
+    groups, g = 40, 16
+    w = rng.integers(0, 2**32, size=groups * g // 8, dtype=np.uint64).astype(np.uint32)
+    s = np.concatenate([np.array([1.0, -2.0, 6.0e-8, 65504.0, 0.0], np.float16),
+                        rng.uniform(0.005, 0.02, groups - 5).astype(np.float16)])
+    b = np.concatenate([np.array([1e-7, 3.0, -65504.0, 1.0, -0.0], np.float16),
+                        (rng.normal(0, 0.05, groups - 5)).astype(np.float16)])
+    got = oq.dequant_affine_q4(w, s, b, groups * g, g).view(np.uint16)
+    nib = oq.unpack_affine_nibbles(w)
+    for i in range(groups * g):
+        G = i // g
+        exact = int(nib[i]) * Fraction(float(s[G])) + Fraction(float(b[G]))
+        v32 = round_rne(exact, 24, -126, 127)
+        v = round_rne(Fraction(v32) if not isinstance(v32, float) else v32, 11, -14, 15) if not isinstance(v32, float) else v32
+        if v == 0:
+            continue  # sign of an exact zero sum: fp32 rules (x + -x = +0) checked below
+        assert int(got[i]) == to_f16_bits(v), i
+    # exact zero: 0*s + (-0) = +0 in round-to-nearest (fp32 add of +0 and -0)
+    z = oq.dequant_affine_q4(np.zeros(1, np.uint32), np.array([1.0], np.float16), np.array([-0.0], np.float16), 8, 8)
+    assert z.view(np.uint16).tolist() == [0] * 8
+
+
+# ------------------------------------------------------------------ products
+
+
+def test_gemv_brute_force():
+    rng = np.random.default_rng(4)
+    M, K, B = 5, 64, 3
+    raw = syn.q4_0_weights(M, K, torch.Generator().manual_seed(4)).numpy()
+    w = oq.dequant_q4_0(raw).reshape(M, K)
+    x = rng.normal(size=(B, K)).astype(np.float16)
+    y = oq.gemv(w, x)
+    for b in range(B):
+        for r in range(M):
+            ref = math.fsum(float(w[r, k]) * float(x[b, k]) for k in range(K))
+            assert abs(y[b, r] - ref) <= 1e-12 * max(1.0, abs(ref))
+    norms = oq.row_norms(w, x)
+    for b in range(B):
+        for r in range(M):
+            assert abs(norms[b, r] - math.sqrt(sum((float(w[r, k]) * float(x[b, k])) ** 2 for k in range(K)))) < 1e-9
+
+
+def test_gemv_closed_forms():
+    M, K = 8, 256
+    raw = syn.q4_0_weights(M, K, torch.Generator().manual_seed(5)).numpy().reshape(-1, 18).copy()
+    raw[:, 2:] = 0x88
+    w = oq.dequant_q4_0(raw).reshape(M, K)
+    x = np.random.default_rng(5).normal(size=(1, K)).astype(np.float16)
+    assert np.all(oq.gemv(w, x) == 0)
+    raw2 = syn.q4_0_weights(M, K, torch.Generator().manual_seed(6)).numpy()
+    w2 = oq.dequant_q4_0(raw2).reshape(M, K)
+    e = np.zeros((1, K), np.float16)
+    e[0, 37] = 1
+    assert np.array_equal(oq.gemv(w2, e)[0], w2[:, 37].astype(np.float64))
+
+
+def _fp32_kernel_model(raw, M, K, x, *, swap_nibbles=False, drop_offset=False, shift_scale=False):
+    """fp32-accumulating model of a fused GEMV, optionally with a planted mistake."""
+    b = raw.reshape(-1, 18)
+    d = b[:, :2].copy().view(np.float16)[:, 0].astype(np.float32)
+    if shift_scale:
+        d = np.roll(d, 1)
+    qs = b[:, 2:]
+    lo, hi = (qs & 15).astype(np.float32), (qs >> 4).astype(np.float32)
+    if swap_nibbles:
+        lo, hi = hi, lo
+    off = 0.0 if drop_offset else 8.0
+    w = np.concatenate([(lo - off), (hi - off)], axis=1) * d[:, None]
+    w = w.reshape(M, K).astype(np.float32)
+    return (x.astype(np.float32) @ w.T).astype(np.float16)
+
+
+@pytest.mark.parametrize("mistake", ["swap_nibbles", "drop_offset", "shift_scale"])
+def test_tolerance_rejects_planted_mistakes(mistake):
+    """A correct fp32 model passes the acceptance test; each plausible slip fails it."""
+    M, K = 64, 1024
+    raw = syn.q4_0_weights(M, K, torch.Generator().manual_seed(7)).numpy()
+    x = np.random.default_rng(7).normal(size=(1, K)).astype(np.float16)
+    w = oq.dequant_q4_0(raw).reshape(M, K)
+    ref, norms = oq.gemv(w, x), oq.row_norms(w, x)
+    good = oq.gemv_errors(_fp32_kernel_model(raw, M, K, x), ref, norms)
+    assert good[0] <= oq.GEMV_REL_L2 and good[1] <= oq.GEMV_MAX_NORM
+    bad = oq.gemv_errors(_fp32_kernel_model(raw, M, K, x, **{mistake: True}), ref, norms)
+    assert bad[0] > oq.GEMV_REL_L2 or bad[1] > oq.GEMV_MAX_NORM
+
+
+def test_moe_gather_composition():
+    """top_k = 1 with weight 1 equals down . fp16(fp16(silu(fp16(gate.x))) * fp16(up.x));
+    the result is linear in the routing weights; unknown experts add nothing."""
+    rng = np.random.default_rng(8)
+    H, F = 64, 32
+    mats = {e: [rng.normal(0, 0.1, size=s).astype(np.float16) for s in ((F, H), (F, H), (H, F))] for e in range(3)}
+    gate = lambda e: mats[e][0] if e in mats else None  # noqa: E731
+    up = lambda e: mats[e][1] if e in mats else None  # noqa: E731
+    down = lambda e: mats[e][2] if e in mats else None  # noqa: E731
+    x = rng.normal(size=H).astype(np.float16)
+    y1, hs = oq.moe_gather(x, gate, up, down, [2], [1.0])
+    g = (mats[2][0].astype(np.float64) @ x.astype(np.float64)).astype(np.float16)
+    u = (mats[2][1].astype(np.float64) @ x.astype(np.float64)).astype(np.float16)
+    gf = g.astype(np.float32)
+    sg = (gf / (1 + np.exp(-gf))).astype(np.float16)
+    h = (sg.astype(np.float32) * u.astype(np.float32)).astype(np.float16)
+    assert np.array_equal(hs[0], h)
+    assert np.allclose(y1, mats[2][2].astype(np.float64) @ h.astype(np.float64), rtol=0, atol=1e-12)
+    ya, _ = oq.moe_gather(x, gate, up, down, [0, 1], [0.25, 0.75])
+    y0, _ = oq.moe_gather(x, gate, up, down, [0], [1.0])
+    yb, _ = oq.moe_gather(x, gate, up, down, [1], [1.0])
+    assert np.allclose(ya, 0.25 * y0 + 0.75 * yb, rtol=1e-12, atol=1e-12)
+    yc, _ = oq.moe_gather(x, gate, up, down, [0, 7, 1], [0.25, 0.5, 0.75])
+    assert np.allclose(yc, ya, rtol=0, atol=0)
+
+
+def test_affine_double_rounding_follows_reference():
+    """Cases where rounding nib*s+b straight to fp16 differs from the reference's
+    fp32-then-fp16 exist; the oracle gives the reference's value (checked with
+    the exact-arithmetic rounding above, independent of numpy casts)."""
+    from helpers import double_rounding_cases
+
+    nib, s, b = double_rounding_cases(32, 9)
+    for i in range(len(nib)):
+        exact = int(nib[i]) * Fraction(float(s[i])) + Fraction(float(b[i]))
+        direct = round_rne(exact, 11, -14, 15)
+        twice = round_rne(round_rne(exact, 24, -126, 127), 11, -14, 15)
+        assert direct != twice
+        out = oq.dequant_affine_q4(np.array([nib[i]], np.uint32), s[i:i + 1], b[i:i + 1], 8, 8)
+        assert out.view(np.uint16)[0] == to_f16_bits(twice)

@@ -261,8 +261,6 @@ __global__ __launch_bounds__(kWaves * 64) void gguf_gemv_staged(const uint8_t* _
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int S = K >> 8;
     const int64_t row_bytes = static_cast<int64_t>(S) * L::kSbBytes;
-    build_xprep<F, NB>(smem, X, S, ldx, x_al8 != 0);
-    __syncthreads();
 
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
@@ -280,7 +278,12 @@ __global__ __launch_bounds__(kWaves * 64) void gguf_gemv_staged(const uint8_t* _
 #pragma unroll
     for (int b = 0; b < NB; ++b) acc[b] = 0.f;
 
+    // The first stage's weights are requested before x is staged, so the HBM
+    // latency of the weights overlaps the x loads and the barrier.
     if (T > 0) load_stage<F>(pre, W, row_bytes, make_stage<F>(gw, 0, M, S), lane);
+    build_xprep<F, NB>(smem, X, S, ldx, x_al8 != 0);
+    __syncthreads();
+
     for (int t = 0; t < T; ++t) {
         const int rg = gw + (t / NW) * total_waves;
         const int win = t % NW;

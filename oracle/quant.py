@@ -102,12 +102,29 @@ def row_norms(w_fp16: np.ndarray, x_fp16: np.ndarray) -> np.ndarray:
     return np.sqrt((x * x) @ (w * w).T)
 
 
+def fp16_ulp(v: np.ndarray) -> np.ndarray:
+    """Spacing of the fp16 grid at |v| (float64): the size of one output rounding step."""
+    with np.errstate(over="ignore"):
+        h = np.abs(np.asarray(v, dtype=np.float64)).astype(np.float16)
+    return np.spacing(h).astype(np.float64)
+
+
 def gemv_errors(y_test, y_ref: np.ndarray, norms: np.ndarray) -> tuple[float, float]:
-    """(relative L2 error, max |y - y_ref| / ||w_r * x||) of a kernel result."""
+    """(relative L2 error, max per-row accumulation error / ||w_r * x||) of a kernel result.
+
+    Every kernel (the reference's included, runtime/fused_gemv.cu:102) rounds
+    its fp32 sum once to fp16, an error of up to one fp16 ulp of the result
+    that does not shrink with ||w_r * x||: when the terms of a row share a sign
+    (affine weights have mean ~7.5*scale + bias) |y_r| reaches 50x ||w_r * x||
+    and the correctly rounded fp16 value alone would exceed the 1e-2 bound.
+    The per-row figure therefore charges only what exceeds one fp16 ulp of
+    y_ref; the relative L2 figure charges everything.
+    """
     y = np.asarray(y_test, dtype=np.float64).reshape(y_ref.shape)
     diff = y - y_ref
     rel = float(np.linalg.norm(diff) / max(np.linalg.norm(y_ref), 1e-30))
-    mx = float(np.max(np.abs(diff) / np.maximum(norms, 1e-30))) if diff.size else 0.0
+    excess = np.maximum(np.abs(diff) - fp16_ulp(y_ref), 0.0)
+    mx = float(np.max(excess / np.maximum(norms, 1e-30))) if diff.size else 0.0
     return rel, mx
 
 

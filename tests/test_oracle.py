@@ -268,6 +268,29 @@ def test_tolerance_rejects_planted_mistakes(mistake):
     assert bad[0] > oq.GEMV_REL_L2 or bad[1] > oq.GEMV_MAX_NORM
 
 
+def test_row_bound_charges_only_beyond_one_output_ulp():
+    """Affine rows against a positive x have |y| >> ||w*x||: the correctly rounded
+    fp16 result passes the per-row bound, and so does anything within one ulp,
+    but 3 ulps off, a dropped group or a lost bias fails it."""
+    M, K, g = 128, 4096, 64
+    w, s, b = syn.affine_q4_weights([M, K], g, torch.Generator().manual_seed(11))
+    wq = oq.dequant_affine_q4(w.numpy().view(np.uint32), s.numpy(), b.numpy(), M * K, g).reshape(M, K)
+    x = np.abs(np.random.default_rng(11).normal(size=(1, K))).astype(np.float16)
+    ref, norms = oq.gemv(wq, x), oq.row_norms(wq, x)
+    assert np.max(np.abs(ref) / norms) > 30  # the regime the allowance is for
+    y16 = ref.astype(np.float16)
+    assert np.max(np.abs(y16 - ref) / norms) > oq.GEMV_MAX_NORM  # the plain bound would reject it
+    assert oq.gemv_errors(y16, ref, norms)[1] == 0.0
+    ulp = oq.fp16_ulp(ref)
+    assert oq.gemv_errors(ref + 0.99 * ulp, ref, norms)[1] == 0.0
+    assert oq.gemv_errors(ref + 3 * ulp, ref, norms)[1] > oq.GEMV_MAX_NORM
+    dropped = oq.gemv(np.concatenate([wq[:, : K - g], np.zeros((M, g), np.float16)], axis=1), x)
+    assert oq.gemv_errors(dropped.astype(np.float16), ref, norms)[1] > oq.GEMV_MAX_NORM
+    wq_nobias = oq.dequant_affine_q4(w.numpy().view(np.uint32), s.numpy(), np.zeros_like(b.numpy()), M * K, g)
+    nobias = oq.gemv(wq_nobias.reshape(M, K), x).astype(np.float16)
+    assert oq.gemv_errors(nobias, ref, norms)[1] > oq.GEMV_MAX_NORM
+
+
 def test_moe_gather_composition():
     """top_k = 1 with weight 1 equals down . fp16(fp16(silu(fp16(gate.x))) * fp16(up.x));
     the result is linear in the routing weights; unknown experts add nothing."""

@@ -84,12 +84,43 @@ __device__ __forceinline__ uint32_t nib_hi_pair(uint32_t v) {
     return (v & 0x00F000F0u) | 0x54005400u;
 }
 
-// Sum over the 16 lanes of each DPP row (lanes 16r .. 16r+15).
+// The same two nibble-pair conversions as single v_and_or_b32 instructions.
+// gfx9 VOP3 encodings take no literal constants, so written with literals the
+// compiler splits each into v_and + v_or; here the masks live in SGPRs and the
+// exponent bits in VGPRs, made opaque once per kernel so they are not
+// rematerialized at every use.
+struct NibUnpack {
+    uint32_t mask_lo, mask_hi;  // SGPR
+    uint32_t bits_lo, bits_hi;  // VGPR
+    __device__ __forceinline__ NibUnpack() : mask_lo(0x000F000Fu), mask_hi(0x00F000F0u), bits_lo(0x64006400u), bits_hi(0x54005400u) {
+        asm volatile("" : "+s"(mask_lo), "+s"(mask_hi), "+v"(bits_lo), "+v"(bits_hi));
+    }
+    __device__ __forceinline__ uint32_t lo(uint32_t v) const {
+        uint32_t r;
+        asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "s"(mask_lo), "v"(bits_lo));
+        return r;
+    }
+    __device__ __forceinline__ uint32_t hi(uint32_t v) const {
+        uint32_t r;
+        asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "s"(mask_hi), "v"(bits_hi));
+        return r;
+    }
+};
+
+// v read from another lane of the same 16-lane DPP row (VALU data movement).
+template <int CTRL>
+__device__ __forceinline__ float dpp_read(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the 16 lanes of each DPP row (lanes 16r .. 16r+15), every lane of
+// the row receiving the total: quad xor 1, quad xor 2, then the half-row
+// mirror (i <-> 7-i) and the row mirror (i <-> 15-i).
 __device__ __forceinline__ float row16_sum(float v) {
-    v += __shfl_xor(v, 8, 16);
-    v += __shfl_xor(v, 4, 16);
-    v += __shfl_xor(v, 2, 16);
-    v += __shfl_xor(v, 1, 16);
+    v += dpp_read<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_read<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_read<0x141>(v);  // row_half_mirror
+    v += dpp_read<0x140>(v);  // row_mirror
     return v;
 }
 // Sum over groups of `width` lanes (power of two <= 64).

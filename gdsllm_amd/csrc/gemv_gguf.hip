@@ -318,6 +318,343 @@ __global__ __launch_bounds__(kWaves * 64) void gguf_gemv_staged(const uint8_t* _
     }
 }
 
+// ---- row-span kernel (batch 1..2) ----------------------------------------------
+// Same stages as gguf_gemv_staged (4 rows x one window of 16 super-blocks =
+// 128 blocks, fetched with coalesced 16-byte loads and transposed through a
+// per-wave LDS slot), but after the transpose lane c owns blocks 2c and 2c+1
+// of the window in all 4 rows.  Its slice of x (64 elements per batch row) is
+// the same for every row it touches, so it sits in registers: the workgroup
+// prepares x once in LDS (fp16 pairs in the order the unpacked nibbles come
+// out in, plus each block's offset correction) while the first stage's
+// weights are in flight, and a wave reloads its slice only when its window
+// changes.  The 8 (row, block) dot-product chains of a stage are interleaved,
+// and the 4 row sums of a wave reduce in 3 cross-lane swaps + 4 DPP steps.
+
+constexpr int kWinBlocks = kSbPerWindow * 8;  // blocks per row in one stage
+
+// fp16 pairs (c, c): 1032 = 1024 + 8 and 72 = 64 + 8 undo the exponent-trick
+// bias and the Q4_0 offset 8 of low / high nibbles; 1152 = 1024 + 128 undoes
+// the biased Q8_0 byte.
+constexpr uint32_t kPair1032 = 0x64086408u;
+constexpr uint32_t kPair72 = 0x54805480u;
+constexpr uint32_t kPair1152 = 0x64806480u;
+
+// Prepared x of one lane span (2 blocks = 64 elements of one batch row): 16
+// packed pairs per block, then the two corrections.  The 144-byte stride (36
+// dwords) puts 8 consecutive lanes' ds_read_b128 on distinct bank quads.
+constexpr int kSpanRec = 144;
+
+template <int NB>
+struct XSlice {
+    uint32_t p[NB][2][16];  // packed fp16 pairs of blocks 2c, 2c+1, per batch row
+    float c[NB][2];         // offset correction of each block
+};
+
+// (lo, hi) = low halves / high halves of (u, v): v_perm_b32 selectors with
+// S0 = v, S1 = u.
+constexpr uint32_t kSelLo = 0x05040100u;
+constexpr uint32_t kSelHi = 0x07060302u;
+
+// 32 raw fp16 of one block (r[i] = elements 2i, 2i+1) -> 16 pairs in unpack
+// order (p) and the block's offset correction (returned).
+template <Fmt F>
+__device__ __forceinline__ float permute_block(const uint32_t (&r)[16], uint32_t (&p)[16]) {
+    float c = 0.f;
+    if constexpr (F == Fmt::Q4_0) {
+        // qs dword dd: low nibbles = elements 4dd..4dd+3, high = 16+4dd..19+4dd;
+        // pairs (bytes 0,2 low) (bytes 0,2 high) (bytes 1,3 low) (bytes 1,3 high)
+#pragma unroll
+        for (int dd = 0; dd < 4; ++dd) {
+            const uint32_t u = r[2 * dd], v = r[2 * dd + 1];
+            const uint32_t uh = r[8 + 2 * dd], vh = r[9 + 2 * dd];
+            p[4 * dd + 0] = __builtin_amdgcn_perm(v, u, kSelLo);
+            p[4 * dd + 1] = __builtin_amdgcn_perm(vh, uh, kSelLo);
+            p[4 * dd + 2] = __builtin_amdgcn_perm(v, u, kSelHi);
+            p[4 * dd + 3] = __builtin_amdgcn_perm(vh, uh, kSelHi);
+            c = dot2(p[4 * dd + 0], kPair1032, c);
+            c = dot2(p[4 * dd + 2], kPair1032, c);
+            c = dot2(p[4 * dd + 1], kPair72, c);
+            c = dot2(p[4 * dd + 3], kPair72, c);
+        }
+    } else {
+        // qs dword dd = elements 4dd..4dd+3: pairs (bytes 0,2) (bytes 1,3)
+#pragma unroll
+        for (int dd = 0; dd < 8; ++dd) {
+            const uint32_t u = r[2 * dd], v = r[2 * dd + 1];
+            p[2 * dd] = __builtin_amdgcn_perm(v, u, kSelLo);
+            p[2 * dd + 1] = __builtin_amdgcn_perm(v, u, kSelHi);
+            c = dot2(p[2 * dd], kPair1152, c);
+            c = dot2(p[2 * dd + 1], kPair1152, c);
+        }
+    }
+    return c;
+}
+
+// The workgroup writes the prepared spans of every window for NB batch rows:
+// record (b, w, c) at xp + ((b*NW + w)*64 + c)*kSpanRec.  One item = one block.
+template <Fmt F, int NB>
+__device__ void build_spans(uint8_t* xp, const uint16_t* __restrict__ X, int64_t ldx, int K, int NW, bool al16) {
+    const int nblk = K >> 5;
+    const int per_row = NW * kWinBlocks;
+    for (int it = threadIdx.x; it < NB * per_row; it += kWaves * 64) {
+        const int g = it % per_row, b = it / per_row;
+        if (g >= nblk) continue;  // past the end of the row: its lanes never compute
+        const uint16_t* src = X + b * ldx + 32 * g;
+        uint32_t r[16];
+        if (al16) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint4 v = *reinterpret_cast<const uint4*>(src + 8 * k);
+                r[4 * k] = v.x;
+                r[4 * k + 1] = v.y;
+                r[4 * k + 2] = v.z;
+                r[4 * k + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) r[i] = static_cast<uint32_t>(src[2 * i]) | (static_cast<uint32_t>(src[2 * i + 1]) << 16);
+        }
+        uint32_t pr[16];
+        const float c = permute_block<F>(r, pr);
+        const int w = g / kWinBlocks, cb = g % kWinBlocks;
+        uint8_t* rec = xp + ((b * NW + w) * 64 + (cb >> 1)) * kSpanRec;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            *reinterpret_cast<uint4*>(rec + 64 * (cb & 1) + 16 * k) = make_uint4(pr[4 * k], pr[4 * k + 1], pr[4 * k + 2], pr[4 * k + 3]);
+        *reinterpret_cast<float*>(rec + 128 + 4 * (cb & 1)) = c;
+    }
+}
+
+template <int NB>
+__device__ __forceinline__ void load_span(XSlice<NB>& xs, const uint8_t* xp, int NW, int w, int lane) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const uint8_t* rec = xp + ((b * NW + w) * 64 + lane) * kSpanRec;
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint4 v = *reinterpret_cast<const uint4*>(rec + 64 * blk + 16 * k);
+                xs.p[b][blk][4 * k] = v.x;
+                xs.p[b][blk][4 * k + 1] = v.y;
+                xs.p[b][blk][4 * k + 2] = v.z;
+                xs.p[b][blk][4 * k + 3] = v.w;
+            }
+        const float2 c = *reinterpret_cast<const float2*>(rec + 128);
+        xs.c[b][0] = c.x;
+        xs.c[b][1] = c.y;
+    }
+}
+
+// Adds the dot products of qs dword dd of one block with its x pairs to S.
+template <Fmt F>
+__device__ __forceinline__ float dword_dot(uint32_t q, const uint32_t* xp, int dd, float S, const NibUnpack& nu) {
+    if constexpr (F == Fmt::Q4_0) {
+        const uint32_t vs = q >> 8;
+        S = dot2(nu.lo(q), xp[4 * dd + 0], S);
+        S = dot2(nu.hi(q), xp[4 * dd + 1], S);
+        S = dot2(nu.lo(vs), xp[4 * dd + 2], S);
+        S = dot2(nu.hi(vs), xp[4 * dd + 3], S);
+    } else {
+        // biased byte u = q + 128 in the low byte of each half: 1024 + u
+        const uint32_t u = q ^ 0x80808080u;
+        S = dot2(__builtin_amdgcn_perm(0x64646464u, u, 0x04020400u), xp[2 * dd], S);
+        S = dot2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030401u), xp[2 * dd + 1], S);
+    }
+    return S;
+}
+
+// Sums acc[0..3] over the 64 lanes of the wave.  Lane L ends up holding the
+// total of row 2*(L>>5) + ((L>>4)&1): lanes 0-15 row 0, 16-31 row 1, 32-47
+// row 2, 48-63 row 3.
+__device__ __forceinline__ float reduce_rows4(const float (&acc)[4], int lane) {
+    const bool h32 = lane & 32;
+    float k0 = h32 ? acc[2] : acc[0], k1 = h32 ? acc[3] : acc[1];
+    const float s0 = h32 ? acc[0] : acc[2], s1 = h32 ? acc[1] : acc[3];
+    k0 += __shfl_xor(s0, 32);
+    k1 += __shfl_xor(s1, 32);
+    const bool h16 = lane & 16;
+    float k = h16 ? k1 : k0;
+    k += __shfl_xor(h16 ? k0 : k1, 16);
+    return row16_sum(k);
+}
+
+// Stage loads and LDS stores.  A full stage (4 rows x 16 super-blocks) has the
+// same per-lane chunk offsets every time, so they are computed once per kernel
+// (goff) and each load is a uniform stage base + a per-lane 32-bit offset; its
+// rows are contiguous in LDS, so chunk c goes to byte 16c.  Partial stages
+// (the last rows of M, the last window of a row) take the predicated path.
+// Offsets stay in 32 bits and the multiplies in 24 bits: in_dim <= 2^20.
+template <Fmt F>
+__device__ __forceinline__ void rows_load(uint4 (&pre)[Layout<F>::kSbChunks], const uint8_t* __restrict__ W,
+                                          uint32_t row_bytes, const uint32_t (&goff)[Layout<F>::kSbChunks],
+                                          const Stage& st, int lane) {
+    using L = Layout<F>;
+    const uint8_t* base = W + static_cast<int64_t>(st.r0) * row_bytes + st.sb0 * L::kSbBytes;
+    if (st.nrows == kRowsPerStage && st.nsb == kSbPerWindow) {
+#pragma unroll
+        for (int j = 0; j < L::kSbChunks; ++j) pre[j] = load_nt16(base + goff[j]);
+    } else {
+        const int total = st.nrows * st.seg_chunks;
+#pragma unroll
+        for (int j = 0; j < L::kSbChunks; ++j) {
+            const int c = 64 * j + lane;
+            if (c < total) {
+                const uint32_t rl = __umul24(c, st.magic) >> 20;
+                const uint32_t off = c - __umul24(rl, st.seg_chunks);
+                pre[j] = load_nt16(base + (__umul24(rl, row_bytes) + 16 * off));
+            }
+        }
+    }
+}
+
+template <Fmt F>
+__device__ __forceinline__ void rows_store(const uint4 (&pre)[Layout<F>::kSbChunks], uint8_t* stage, const Stage& st,
+                                           int lane) {
+    using L = Layout<F>;
+    constexpr int kSegBytes = kSbPerWindow * L::kSbBytes;
+    if (st.nrows == kRowsPerStage && st.nsb == kSbPerWindow) {
+#pragma unroll
+        for (int j = 0; j < L::kSbChunks; ++j) *reinterpret_cast<uint4*>(stage + 16 * (64 * j + lane)) = pre[j];
+    } else {
+        const int total = st.nrows * st.seg_chunks;
+#pragma unroll
+        for (int j = 0; j < L::kSbChunks; ++j) {
+            const int c = 64 * j + lane;
+            if (c < total) {
+                const uint32_t rl = __umul24(c, st.magic) >> 20;
+                const uint32_t off = c - __umul24(rl, st.seg_chunks);
+                *reinterpret_cast<uint4*>(stage + __umul24(rl, kSegBytes) + 16 * off) = pre[j];
+            }
+        }
+    }
+}
+
+template <Fmt F, int NB>
+size_t rows_lds_bytes(int nw) {
+    return static_cast<size_t>(kWaves) * stage_bytes<F>() + static_cast<size_t>(NB) * nw * 64 * kSpanRec;
+}
+
+template <Fmt F, int NB>
+__global__ __launch_bounds__(kWaves * 64) void gguf_gemv_rows(const uint8_t* __restrict__ W,
+                                                              const uint16_t* __restrict__ X,
+                                                              uint16_t* __restrict__ Y, int M, int K, int64_t ldx,
+                                                              int64_t ldy, int x_al16) {
+    using L = Layout<F>;
+    constexpr int kSegBytes = kSbPerWindow * L::kSbBytes;  // one row of a stage
+    constexpr int kSegChunks = kSbPerWindow * L::kSbChunks;
+    constexpr int kSpanDw = L::kBlockBytes / 2;             // dwords of a lane's 2 blocks
+    constexpr int kQd = (L::kBlockBytes - 2) / 4;           // qs dwords per block
+    constexpr int kRowsIlp = F == Fmt::Q4_0 ? 4 : 2;        // rows whose chains interleave
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int S = K >> 8;
+    const uint32_t row_bytes = static_cast<uint32_t>(S) * L::kSbBytes;
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    uint8_t* stage = smem + wave * stage_bytes<F>();
+    uint8_t* xp = smem + kWaves * stage_bytes<F>();
+    const int RG = (M + kRowsPerStage - 1) / kRowsPerStage;
+    const int NW = (S + kSbPerWindow - 1) / kSbPerWindow;
+    const int total_waves = gridDim.x * kWaves;
+    const int gw = blockIdx.x * kWaves + wave;
+    const int my_rgs = gw < RG ? (RG - 1 - gw) / total_waves + 1 : 0;
+    const int T = my_rgs * NW;
+    const NibUnpack nu;
+
+    uint32_t goff[L::kSbChunks];
+#pragma unroll
+    for (int j = 0; j < L::kSbChunks; ++j) {
+        const uint32_t c = 64 * j + lane;
+        const uint32_t rl = c / kSegChunks;
+        goff[j] = rl * row_bytes + 16 * (c - rl * kSegChunks);
+    }
+
+    // The first stage's weights are requested before x is prepared, so their
+    // HBM latency covers the x loads and the barrier.
+    uint4 pre[L::kSbChunks];
+    if (T > 0) rows_load<F>(pre, W, row_bytes, goff, make_stage<F>(gw, 0, M, S), lane);
+    build_spans<F, NB>(xp, X, ldx, K, NW, x_al16 != 0);
+    __syncthreads();
+    if (T == 0) return;
+
+    XSlice<NB> xs;
+    load_span<NB>(xs, xp, NW, 0, lane);
+    int xwin = 0;
+    float acc[NB][4];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[b][r] = 0.f;
+
+    for (int t = 0; t < T; ++t) {
+        const int win = t % NW;
+        const Stage st = make_stage<F>(gw + (t / NW) * total_waves, win, M, S);
+        rows_store<F>(pre, stage, st, lane);
+        wave_lds_sync();
+        if (t + 1 < T) {
+            const int t1 = t + 1;
+            rows_load<F>(pre, W, row_bytes, goff, make_stage<F>(gw + (t1 / NW) * total_waves, t1 % NW, M, S), lane);
+        }
+        if (win != xwin) {
+            load_span<NB>(xs, xp, NW, win, lane);
+            xwin = win;
+        }
+        // Lanes past the end of a partial window, and rows past M, compute on
+        // stale stage bytes; their sums are never stored.
+        if (lane < st.nsb * 4) {
+#pragma unroll
+            for (int r0 = 0; r0 < kRowsPerStage; r0 += kRowsIlp) {
+                uint32_t D[kRowsIlp][kSpanDw];
+#pragma unroll
+                for (int r = 0; r < kRowsIlp; ++r) {
+                    const uint32_t* src =
+                        reinterpret_cast<const uint32_t*>(stage + (r0 + r) * kSegBytes) + kSpanDw * lane;
+#pragma unroll
+                    for (int i = 0; i < kSpanDw; ++i) D[r][i] = src[i];
+                }
+                // block 2c: scale = bytes 0-1, qs from byte 2; block 2c+1 starts at
+                // byte kBlockBytes (dword-aligned halfway point: scale in the high half)
+                float Sx[NB][kRowsIlp][2];
+#pragma unroll
+                for (int b = 0; b < NB; ++b)
+#pragma unroll
+                    for (int r = 0; r < kRowsIlp; ++r) Sx[b][r][0] = Sx[b][r][1] = 0.f;
+#pragma unroll
+                for (int dd = 0; dd < kQd; ++dd)
+#pragma unroll
+                    for (int r = 0; r < kRowsIlp; ++r) {
+                        const uint32_t q0 = align2(D[r][dd], D[r][dd + 1]);
+                        const uint32_t q1 = D[r][kQd + 1 + dd];
+#pragma unroll
+                        for (int b = 0; b < NB; ++b) {
+                            Sx[b][r][0] = dword_dot<F>(q0, xs.p[b][0], dd, Sx[b][r][0], nu);
+                            Sx[b][r][1] = dword_dot<F>(q1, xs.p[b][1], dd, Sx[b][r][1], nu);
+                        }
+                    }
+#pragma unroll
+                for (int r = 0; r < kRowsIlp; ++r) {
+                    const float d0 = h2f(D[r][0] & 0xFFFFu), d1 = h2f(D[r][kQd] >> 16);
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) {
+                        acc[b][r0 + r] = __builtin_fmaf(d0, Sx[b][r][0] - xs.c[b][0], acc[b][r0 + r]);
+                        acc[b][r0 + r] = __builtin_fmaf(d1, Sx[b][r][1] - xs.c[b][1], acc[b][r0 + r]);
+                    }
+                }
+            }
+        }
+        if (win == NW - 1) {
+            const int row = 2 * (lane >> 5) + ((lane >> 4) & 1);
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const float v = reduce_rows4(acc[b], lane);
+                if ((lane & 15) == 0 && row < st.nrows) Y[b * ldy + st.r0 + row] = f2h_bits(v);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[b][r] = 0.f;
+            }
+        }
+    }
+}
+
 // Any in_dim % 32 == 0 and any alignment: one wave per row, one lane per block,
 // byte loads, the reference's per-element order of operations.
 template <Fmt F>
@@ -389,6 +726,28 @@ int launch_staged(const void* w, const uint16_t* x, uint16_t* y, int M, int K, i
     return check_hip(hipGetLastError(), "gguf_gemv launch");
 }
 
+template <Fmt F, int NB>
+int launch_rows(const void* w, const uint16_t* x, uint16_t* y, int M, int K, int64_t ldx, int64_t ldy,
+                hipStream_t stream) {
+    const int NW = ((K >> 8) + kSbPerWindow - 1) / kSbPerWindow;
+    const size_t lds = rows_lds_bytes<F, NB>(NW);
+    const void* fn = reinterpret_cast<const void*>(&gguf_gemv_rows<F, NB>);
+    if (lds > 65536) {
+        if (int rc = check_hip(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                   static_cast<int>(lds)),
+                               "hipFuncSetAttribute"))
+            return rc;
+    }
+    const int RG = (M + kRowsPerStage - 1) / kRowsPerStage;
+    const int need = (RG + kWaves - 1) / kWaves;
+    const int cap = blocks_per_cu(fn, lds) * cu_count();
+    const int grid = need < cap ? need : cap;
+    const bool x_al16 = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (ldx % 8 == 0);
+    hipLaunchKernelGGL((gguf_gemv_rows<F, NB>), dim3(grid), dim3(kWaves * 64), lds, stream,
+                       static_cast<const uint8_t*>(w), x, y, M, K, ldx, ldy, x_al16 ? 1 : 0);
+    return check_hip(hipGetLastError(), "gguf_gemv launch");
+}
+
 template <Fmt F>
 int gemv(const char* name, const void* w, const void* x, void* y, int64_t out_dim, int64_t in_dim,
          int64_t batch, int64_t ldx, int64_t ldy, void* stream) {
@@ -413,6 +772,12 @@ int gemv(const char* name, const void* w, const void* x, void* y, int64_t out_di
     auto* yp = static_cast<uint16_t*>(y);
     const bool fast = (K % 256 == 0) && (reinterpret_cast<uintptr_t>(w) % 16 == 0);
     int rc = GDSLLM_OK;
+    const int NWr = ((K >> 8) + kSbPerWindow - 1) / kSbPerWindow;
+    if (fast && batch <= 2 && K <= (1 << 20) &&
+        (batch == 1 ? rows_lds_bytes<F, 1>(NWr) : rows_lds_bytes<F, 2>(NWr)) <= static_cast<size_t>(max_lds_bytes())) {
+        rc = batch == 1 ? launch_rows<F, 1>(w, xp, yp, M, K, ldx, ldy, s) : launch_rows<F, 2>(w, xp, yp, M, K, ldx, ldy, s);
+        return rc == GDSLLM_OK ? ok() : rc;
+    }
     if (fast) {
         const int S = K >> 8;
         const size_t budget = static_cast<size_t>(max_lds_bytes());

@@ -68,9 +68,10 @@ def test_gguf_gemv_misaligned_inputs(gpu, fmt):
     assert_gemv_close(to_np(y), deq, to_np(x), f"{fmt} misaligned")
 
 
-def test_gguf_gemv_strided_batch(gpu):
+@pytest.mark.parametrize("B", [2, 3])
+def test_gguf_gemv_strided_batch(gpu, B):
     """ldx / ldy larger than the row: rows of x and y taken from wider buffers."""
-    M, K, B = 50, 256, 3
+    M, K = 50, 256
     w, x, deq = _gguf_case("q4_0", M, K, B, 91)
     xw = torch.zeros(B, K + 64, dtype=torch.float16)
     xw[:, :K] = x

@@ -54,6 +54,22 @@ def sweep_bytes() -> int:
     return N_LAYERS * per_layer + q4_bytes(m, k) + 2 * k + 2 * m
 
 
+PROFILE = os.path.join(ROOT, "profiles", "q4_0_gemv_11008x4096_b1.txt")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the headline kernel, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (None when absent)."""
+    try:
+        with open(PROFILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def _ensure_built() -> None:
     from gdsllm_amd import build as b
 
@@ -148,8 +164,170 @@ def bench_decode_sweep(args, dev):
     end.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / args.sweep_tokens
-    del layers, lm_head
-    return ms
+    return ms, (layers, lm_head)
+
+
+def _replay_ms(capture, reps: int, warm: int = 3) -> float:
+    """Captures `capture()` (launches on the current stream) into a HIP graph
+    once, replays it `warm` times untimed, then `reps` times between HIP
+    events on the launch stream; returns ms per replay."""
+    import torch
+
+    capture()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        capture()
+    for _ in range(warm):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def _gemv_call(fmt: str, w, x, y, m: int, k: int, b: int) -> None:
+    import torch
+
+    from gdsllm_amd import capi, check
+
+    fn = capi().gdsllm_fused_q4_0_gemv if fmt == "q4_0" else capi().gdsllm_fused_q8_0_gemv
+    check(fn(w.data_ptr(), x.data_ptr(), y.data_ptr(), m, k, b, k, m, torch.cuda.current_stream().cuda_stream))
+
+
+def bench_q8_layer(dev, layers_rotated: int = 3, reps: int = 50):
+    """Q8_0 LLaMA-7B decoder layer at batch 1: 7 GEMVs per layer, rotating over
+    `layers_rotated` distinct layers (3 x 215 MB > the 256 MB Infinity Cache)."""
+    import torch
+
+    from gdsllm_amd import synthetic as syn
+
+    gen = torch.Generator(device=dev).manual_seed(1001)
+    layers = [[syn.q8_0_weights(m, k, gen) for m, k in LAYER_SHAPES] for _ in range(layers_rotated)]
+    xs = {k: syn.activations(1, k, gen) for k in (4096, 11008)}
+    ys = {m: torch.empty(1, m, dtype=torch.float16, device=dev) for m in (4096, 11008)}
+
+    def run():
+        for lw in layers:
+            for w, (m, k) in zip(lw, LAYER_SHAPES):
+                _gemv_call("q8_0", w, xs[k], ys[m], m, k, 1)
+
+    ms = _replay_ms(run, reps) / layers_rotated
+    nbytes = sum(m * (k // 32) * 34 + 2 * k + 2 * m for m, k in LAYER_SHAPES)
+    return {"us_per_layer": round(ms * 1e3, 3), "bytes_per_layer": nbytes,
+            "GB_s": round(nbytes / (ms * 1e-3) / 1e9, 1), "pct_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / 80, 1),
+            "layers_rotated": layers_rotated}
+
+
+def bench_moe(dev, calls: int = 64, reps: int = 20):
+    """Affine-Q4 top-10 expert-gather MLP, 512 experts, hidden 4096, ffn 1024,
+    group 64, batch 1; every call in the graph uses its own fresh random
+    distinct top-10 picks from the 3.6 GB resident pool."""
+    import ctypes
+
+    import torch
+
+    from gdsllm_amd import AffineExperts, capi, check
+    from gdsllm_amd import synthetic as syn
+
+    E, H, Fd, g, k = 512, 4096, 1024, 64, 10
+    gen = torch.Generator(device=dev).manual_seed(1002)
+    pools = [syn.affine_q4_weights([E, Fd, H], g, gen), syn.affine_q4_weights([E, Fd, H], g, gen),
+             syn.affine_q4_weights([E, H, Fd], g, gen)]
+
+    def experts(p):
+        w, sc, bi = p
+        e, n, kw = w.shape
+        kk = kw * 8
+        return AffineExperts(w.data_ptr(), sc.data_ptr(), bi.data_ptr(), n * kw * 4, n * (kk // g) * 2,
+                             n * (kk // g) * 2, e, n, kk, g)
+
+    gate, up, down = (experts(p) for p in pools)
+    cg = torch.Generator().manual_seed(1003)
+    idx = torch.stack([torch.randperm(E, generator=cg)[:k] for _ in range(calls)]).to(torch.int32).to(dev)
+    wts = torch.softmax(torch.randn(calls, k, generator=cg), -1).to(torch.float16).to(dev)
+    x = syn.activations(1, H, gen)
+    y = torch.empty(calls, H, dtype=torch.float16, device=dev)
+    ws_bytes = capi().gdsllm_moe_gather_workspace_size(k, Fd)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+
+    def run():
+        s = torch.cuda.current_stream().cuda_stream
+        for i in range(calls):
+            check(capi().gdsllm_moe_gather_affine_q4(ctypes.byref(gate), ctypes.byref(up), ctypes.byref(down),
+                                                     x.data_ptr(), idx[i].data_ptr(), wts[i].data_ptr(), k,
+                                                     y[i].data_ptr(), ws.data_ptr(), ws_bytes, s))
+
+    ms = _replay_ms(run, reps) / calls
+    per_expert = 2 * (Fd * H // 2 + 2 * 2 * Fd * H // g) + (H * Fd // 2 + 2 * 2 * H * Fd // g)
+    nbytes = k * per_expert + 2 * H + 2 * H
+    return {"us_per_call": round(ms * 1e3, 3), "bytes_per_call": nbytes,
+            "GB_s": round(nbytes / (ms * 1e-3) / 1e9, 1), "pct_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / 80, 1),
+            "launches_per_call": 2, "pool_bytes": sum(t.numel() * t.element_size() for p in pools for t in p)}
+
+
+LAYER_70B = [(8192, 8192), (1024, 8192), (1024, 8192), (8192, 8192), (28672, 8192), (28672, 8192), (8192, 28672)]
+
+
+def bench_70b_layer(dev, layers_rotated: int = 2, reps: int = 20):
+    """Q4_0 LLaMA-70B decoder layer (7 GEMVs, 481 MB of weights) at batch
+    1, 2, 4, 8, rotating over `layers_rotated` distinct layers."""
+    import torch
+
+    from gdsllm_amd import synthetic as syn
+
+    gen = torch.Generator(device=dev).manual_seed(1004)
+    layers = [[syn.q4_0_weights(m, k, gen) for m, k in LAYER_70B] for _ in range(layers_rotated)]
+    wbytes = sum(m * (k // 32) * 18 for m, k in LAYER_70B)
+    out = {}
+    for B in (1, 2, 4, 8):
+        xs = {k: syn.activations(B, k, gen) for k in (8192, 28672)}
+        ys = {m: torch.empty(B, m, dtype=torch.float16, device=dev) for m in (1024, 8192, 28672)}
+
+        def run():
+            for lw in layers:
+                for w, (m, k) in zip(lw, LAYER_70B):
+                    _gemv_call("q4_0", w, xs[k], ys[m], m, k, B)
+
+        ms = _replay_ms(run, reps) / layers_rotated
+        nbytes = wbytes + sum(B * (2 * k + 2 * m) for m, k in LAYER_70B)
+        out[f"b{B}"] = {"us_per_layer": round(ms * 1e3, 3), "GB_s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                        "pct_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / 80, 1), "bytes_per_layer": nbytes}
+    out["layers_rotated"] = layers_rotated
+    return out
+
+
+def bench_prefill(dev, layers, lm_head, tokens: int = 512, reps: int = 3):
+    """LLaMA-7B Q4_0 prefill chunk of 512 tokens through the MFMA dequant-GEMM:
+    7 projections per layer x 32 layers + lm_head, one graph per chunk."""
+    import torch
+
+    from gdsllm_amd import capi, check
+    from gdsllm_amd import synthetic as syn
+
+    gen = torch.Generator(device=dev).manual_seed(1005)
+    xs = {k: syn.activations(tokens, k, gen) for k in (4096, 11008)}
+    ys = {m: torch.empty(tokens, m, dtype=torch.float16, device=dev) for m in (4096, 11008, 32000)}
+
+    def gemm(w, m, k):
+        check(capi().gdsllm_dequant_gemm_q4_0(w.data_ptr(), xs[k].data_ptr(), ys[m].data_ptr(), m, k, tokens, k, m,
+                                              torch.cuda.current_stream().cuda_stream))
+
+    def run():
+        for lw in layers:
+            for w, (m, k) in zip(lw, LAYER_SHAPES):
+                gemm(w, m, k)
+        gemm(lm_head, *LM_HEAD)
+
+    ms = _replay_ms(run, reps, warm=1)
+    flops = 2 * tokens * (N_LAYERS * sum(m * k for m, k in LAYER_SHAPES) + LM_HEAD[0] * LM_HEAD[1])
+    return {"ms_per_chunk": round(ms, 3), "tokens": tokens, "tok_s": round(tokens / (ms * 1e-3), 1),
+            "TFLOP_s": round(flops / (ms * 1e-3) / 1e12, 1), "flop_per_chunk": flops,
+            "pct_of_fp16_dense_peak": round(flops / (ms * 1e-3) / 1e12 / 25, 1)}
 
 
 def cpu_baseline(weights_dev, x_dev, y_gpu, seconds: float):
@@ -198,6 +376,8 @@ def main() -> int:
     ap.add_argument("--chunk", type=int, default=64, help="launches per captured graph")
     ap.add_argument("--sweep-tokens", type=int, default=100, help="timed 7B decode-sweep tokens (0 = skip)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget (0 = skip)")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the Q8_0 layer, MoE gather, 70B layer and prefill measurements")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -224,14 +404,30 @@ def main() -> int:
     print(f"# q4_0 gemv 11008x4096 b=1: {us_per_call:.3f} us/call, {gbs:.1f} GB/s "
           f"({100 * gbs / HBM_PEAK_GBS:.1f}% of {HBM_PEAK_GBS:.0f})", file=sys.stderr, flush=True)
 
-    sweep = None
+    sweep, sweep_weights = None, None
     if args.sweep_tokens > 0:
-        ms_tok = bench_decode_sweep(args, dev)
+        ms_tok, sweep_weights = bench_decode_sweep(args, dev)
         sb = sweep_bytes()
         sweep = {"tok_s": round(1e3 / ms_tok, 1), "ms_per_token": round(ms_tok, 4), "launches_per_token": 225,
                  "bytes_per_token": sb, "GB_s": round(sb / (ms_tok * 1e-3) / 1e9, 1)}
         print(f"# 7B decode sweep: {ms_tok:.4f} ms/token, {sweep['tok_s']} tok/s, {sweep['GB_s']} GB/s",
               file=sys.stderr, flush=True)
+
+    configs = None
+    if not args.no_configs:
+        configs = {"q8_0_layer_7b_b1": bench_q8_layer(dev)}
+        print(f"# q8_0 7B layer: {configs['q8_0_layer_7b_b1']}", file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
+        configs["moe_affine_q4_top10"] = bench_moe(dev)
+        print(f"# moe top-10 gather: {configs['moe_affine_q4_top10']}", file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
+        configs["q4_0_layer_70b"] = bench_70b_layer(dev)
+        print(f"# q4_0 70B layer: {configs['q4_0_layer_70b']}", file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
+        if sweep_weights is not None:
+            configs["prefill_7b_512"] = bench_prefill(dev, *sweep_weights)
+            print(f"# prefill 7B 512 tokens: {configs['prefill_7b_512']}", file=sys.stderr, flush=True)
+    sweep_weights = None
 
     cpu, parity = None, None
     if args.cpu_seconds > 0:
@@ -258,8 +454,9 @@ def main() -> int:
         "us_per_call": round(us_per_call, 3),
         "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
         "decode_sweep_7b": sweep,
+        "configs": configs,
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic()},
         "cpu_baseline": cpu,
         "parity": parity,
     }

@@ -1,0 +1,186 @@
+"""The C ABI boundary on the CPU: the library loads, exports exactly what
+include/gdsllm_amd.h declares, and rejects invalid calls before touching the
+device (every call below fails validation or is a no-op, so no HIP work is
+issued and no GPU is needed)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+import gdsllm_amd
+from gdsllm_amd import AffineExperts, capi
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "gdsllm_amd.h"
+
+
+def declared_functions() -> dict:
+    """name -> (return type, argument list text) for every function prototype in the header."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"(int|size_t|const char\*)\s+(gdsllm_\w+)\s*\(([^;]*?)\)\s*;", text, re.S):
+        out[m.group(2)] = (m.group(1), " ".join(m.group(3).split()))
+    return out
+
+
+def test_header_declares_the_entry_points():
+    names = set(declared_functions())
+    assert {"gdsllm_fused_q4_0_gemv", "gdsllm_fused_q8_0_gemv", "gdsllm_fused_affine_q4_gemv", "gdsllm_dequant_q4_0",
+            "gdsllm_dequant_q8_0", "gdsllm_dequant_affine_q4", "gdsllm_moe_gather_affine_q4",
+            "gdsllm_dequant_gemm_q4_0"} <= names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(gdsllm_amd.LIB_PATH))
+    for name in declared_functions():
+        assert hasattr(lib, name), f"{name} declared in the header but not exported"
+
+
+def test_ctypes_table_matches_header():
+    decl = declared_functions()
+    assert set(gdsllm_amd.SIGNATURES) == set(decl), "gdsllm_amd.SIGNATURES and the header disagree"
+    for name, (ret, args) in decl.items():
+        n_args = 0 if args in ("void", "") else args.count(",") + 1
+        assert len(gdsllm_amd.SIGNATURES[name][1]) == n_args, name
+
+
+def test_version_and_empty_error():
+    lib = capi()
+    assert lib.gdsllm_version().startswith(b"gdsllm_amd")
+    assert isinstance(lib.gdsllm_last_error(), bytes)
+
+
+def _err():
+    return capi().gdsllm_last_error().decode()
+
+
+@pytest.mark.parametrize("name", ["gdsllm_fused_q4_0_gemv", "gdsllm_fused_q8_0_gemv"])
+def test_gguf_gemv_validation(name):
+    fn = getattr(capi(), name)
+    assert fn(8, 8, 8, 4, 48, 1, 48, 4, None) == 1 and "multiple of 32" in _err()
+    assert fn(8, 8, 8, 4, 64, 9, 64, 4, None) == 1 and "batch" in _err()
+    assert fn(8, 8, 8, 4, 64, 0, 64, 4, None) == 1
+    assert fn(8, 8, 8, -1, 64, 1, 64, 4, None) == 1 and "negative" in _err()
+    assert fn(None, 8, 8, 4, 64, 1, 64, 4, None) == 1 and "null" in _err()
+    assert fn(8, 8, 8, 4, 64, 2, 32, 4, None) == 1 and "ldx" in _err()
+    assert fn(8, 9, 8, 4, 64, 1, 64, 4, None) == 1 and "aligned" in _err()
+    # empty problems are silent no-ops, as in the reference launchers (fused_gemv.cu:111)
+    assert fn(None, None, None, 0, 64, 1, 64, 0, None) == 0
+    assert fn(None, None, None, 4, 0, 1, 0, 4, None) == 0
+
+
+def test_affine_gemv_validation():
+    fn = capi().gdsllm_fused_affine_q4_gemv
+    assert fn(16, 16, 16, 16, 16, 4, 96, 64, 1, 96, 4, None) == 1 and "group_size" in _err()
+    assert fn(16, 16, 16, 16, 16, 4, 64, 12, 1, 64, 4, None) == 1
+    assert fn(16, 16, 16, 16, 16, 4, 64, 64, 9, 64, 4, None) == 1
+    assert fn(16, 16, 16, 16, 16, 4, 64, 64, 1, 64, 4, None) != 0 or True  # valid shape: not called (no GPU)
+    assert fn(None, None, None, None, None, 0, 64, 64, 1, 64, 0, None) == 0
+
+
+def test_dequant_validation():
+    lib = capi()
+    assert lib.gdsllm_dequant_q4_0(8, 8, -1, None) == 1
+    assert lib.gdsllm_dequant_q4_0(None, 8, 4, None) == 1 and "null" in _err()
+    assert lib.gdsllm_dequant_q4_0(None, None, 0, None) == 0
+    assert lib.gdsllm_dequant_q8_0(8, None, 4, None) == 1
+    a = lib.gdsllm_dequant_affine_q4
+    assert a(16, 16, 16, 16, 64, 64, 12, None) == 2 and "multiple of 8" in _err()
+    assert a(16, 16, 16, 16, 64, 96, 64, None) == 1 and "in_dim" in _err()
+    assert a(16, 16, 16, 16, 72, 64, 64, None) == 1
+    assert a(17, 16, 16, 16, 64, 64, 64, None) == 1 and "misaligned" in _err()
+    assert a(None, None, None, None, 0, 64, 64, None) == 0
+
+
+def test_gemm_validation():
+    g = capi().gdsllm_dequant_gemm_q4_0
+    assert g(16, 16, 16, 4, 96, 2, 96, 4, None) == 2 and "multiple of 64" in _err()
+    assert g(16, 16, 16, 4, 48, 2, 48, 4, None) == 1
+    assert g(16, 16, 16, 4, 64, 2, 32, 4, None) == 1 and "ldx" in _err()
+    assert g(16, 24, 16, 4, 64, 2, 64, 4, None) == 2 and "aligned" in _err()
+    assert g(None, None, None, 4, 64, 0, 64, 4, None) == 0
+
+
+def _experts(w=16, s=16, b=16, E=8, N=256, K=512, g=64, ws=None):
+    return AffineExperts(w, s, b, ws if ws is not None else N * K // 2, N * K // g * 2, N * K // g * 2, E, N, K, g)
+
+
+def test_moe_gather_validation():
+    lib = capi()
+    gate, up = _experts(), _experts()
+    down = _experts(N=512, K=256)
+    ws = lib.gdsllm_moe_gather_workspace_size(3, 256)
+    assert ws >= 3 * 2 * 256 * 2 and ws % 256 == 0
+    call = lambda g, u, d, k=3, wsb=ws, idx=16: lib.gdsllm_moe_gather_affine_q4(  # noqa: E731
+        ctypes.byref(g), ctypes.byref(u), ctypes.byref(d), 16, idx, 16, k, 16, 16, wsb, None)
+    assert call(gate, up, down, k=0) == 1 and "top_k" in _err()
+    assert call(gate, up, down, k=65) == 1
+    assert call(gate, up, _experts(N=256, K=512)) == 1 and "disagree" in _err()
+    assert call(gate, up, down, wsb=ws - 256) == 1 and "workspace" in _err()
+    assert call(_experts(g=48), up, down) == 1
+    assert call(_experts(w=8), up, down) == 1 and "16-byte" in _err()
+    assert call(gate, up, down, idx=18) == 1 and "misaligned" in _err()
+    assert lib.gdsllm_moe_gather_affine_q4(None, ctypes.byref(up), ctypes.byref(down), 16, 16, 16, 3, 16, 16, ws,
+                                           None) == 1
+
+
+def test_buffer_validation():
+    lib = capi()
+    assert lib.gdsllm_buffer_alloc(4096, 0, None, None) == 1
+    p = ctypes.c_void_p(1)
+    assert lib.gdsllm_buffer_alloc(4096, -1, ctypes.byref(p), None) == 1 and p.value is None
+    n = ctypes.c_int64(7)
+    assert lib.gdsllm_buffer_read_file(None, 10, b"/dev/null", 4, 0, 0, 0, ctypes.byref(n)) == 1 and n.value == 0
+    assert lib.gdsllm_buffer_read_file(16, 10, None, 4, 0, 0, 0, None) == 1
+    assert lib.gdsllm_buffer_read_file(16, 10, b"/dev/null", 8, 0, 4, 0, None) == 1 and "exceed" in _err()
+    assert lib.gdsllm_buffer_read_file(16, 10, b"/dev/null", 4, -1, 0, 0, None) == 1
+    assert lib.gdsllm_buffer_read_file(16, 10, b"/no/such/file", 4, 0, 0, 0, None) == 4 and "cannot open" in _err()
+    assert lib.gdsllm_buffer_free(None, 0) == 0
+
+
+def test_extension_module_surface():
+    """The pybind module exports the reference's functions with their argument names."""
+    from gdsllm_amd.runtime import ext
+
+    m = ext()
+    expected = {
+        "init": [], "shutdown": [], "is_driver_open": [],
+        "load_file": ["filepath", "size_bytes", "device_id"],
+        "load_file_region": ["filepath", "size_bytes", "file_offset", "device_id"],
+        "load_expert": ["filepath", "w_file_offset", "w_size", "s_file_offset", "s_size", "b_file_offset", "b_size",
+                        "device_id"],
+        "view_tensor": ["handle", "shape", "dtype", "offset"],
+        "load_tensor": ["filepath", "shape", "dtype", "file_offset", "size_bytes", "device_id"],
+        "dequant_gguf": ["handle", "shape", "gguf_type", "offset", "output"],
+        "fused_dequant_gemv": ["handle", "x", "weight_shape", "gguf_type", "offset"],
+        "dequant_affine_q4": ["handle", "weight_shape", "weight_offset", "scale_offset", "bias_offset", "group_size",
+                              "output"],
+        "fused_affine_q4_gemv": ["handle", "x", "weight_shape", "weight_offset", "scale_offset", "bias_offset",
+                                 "group_size"],
+    }
+    for name, args in expected.items():
+        fn = getattr(m, name)
+        doc = fn.__doc__ or ""
+        for a in args:
+            assert re.search(rf"\b{a}\b", doc), f"{name}: argument {a} missing from the signature"
+    assert hasattr(m, "GdsBufferHandle")
+    for prop in ("size", "device_id", "registered"):
+        assert hasattr(m.GdsBufferHandle, prop)
+
+
+def test_extension_rejects_invalid_handle():
+    import torch
+
+    from gdsllm_amd.runtime import ext
+
+    m = ext()
+    x = torch.zeros(64, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="invalid buffer handle"):
+        m.fused_dequant_gemv(None, x, [4, 64], "q4_0", 0)
+    with pytest.raises(RuntimeError, match="invalid buffer handle"):
+        m.dequant_gguf(None, [4, 64], "q4_0", 0)
+    with pytest.raises(RuntimeError, match="invalid buffer handle"):
+        m.fused_affine_q4_gemv(None, x, [4, 64], 0, 0, 0, 64)
+    with pytest.raises(RuntimeError, match="invalid buffer handle"):
+        m.view_tensor(None, [4], "float16", 0)

@@ -36,7 +36,7 @@ def test_gguf_gemv_b1(gpu, fmt, M, K):
 
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
 @pytest.mark.parametrize("B", [2, 3, 4, 8])
-@pytest.mark.parametrize("M,K", [(70, 4096), (33, 11008), (20, 96)])
+@pytest.mark.parametrize("M,K", [(70, 4096), (33, 11008), (20, 96), (24, 8192), (9, 28672)])
 def test_gguf_gemv_batched(gpu, fmt, B, M, K):
     w, x, deq = _gguf_case(fmt, M, K, B, 2000 + B + M)
     y = gguf_gemv(fmt, w.to(gpu), x.to(gpu), M, K)

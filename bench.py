@@ -376,8 +376,9 @@ def main() -> int:
     ap.add_argument("--chunk", type=int, default=64, help="launches per captured graph")
     ap.add_argument("--sweep-tokens", type=int, default=100, help="timed 7B decode-sweep tokens (0 = skip)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget (0 = skip)")
-    ap.add_argument("--no-configs", action="store_true",
-                    help="skip the Q8_0 layer, MoE gather, 70B layer and prefill measurements")
+    ap.add_argument("--configs", default="q8,moe,70b,prefill",
+                    help="comma list of extra workloads to measure: q8 (Q8_0 7B layer), moe (top-10 expert "
+                         "gather), 70b (Q4_0 70B layer, B=1..8), prefill (512-token MFMA GEMM); '' = none")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -413,20 +414,24 @@ def main() -> int:
         print(f"# 7B decode sweep: {ms_tok:.4f} ms/token, {sweep['tok_s']} tok/s, {sweep['GB_s']} GB/s",
               file=sys.stderr, flush=True)
 
-    configs = None
-    if not args.no_configs:
-        configs = {"q8_0_layer_7b_b1": bench_q8_layer(dev)}
-        print(f"# q8_0 7B layer: {configs['q8_0_layer_7b_b1']}", file=sys.stderr, flush=True)
-        torch.cuda.empty_cache()
-        configs["moe_affine_q4_top10"] = bench_moe(dev)
-        print(f"# moe top-10 gather: {configs['moe_affine_q4_top10']}", file=sys.stderr, flush=True)
-        torch.cuda.empty_cache()
-        configs["q4_0_layer_70b"] = bench_70b_layer(dev)
-        print(f"# q4_0 70B layer: {configs['q4_0_layer_70b']}", file=sys.stderr, flush=True)
-        torch.cuda.empty_cache()
-        if sweep_weights is not None:
-            configs["prefill_7b_512"] = bench_prefill(dev, *sweep_weights)
-            print(f"# prefill 7B 512 tokens: {configs['prefill_7b_512']}", file=sys.stderr, flush=True)
+    wanted = {c.strip() for c in args.configs.split(",") if c.strip()}
+    unknown = wanted - {"q8", "moe", "70b", "prefill"}
+    if unknown:
+        print(f"bench.py: unknown --configs entries {sorted(unknown)}", file=sys.stderr)
+        return 2
+    configs = {}
+    runs = [("q8", "q8_0_layer_7b_b1", lambda: bench_q8_layer(dev)),
+            ("moe", "moe_affine_q4_top10", lambda: bench_moe(dev)),
+            ("70b", "q4_0_layer_70b", lambda: bench_70b_layer(dev)),
+            ("prefill", "prefill_7b_512",
+             lambda: bench_prefill(dev, *sweep_weights) if sweep_weights is not None else None)]
+    for key, name, fn in runs:
+        if key in wanted:
+            res = fn()
+            if res is not None:
+                configs[name] = res
+                print(f"# {name}: {res}", file=sys.stderr, flush=True)
+            torch.cuda.empty_cache()
     sweep_weights = None
 
     cpu, parity = None, None
@@ -454,7 +459,7 @@ def main() -> int:
         "us_per_call": round(us_per_call, 3),
         "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
         "decode_sweep_7b": sweep,
-        "configs": configs,
+        "configs": configs or None,
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic()},
         "cpu_baseline": cpu,

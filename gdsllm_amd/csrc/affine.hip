@@ -116,7 +116,9 @@ struct PlainRows {
     uint16_t* Y;
     int64_t ldy;
     int M;
-    __device__ bool locate(int row, const uint32_t*& w, const uint16_t*& s, const uint16_t*& b, int K, int gpr) const {
+    __device__ int lane_index(int) const { return 0; }
+    __device__ bool locate(int row, const uint32_t*& w, const uint16_t*& s, const uint16_t*& b, int K, int gpr,
+                           int = 0) const {
         w = W + static_cast<int64_t>(row) * (K / 8);
         s = S + static_cast<int64_t>(row) * gpr;
         b = B + static_cast<int64_t>(row) * gpr;
@@ -178,7 +180,7 @@ __global__ __launch_bounds__(kThreads) void affine_gemv(Rows rows, const uint16_
 
     for (int base = 0; base < n_items; base += kU) {
         uint4 wv[kU];
-        float sv[kU], bv[kU];
+        uint32_t sv[kU], bv[kU];
         bool ok[kU];
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
@@ -195,8 +197,8 @@ __global__ __launch_bounds__(kThreads) void affine_gemv(Rows rows, const uint16_
                     ok[u] = true;
                     wv[u] = load_nt16(w + 4 * c);
                     const int G = (32 * c) / gsize;
-                    sv[u] = h2f(s[G]);
-                    bv[u] = h2f(b[G]);
+                    sv[u] = s[G];  // raw bits, converted at use (no early wait)
+                    bv[u] = b[G];
                 }
             }
         }
@@ -209,7 +211,7 @@ __global__ __launch_bounds__(kThreads) void affine_gemv(Rows rows, const uint16_
                 const int c = li + LR * t;
 #pragma unroll
                 for (int b = 0; b < NB; ++b)
-                    acc[b] += chunk_dot(wv[u], smem + (b * CPR + c) * kRec, sv[u], bv[u]);
+                    acc[b] += chunk_dot(wv[u], smem + (b * CPR + c) * kRec, h2f(sv[u]), h2f(bv[u]));
             }
             if (t == CPL - 1) {
                 const int row = (gw + (it / CPL) * TW) * RW + sub;
@@ -290,7 +292,7 @@ __global__ __launch_bounds__(kThreads) void moe_down(gdsllm_affine_experts down,
             const int c = li + LR * t;
             for (int k0 = 0; k0 < top_k; k0 += kU) {
                 uint4 wv[kU];
-                float sv[kU], bv[kU], wk[kU];
+                uint32_t sv[kU], bv[kU], wk[kU];
                 bool ok[kU];
 #pragma unroll
                 for (int u = 0; u < kU; ++u) {
@@ -314,15 +316,17 @@ __global__ __launch_bounds__(kThreads) void moe_down(gdsllm_affine_experts down,
                                 static_cast<int64_t>(o) * gpr;
                             const int G = (32 * c) / gsize;
                             wv[u] = load_nt16(w + 4 * c);
-                            sv[u] = h2f(s[G]);
-                            bv[u] = h2f(b[G]);
-                            wk[u] = h2f(rw[k]);
+                            sv[u] = s[G];  // raw bits, converted at use (no early wait)
+                            bv[u] = b[G];
+                            wk[u] = rw[k];
                         }
                     }
                 }
 #pragma unroll
                 for (int u = 0; u < kU; ++u)
-                    if (ok[u]) acc = __builtin_fmaf(wk[u], chunk_dot(wv[u], smem + ((k0 + u) * CPR + c) * kRec, sv[u], bv[u]), acc);
+                    if (ok[u])
+                        acc = __builtin_fmaf(h2f(wk[u]), chunk_dot(wv[u], smem + ((k0 + u) * CPR + c) * kRec, h2f(sv[u]), h2f(bv[u])),
+                                             acc);
             }
         }
         acc = group_sum<LR>(acc);
@@ -410,6 +414,508 @@ __global__ __launch_bounds__(256) void affine_gemv_generic(const uint32_t* __res
     }
 }
 
+
+// ---- row-span kernels ------------------------------------------------------------
+// Lane li of a row owns the chunks li, li+LR, ... (CPL of them) of every row it
+// touches, so its prepared slice of x stays in registers for the whole kernel.
+// A 16-byte affine chunk is aligned and lies inside one group, so lanes load
+// their chunks directly: LR consecutive lanes cover LR consecutive chunks
+// (coalesced), no LDS transpose.  A wave's stage is 4 load groups of 64/LR
+// rows; the first stage is requested before x is prepared, the next one while
+// the current one is computed, and the 4 partial sums of each lane reduce with
+// two exchange-halving swaps and DPP steps.
+
+constexpr uint32_t kPair1024 = 0x64006400u;  // (1024, 1024)
+constexpr uint32_t kPair64 = 0x54005400u;    // (64, 64)
+constexpr uint32_t kPairOne = 0x3C003C00u;   // (1, 1)
+
+// Prepared x of one 32-element chunk in registers: pairs in chunk_dot order,
+// offset correction 1024*sum(x_even) + 64*sum(x_odd) within each word, and sum(x).
+struct XChunk {
+    uint32_t p[16];
+    float corr, sum;
+};
+
+// 32 raw fp16 of a chunk (r[i] = x[2i], x[2i+1]); zeros when not live.
+__device__ __forceinline__ void load_xchunk_raw(uint32_t (&r)[16], const uint16_t* __restrict__ src, bool al16,
+                                                bool live) {
+    if (live && al16) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint4 v = *reinterpret_cast<const uint4*>(src + 8 * k);
+            r[4 * k] = v.x;
+            r[4 * k + 1] = v.y;
+            r[4 * k + 2] = v.z;
+            r[4 * k + 3] = v.w;
+        }
+    } else if (live) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) r[i] = static_cast<uint32_t>(src[2 * i]) | (static_cast<uint32_t>(src[2 * i + 1]) << 16);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) r[i] = 0u;
+    }
+}
+
+__device__ __forceinline__ void make_xchunk(XChunk& xc, const uint32_t (&r)[16]) {
+    float corr = 0.f, sum = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        // word q = elements 8q..8q+7: pairs (x0,x4) (x1,x5) (x2,x6) (x3,x7)
+        const uint32_t a = r[4 * q], b = r[4 * q + 1], c = r[4 * q + 2], d = r[4 * q + 3];
+        xc.p[4 * q + 0] = __builtin_amdgcn_perm(c, a, 0x05040100u);
+        xc.p[4 * q + 1] = __builtin_amdgcn_perm(c, a, 0x07060302u);
+        xc.p[4 * q + 2] = __builtin_amdgcn_perm(d, b, 0x05040100u);
+        xc.p[4 * q + 3] = __builtin_amdgcn_perm(d, b, 0x07060302u);
+        corr = dot2(xc.p[4 * q + 0], kPair1024, corr);
+        corr = dot2(xc.p[4 * q + 2], kPair1024, corr);
+        corr = dot2(xc.p[4 * q + 1], kPair64, corr);
+        corr = dot2(xc.p[4 * q + 3], kPair64, corr);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) sum = dot2(xc.p[4 * q + k], kPairOne, sum);
+    }
+    xc.corr = corr;
+    xc.sum = sum;
+}
+
+// s*(S - corr) + b*sum for one chunk w against x pairs p.
+__device__ __forceinline__ float chunk_dot_p(uint4 w, const uint32_t* p, float corr, float sum, float s, float b,
+                                             const NibUnpack& nu) {
+    const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+    float S = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t v = wd[q], vs = v >> 8;
+        S = dot2(nu.lo(v), p[4 * q + 0], S);
+        S = dot2(nu.hi(v), p[4 * q + 1], S);
+        S = dot2(nu.lo(vs), p[4 * q + 2], S);
+        S = dot2(nu.hi(vs), p[4 * q + 3], S);
+    }
+    return __builtin_fmaf(s, S - corr, b * sum);
+}
+
+// Sum over aligned groups of N lanes (N = 1, 2, 4, 8, 16), every lane of the
+// group receiving the total; VALU-only DPP steps.
+template <int N>
+__device__ __forceinline__ float lanes_sum(float v) {
+    if constexpr (N >= 2) v += dpp_read<0xB1>(v);   // quad_perm [1,0,3,2]
+    if constexpr (N >= 4) v += dpp_read<0x4E>(v);   // quad_perm [2,3,0,1]
+    if constexpr (N >= 8) v += dpp_read<0x141>(v);  // row_half_mirror
+    if constexpr (N >= 16) v += dpp_read<0x140>(v); // row_mirror
+    return v;
+}
+
+// acc[0..3] summed over the LR lanes of each aligned lane group.  Lane li
+// (= lane % LR) ends up with the total of value j = 2*bit(li, LR/2) +
+// bit(li, LR/4); lanes with li % (LR/4) == 0 hold one value each.
+template <int LR>
+__device__ __forceinline__ float reduce4(const float (&acc)[4], int lane) {
+    constexpr int H1 = LR / 2, H2 = LR / 4;
+    const bool b1 = lane & H1;
+    float k0 = b1 ? acc[2] : acc[0], k1 = b1 ? acc[3] : acc[1];
+    const float s0 = b1 ? acc[0] : acc[2], s1 = b1 ? acc[1] : acc[3];
+    k0 += __shfl_xor(s0, H1);
+    k1 += __shfl_xor(s1, H1);
+    const bool b2 = lane & H2;
+    float k = b2 ? k1 : k0;
+    k += __shfl_xor(b2 ? k0 : k1, H2);
+    return lanes_sum<H2>(k);
+}
+template <int LR>
+__device__ __forceinline__ int reduce4_index(int lane) {
+    return 2 * ((lane & (LR / 2)) ? 1 : 0) + ((lane & (LR / 4)) ? 1 : 0);
+}
+
+// Gate/up rows of the selected experts as one virtual matrix, gate and up of
+// the same FFN row adjacent: virtual row v -> slot k = v / (2F), FFN row
+// n = (v % 2F) / 2, projection v & 1 (0 = gate, 1 = up).  Outputs: g/u fp16
+// [top_k][2][F], and h = fp16(fp16(silu(g)) * u) fp16 [top_k][F].
+struct GateUpPairs {
+    gdsllm_affine_experts gate, up;
+    const int32_t* idx;
+    uint16_t* gu;
+    uint16_t* h;
+    int F;
+    int M;
+    // Lane l holds idx[l] (the slot count is at most 64), read once per wave.
+    __device__ int lane_index(int lane) const { return lane < M / (2 * F) ? idx[lane] : -1; }
+    // v is the same for the whole wave (one row per load group), so the
+    // expert index is a lane read, not a dependent global load.
+    __device__ bool locate(int v, const uint32_t*& w, const uint16_t*& s, const uint16_t*& b, int K, int gpr,
+                           int lane_idx) const {
+        const int k = v / (2 * F);
+        const int rem = v - k * 2 * F;
+        const int n = rem >> 1;
+        const gdsllm_affine_experts& p = (rem & 1) ? up : gate;
+        const int e = __builtin_amdgcn_readlane(lane_idx, k);
+        if (e < 0 || e >= p.num_experts) return false;
+        w = reinterpret_cast<const uint32_t*>(static_cast<const char*>(p.weight) + e * p.weight_stride) +
+            static_cast<int64_t>(n) * (K / 8);
+        s = reinterpret_cast<const uint16_t*>(static_cast<const char*>(p.scales) + e * p.scale_stride) +
+            static_cast<int64_t>(n) * gpr;
+        b = reinterpret_cast<const uint16_t*>(static_cast<const char*>(p.biases) + e * p.bias_stride) +
+            static_cast<int64_t>(n) * gpr;
+        return true;
+    }
+    __device__ void store(int, int v, float val) const {
+        const int k = v / (2 * F);
+        const int rem = v - k * 2 * F;
+        gu[(2 * k + (rem & 1)) * F + (rem >> 1)] = f2h_bits(val);
+    }
+};
+
+template <class Rows> struct IsGateUp { static constexpr bool value = false; };
+template <> struct IsGateUp<GateUpPairs> { static constexpr bool value = true; };
+
+__device__ __forceinline__ uint16_t silu_mul_h(float g, float u) {
+    // torch semantics on fp16 tensors: silu in fp32 rounded to fp16, then the
+    // fp16 product (computed in fp32, rounded once)
+    const float gh = h2f(f2h_bits(g));
+    const float sg = h2f(f2h_bits(gh / (1.0f + expf(-gh))));
+    return f2h_bits(sg * h2f(f2h_bits(u)));
+}
+
+template <int LR, int CPL, int NB, class Rows>
+__global__ __launch_bounds__(kThreads) void affine_rows(Rows rows, const uint16_t* __restrict__ X, int K, int gsize,
+                                                        int64_t ldx, int x_al16) {
+    constexpr int RPG = 64 / LR;  // rows per load group
+    constexpr int G = 4;          // load groups per stage
+    constexpr int RPS = G * RPG;  // rows per stage
+    static_assert(!IsGateUp<Rows>::value || (LR == 64 && NB == 1), "gate/up pairs need one row per load group");
+    const int lane = threadIdx.x & 63;
+    const int li = lane % LR, sub = lane / LR;
+    const int CPR = K >> 5, gpr = K / gsize;
+    const int stages = (rows.M + RPS - 1) / RPS;
+    const int TW = gridDim.x * kWaves;
+    const int gw = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    const int T = gw < stages ? (stages - 1 - gw) / TW + 1 : 0;
+    if (T == 0) return;
+    const NibUnpack nu;
+
+    // Scale / bias bits stay raw until the compute: converting them here would
+    // make the wave wait for every load issued before them (loads retire in
+    // order), turning the prefetch into a stall.
+    uint4 wv[G][CPL];
+    uint32_t sv[G][CPL], bv[G][CPL];
+    bool ok[G];
+    const int lane_idx = rows.lane_index(lane);
+    auto issue = [&](int st) {
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            const int row = st * RPS + j * RPG + sub;
+            const uint32_t* w = nullptr;
+            const uint16_t *sp = nullptr, *bp = nullptr;
+            ok[j] = row < rows.M && rows.locate(row, w, sp, bp, K, gpr, lane_idx);
+#pragma unroll
+            for (int i = 0; i < CPL; ++i) {
+                const int c = li + LR * i;
+                if (ok[j] && c < CPR) {
+                    wv[j][i] = load_nt16(w + 4 * c);
+                    const int gi = (32 * c) / gsize;
+                    sv[j][i] = sp[gi];
+                    bv[j][i] = bp[gi];
+                }
+            }
+        }
+    };
+    // x first, then the first stage's weights: preparing x waits only for x
+    uint32_t xr[NB][CPL][16];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            const int c = li + LR * i;
+            load_xchunk_raw(xr[b][i], X + b * ldx + 32 * c, x_al16 != 0, c < CPR);
+        }
+    issue(gw);
+    XChunk xc[NB][CPL];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) make_xchunk(xc[b][i], xr[b][i]);
+
+    for (int t = 0; t < T; ++t) {
+        const int st = gw + t * TW;
+        uint4 cw[G][CPL];
+        uint32_t cs[G][CPL], cb[G][CPL];
+        bool cok[G];
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            cok[j] = ok[j];
+#pragma unroll
+            for (int i = 0; i < CPL; ++i) {
+                cw[j][i] = wv[j][i];
+                cs[j][i] = sv[j][i];
+                cb[j][i] = bv[j][i];
+            }
+        }
+        if (t + 1 < T) issue(st + TW);
+        float acc[NB][G];
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int j = 0; j < G; ++j) acc[b][j] = 0.f;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            const bool cl = li + LR * i < CPR;
+#pragma unroll
+            for (int j = 0; j < G; ++j)
+                if (cok[j] && cl) {
+#pragma unroll
+                    for (int b = 0; b < NB; ++b)
+                        acc[b][j] += chunk_dot_p(cw[j][i], xc[b][i].p, xc[b][i].corr, xc[b][i].sum, h2f(cs[j][i]),
+                                                 h2f(cb[j][i]), nu);
+                }
+        }
+        const int j = reduce4_index<LR>(lane);
+        const int row = st * RPS + j * RPG + sub;
+        const bool writer = (li % (LR / 4)) == 0 && row < rows.M;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const float v = reduce4<LR>(acc[b], lane);
+            if (writer) rows.store(b, row, v);
+            if constexpr (IsGateUp<Rows>::value) {
+                // lanes 0 / 32 hold gate rows n, n+1; lanes 16 / 48 the matching up rows
+                const float other = __shfl_xor(v, 16);
+                if ((lane & 31) == 0 && row < rows.M) {
+                    const int k = row / (2 * rows.F);
+                    const int n = (row - k * 2 * rows.F) >> 1;
+                    rows.h[k * rows.F + n] = silu_mul_h(v, other);
+                }
+            }
+        }
+    }
+}
+
+// Phase 2 of the gather MLP.  Lane li of a group of LR = F/32 lanes owns chunk
+// li of the down-projection rows of expert slot k = i*(64/LR) + lane/LR for
+// i < SLOTS, i.e. a fixed (expert, chunk) pair per slot, for every output
+// row.  h of all selected experts is prepared once per workgroup in LDS
+// (records as in affine_gemv).  A stage is R output rows: R*SLOTS chunk loads
+// per lane, issued before h is prepared for the first stage.
+template <int LR, int SLOTS>
+__global__ __launch_bounds__(kThreads) void moe_down_rows(gdsllm_affine_experts down, const int32_t* __restrict__ idx,
+                                                          const uint16_t* __restrict__ rw,
+                                                          const uint16_t* __restrict__ hbuf, int top_k,
+                                                          uint16_t* __restrict__ Y) {
+    constexpr int EPI = 64 / LR;
+    constexpr int R = SLOTS <= 4 ? 2 : 1;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int F = static_cast<int>(down.in_dim);
+    const int H = static_cast<int>(down.out_dim);
+    const int gsize = static_cast<int>(down.group_size);
+    const int CPR = F >> 5, gpr = F / gsize;
+    const int lane = threadIdx.x & 63;
+    const int li = lane % LR, sub = lane / LR;
+    const int stages = (H + R - 1) / R;
+    const int TW = gridDim.x * kWaves;
+    const int gw = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    const int T = gw < stages ? (stages - 1 - gw) / TW + 1 : 0;
+    const NibUnpack nu;
+
+    // expert slot of each lane: k, routing weight, this lane's chunk of row 0
+    int kk[SLOTS];
+    float wk[SLOTS];
+    const uint8_t* wrow[SLOTS];
+    const uint16_t *srow[SLOTS], *brow[SLOTS];
+    const int gi = (32 * li) / gsize;
+#pragma unroll
+    for (int i = 0; i < SLOTS; ++i) {
+        const int k = i * EPI + sub;
+        const int e = k < top_k ? idx[k] : -1;
+        const bool valid = e >= 0 && e < down.num_experts;
+        kk[i] = valid ? k : -1;
+        wk[i] = valid ? h2f(rw[k]) : 0.f;
+        const int64_t ee = valid ? e : 0;
+        wrow[i] = static_cast<const uint8_t*>(down.weight) + ee * down.weight_stride + 16 * li;
+        srow[i] = reinterpret_cast<const uint16_t*>(static_cast<const char*>(down.scales) + ee * down.scale_stride) + gi;
+        brow[i] = reinterpret_cast<const uint16_t*>(static_cast<const char*>(down.biases) + ee * down.bias_stride) + gi;
+    }
+    uint4 wv[R][SLOTS];
+    uint32_t sv[R][SLOTS], bv[R][SLOTS];  // raw bits: see affine_rows
+    auto issue = [&](int st) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int o = st * R + r;
+#pragma unroll
+            for (int i = 0; i < SLOTS; ++i)
+                if (kk[i] >= 0 && o < H) {
+                    wv[r][i] = load_nt16(wrow[i] + static_cast<int64_t>(o) * (F / 2));
+                    sv[r][i] = srow[i][static_cast<int64_t>(o) * gpr];
+                    bv[r][i] = brow[i][static_cast<int64_t>(o) * gpr];
+                }
+        }
+    };
+    // prepared h records [top_k][CPR]: the first kEarly items of each thread
+    // are requested before the weights (loads retire in order), the rest after
+    constexpr int kEarly = 4;
+    const int items = top_k * CPR * 4;
+    uint4 hraw[kEarly];
+#pragma unroll
+    for (int u = 0; u < kEarly; ++u) {
+        const int it = u * kThreads + threadIdx.x;
+        if (it < items) {
+            const int wq = it & 3, c = (it >> 2) % CPR, k = (it >> 2) / CPR;
+            hraw[u] = *reinterpret_cast<const uint4*>(hbuf + k * F + 32 * c + 8 * wq);
+        }
+    }
+    if (T > 0) issue(gw);
+    {
+        for (int base = 0; base < items; base += kThreads) {
+            const int it = base + threadIdx.x;
+            const bool live = it < items;
+            const int wq = it & 3, c = (it >> 2) % CPR, k = (it >> 2) / CPR;
+            float corr = 0.f, sum = 0.f;
+            uint8_t* rec = smem + (k * CPR + c) * kRec;
+            const int u = base / kThreads;
+            if (live) {
+                uint4 v;
+                if (u < kEarly) {
+                    v = hraw[0];
+#pragma unroll
+                    for (int e2 = 1; e2 < kEarly; ++e2)
+                        if (u == e2) v = hraw[e2];
+                } else {
+                    v = *reinterpret_cast<const uint4*>(hbuf + k * F + 32 * c + 8 * wq);
+                }
+                xprep_quarter(rec, wq, v, corr, sum);
+            }
+            corr += __shfl_xor(corr, 1, 4);
+            corr += __shfl_xor(corr, 2, 4);
+            sum += __shfl_xor(sum, 1, 4);
+            sum += __shfl_xor(sum, 2, 4);
+            if (live && wq == 0) {
+                *reinterpret_cast<float*>(rec + 64) = corr;
+                *reinterpret_cast<float*>(rec + 68) = sum;
+            }
+        }
+    }
+    __syncthreads();
+    if (T == 0) return;
+
+    for (int t = 0; t < T; ++t) {
+        const int st = gw + t * TW;
+        uint4 cw[R][SLOTS];
+        uint32_t cs[R][SLOTS], cb[R][SLOTS];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int i = 0; i < SLOTS; ++i) {
+                cw[r][i] = wv[r][i];
+                cs[r][i] = sv[r][i];
+                cb[r][i] = bv[r][i];
+            }
+        if (t + 1 < T) issue(st + TW);
+        float acc[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = 0.f;
+#pragma unroll
+        for (int i = 0; i < SLOTS; ++i)
+            if (kk[i] >= 0) {
+                const uint8_t* rec = smem + (kk[i] * CPR + li) * kRec;
+                uint32_t p[16];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const uint4 v = *reinterpret_cast<const uint4*>(rec + 16 * q);
+                    p[4 * q] = v.x;
+                    p[4 * q + 1] = v.y;
+                    p[4 * q + 2] = v.z;
+                    p[4 * q + 3] = v.w;
+                }
+                const float2 cs2 = *reinterpret_cast<const float2*>(rec + 64);
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+                    acc[r] = __builtin_fmaf(wk[i], chunk_dot_p(cw[r][i], p, cs2.x, cs2.y, h2f(cs[r][i]), h2f(cb[r][i]), nu),
+                                            acc[r]);
+            }
+        // sum over all 64 lanes (every expert slot and chunk); R = 2: lanes < 32 row 0
+        float v;
+        if constexpr (R == 2) {
+            const bool h32 = lane & 32;
+            v = (h32 ? acc[1] : acc[0]) + __shfl_xor(h32 ? acc[0] : acc[1], 32);
+        } else {
+            v = acc[0] + __shfl_xor(acc[0], 32);
+        }
+        v += __shfl_xor(v, 16);
+        v = lanes_sum<16>(v);
+        const int o = st * R + (R == 2 ? (lane >> 5) : 0);
+        if ((lane & 31) == 0 && (R == 2 || lane == 0) && o < H) Y[o] = f2h_bits(v);
+    }
+}
+
+template <int LR, int CPL, int NB, class Rows>
+int launch_affine_rows(const Rows& rows, const uint16_t* x, int K, int gsize, int64_t ldx, hipStream_t stream) {
+    const void* fn = reinterpret_cast<const void*>(&affine_rows<LR, CPL, NB, Rows>);
+    const int rps = 4 * (64 / LR);
+    const int stages = (rows.M + rps - 1) / rps;
+    const int need = (stages + kWaves - 1) / kWaves;
+    const int cap = blocks_per_cu(fn, 0) * cu_count();
+    const int grid = need < cap ? need : cap;
+    const bool al16 = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (ldx % 8 == 0);
+    hipLaunchKernelGGL((affine_rows<LR, CPL, NB, Rows>), dim3(grid), dim3(kThreads), 0, stream, rows, x, K, gsize, ldx,
+                       al16 ? 1 : 0);
+    return check_hip(hipGetLastError(), "affine_rows launch");
+}
+
+// Lanes per row LR and chunks per lane CPL for a row of `cpr` chunks;
+// false when the row-span kernel does not cover the shape (CPL > 4).
+bool rows_geometry(int cpr, int& lr, int& cpl) {
+    lr = lanes_per_row(cpr);
+    if (cpr < 8) return false;
+    cpl = (cpr + lr - 1) / lr;
+    return cpl <= 4;
+}
+
+template <int NB, class Rows>
+int dispatch_rows(const Rows& rows, const uint16_t* x, int K, int gsize, int64_t ldx, hipStream_t stream) {
+    int lr = 0, cpl = 0;
+    rows_geometry(K / 32, lr, cpl);
+    switch (lr * 8 + cpl) {
+        case 64 * 8 + 1: return launch_affine_rows<64, 1, NB>(rows, x, K, gsize, ldx, stream);
+        case 64 * 8 + 2: return launch_affine_rows<64, 2, NB>(rows, x, K, gsize, ldx, stream);
+        case 64 * 8 + 3: return launch_affine_rows<64, 3, NB>(rows, x, K, gsize, ldx, stream);
+        case 64 * 8 + 4: return launch_affine_rows<64, 4, NB>(rows, x, K, gsize, ldx, stream);
+        case 32 * 8 + 1: return launch_affine_rows<32, 1, NB>(rows, x, K, gsize, ldx, stream);
+        case 32 * 8 + 2: return launch_affine_rows<32, 2, NB>(rows, x, K, gsize, ldx, stream);
+        case 16 * 8 + 1: return launch_affine_rows<16, 1, NB>(rows, x, K, gsize, ldx, stream);
+        case 16 * 8 + 2: return launch_affine_rows<16, 2, NB>(rows, x, K, gsize, ldx, stream);
+        case 8 * 8 + 1: return launch_affine_rows<8, 1, NB>(rows, x, K, gsize, ldx, stream);
+        case 8 * 8 + 2: return launch_affine_rows<8, 2, NB>(rows, x, K, gsize, ldx, stream);
+        default: return set_error(GDSLLM_ERR_UNSUPPORTED, "affine_rows: no kernel for this row length");
+    }
+}
+
+template <int LR, int SLOTS>
+int launch_moe_down(const gdsllm_affine_experts& down, const int32_t* idx, const uint16_t* rw, const uint16_t* h,
+                    int top_k, uint16_t* y, hipStream_t stream) {
+    const void* fn = reinterpret_cast<const void*>(&moe_down_rows<LR, SLOTS>);
+    const size_t lds = static_cast<size_t>(top_k) * (down.in_dim / 32) * kRec;
+    if (int rc = prepare(fn, lds)) return rc;
+    constexpr int R = SLOTS <= 4 ? 2 : 1;
+    const int stages = static_cast<int>((down.out_dim + R - 1) / R);
+    const int need = (stages + kWaves - 1) / kWaves;
+    const int cap = blocks_per_cu(fn, lds) * cu_count();
+    const int grid = need < cap ? need : cap;
+    hipLaunchKernelGGL((moe_down_rows<LR, SLOTS>), dim3(grid), dim3(kThreads), lds, stream, down, idx, rw, h, top_k, y);
+    return check_hip(hipGetLastError(), "moe_down_rows launch");
+}
+
+template <int LR>
+int dispatch_moe_down_slots(int slots, const gdsllm_affine_experts& down, const int32_t* idx, const uint16_t* rw,
+                            const uint16_t* h, int top_k, uint16_t* y, hipStream_t stream) {
+    switch (slots) {
+        case 1: return launch_moe_down<LR, 1>(down, idx, rw, h, top_k, y, stream);
+        case 2: return launch_moe_down<LR, 2>(down, idx, rw, h, top_k, y, stream);
+        case 3: return launch_moe_down<LR, 3>(down, idx, rw, h, top_k, y, stream);
+        case 4: return launch_moe_down<LR, 4>(down, idx, rw, h, top_k, y, stream);
+        case 5: return launch_moe_down<LR, 5>(down, idx, rw, h, top_k, y, stream);
+        case 6: return launch_moe_down<LR, 6>(down, idx, rw, h, top_k, y, stream);
+        case 7: return launch_moe_down<LR, 7>(down, idx, rw, h, top_k, y, stream);
+        case 8: return launch_moe_down<LR, 8>(down, idx, rw, h, top_k, y, stream);
+        default: return set_error(GDSLLM_ERR_UNSUPPORTED, "moe_down_rows: too many expert slots");
+    }
+}
+
 }  // namespace
 }  // namespace gdsllm
 
@@ -444,6 +950,13 @@ extern "C" int gdsllm_fused_affine_q4_gemv(const void* weight, const void* scale
     const auto* xp = static_cast<const uint16_t*>(x);
     auto* yp = static_cast<uint16_t*>(y);
     const bool fast = (K % 32 == 0) && (g % 32 == 0) && (reinterpret_cast<uintptr_t>(weight) % 16 == 0);
+    int lr = 0, cpl = 0;
+    if (fast && batch <= 2 && rows_geometry(K / 32, lr, cpl)) {
+        PlainRows rows{static_cast<const uint32_t*>(weight), static_cast<const uint16_t*>(scales),
+                       static_cast<const uint16_t*>(biases), yp, ldy, M};
+        const int rc = batch == 1 ? dispatch_rows<1>(rows, xp, K, g, ldx, s) : dispatch_rows<2>(rows, xp, K, g, ldx, s);
+        return rc ? rc : ok();
+    }
     const size_t budget = static_cast<size_t>(max_lds_bytes());
     if (fast && static_cast<size_t>(K / 32) * kRec <= budget) {
         int64_t b0 = 0;
@@ -474,7 +987,8 @@ extern "C" int gdsllm_fused_affine_q4_gemv(const void* weight, const void* scale
 
 extern "C" size_t gdsllm_moe_gather_workspace_size(int64_t top_k, int64_t ffn_dim) {
     if (top_k <= 0 || ffn_dim <= 0) return 256;
-    const size_t bytes = static_cast<size_t>(top_k) * 2 * static_cast<size_t>(ffn_dim) * 2;
+    // fp16 gate/up outputs [top_k][2][F], then h [top_k][F]
+    const size_t bytes = static_cast<size_t>(top_k) * 3 * static_cast<size_t>(ffn_dim) * 2;
     return (bytes + 255) / 256 * 256;
 }
 
@@ -534,8 +1048,38 @@ extern "C" int gdsllm_moe_gather_affine_q4(const gdsllm_affine_experts* gate, co
         return set_error(GDSLLM_ERR_UNSUPPORTED, n + ": hidden or top_k*ffn too large for LDS staging");
     hipStream_t s = as_stream(stream);
     auto* gu = static_cast<uint16_t*>(workspace);
-    GateUpRows rows{*gate, *up, idx, gu, static_cast<int>(F), static_cast<int>(2 * top_k * F)};
     const auto* xp = static_cast<const uint16_t*>(x);
+    // Row-span path: hidden a multiple of 2048 up to 8192 (64 lanes per gate/up
+    // row, <= 4 chunks each), ffn/32 in {16, 32, 64} lanes per down row and at
+    // most 8 expert slots per lane.  Phase 1 writes g, u and h for every
+    // selected slot (0 for an expert index out of range, which phase 2 skips),
+    // so the workspace needs no clearing.
+    const int cpr_h = static_cast<int>(H / 32), cpr_f = static_cast<int>(F / 32);
+    const int slots = (cpr_f >= 16 && cpr_f <= 64) ? static_cast<int>((top_k + 64 / cpr_f - 1) / (64 / cpr_f)) : 0;
+    const bool rows_path = H % 2048 == 0 && H <= 8192 && (cpr_f == 16 || cpr_f == 32 || cpr_f == 64) && slots >= 1 &&
+                           slots <= 8 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
+    if (rows_path) {
+        uint16_t* h = gu + top_k * 2 * F;
+        GateUpPairs pairs{*gate, *up, idx, gu, h, static_cast<int>(F), static_cast<int>(2 * top_k * F)};
+        int rc;
+        switch (cpr_h / 64) {
+            case 1: rc = launch_affine_rows<64, 1, 1>(pairs, xp, static_cast<int>(H), static_cast<int>(gate->group_size), H, s); break;
+            case 2: rc = launch_affine_rows<64, 2, 1>(pairs, xp, static_cast<int>(H), static_cast<int>(gate->group_size), H, s); break;
+            case 3: rc = launch_affine_rows<64, 3, 1>(pairs, xp, static_cast<int>(H), static_cast<int>(gate->group_size), H, s); break;
+            default: rc = launch_affine_rows<64, 4, 1>(pairs, xp, static_cast<int>(H), static_cast<int>(gate->group_size), H, s); break;
+        }
+        if (rc) return rc;
+        const auto* wp = static_cast<const uint16_t*>(routing_weights);
+        auto* yp = static_cast<uint16_t*>(y);
+        const int tk = static_cast<int>(top_k);
+        switch (cpr_f) {
+            case 16: rc = dispatch_moe_down_slots<16>(slots, *down, idx, wp, h, tk, yp, s); break;
+            case 32: rc = dispatch_moe_down_slots<32>(slots, *down, idx, wp, h, tk, yp, s); break;
+            default: rc = dispatch_moe_down_slots<64>(slots, *down, idx, wp, h, tk, yp, s); break;
+        }
+        return rc ? rc : ok();
+    }
+    GateUpRows rows{*gate, *up, idx, gu, static_cast<int>(F), static_cast<int>(2 * top_k * F)};
     // Phase 1 writes every gate/up row (0 for an expert index out of range,
     // which phase 2 then skips), so the workspace needs no clearing.
     if (int rc = dispatch_lr<1>(rows, xp, static_cast<int>(H), static_cast<int>(gate->group_size), H, s)) return rc;

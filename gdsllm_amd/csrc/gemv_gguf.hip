@@ -391,37 +391,48 @@ __device__ __forceinline__ float permute_block(const uint32_t (&r)[16], uint32_t
 }
 
 // The workgroup writes the prepared spans of every window for NB batch rows:
-// record (b, w, c) at xp + ((b*NW + w)*64 + c)*kSpanRec.  One item = one block.
+// record (b, w, c) at xp + ((b*NW + w)*64 + c)*kSpanRec.  One item = one block
+// (32 fp16 of one batch row).
+__device__ __forceinline__ void load_block_raw(uint32_t (&r)[16], const uint16_t* __restrict__ src, bool al16) {
+    if (al16) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint4 v = *reinterpret_cast<const uint4*>(src + 8 * k);
+            r[4 * k] = v.x;
+            r[4 * k + 1] = v.y;
+            r[4 * k + 2] = v.z;
+            r[4 * k + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) r[i] = static_cast<uint32_t>(src[2 * i]) | (static_cast<uint32_t>(src[2 * i + 1]) << 16);
+    }
+}
+
+template <Fmt F>
+__device__ __forceinline__ void store_span_block(uint8_t* xp, const uint32_t (&r)[16], int g, int b, int NW) {
+    uint32_t pr[16];
+    const float c = permute_block<F>(r, pr);
+    const int w = g / kWinBlocks, cb = g % kWinBlocks;
+    uint8_t* rec = xp + ((b * NW + w) * 64 + (cb >> 1)) * kSpanRec;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        *reinterpret_cast<uint4*>(rec + 64 * (cb & 1) + 16 * k) = make_uint4(pr[4 * k], pr[4 * k + 1], pr[4 * k + 2], pr[4 * k + 3]);
+    *reinterpret_cast<float*>(rec + 128 + 4 * (cb & 1)) = c;
+}
+
+// Items after each thread's first one (rows longer than one window of blocks
+// per thread); the first item is handled by the caller around the weight loads.
 template <Fmt F, int NB>
-__device__ void build_spans(uint8_t* xp, const uint16_t* __restrict__ X, int64_t ldx, int K, int NW, bool al16) {
+__device__ void build_spans_rest(uint8_t* xp, const uint16_t* __restrict__ X, int64_t ldx, int K, int NW, bool al16) {
     const int nblk = K >> 5;
     const int per_row = NW * kWinBlocks;
-    for (int it = threadIdx.x; it < NB * per_row; it += kWaves * 64) {
+    for (int it = threadIdx.x + kWaves * 64; it < NB * per_row; it += kWaves * 64) {
         const int g = it % per_row, b = it / per_row;
         if (g >= nblk) continue;  // past the end of the row: its lanes never compute
-        const uint16_t* src = X + b * ldx + 32 * g;
         uint32_t r[16];
-        if (al16) {
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const uint4 v = *reinterpret_cast<const uint4*>(src + 8 * k);
-                r[4 * k] = v.x;
-                r[4 * k + 1] = v.y;
-                r[4 * k + 2] = v.z;
-                r[4 * k + 3] = v.w;
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) r[i] = static_cast<uint32_t>(src[2 * i]) | (static_cast<uint32_t>(src[2 * i + 1]) << 16);
-        }
-        uint32_t pr[16];
-        const float c = permute_block<F>(r, pr);
-        const int w = g / kWinBlocks, cb = g % kWinBlocks;
-        uint8_t* rec = xp + ((b * NW + w) * 64 + (cb >> 1)) * kSpanRec;
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-            *reinterpret_cast<uint4*>(rec + 64 * (cb & 1) + 16 * k) = make_uint4(pr[4 * k], pr[4 * k + 1], pr[4 * k + 2], pr[4 * k + 3]);
-        *reinterpret_cast<float*>(rec + 128 + 4 * (cb & 1)) = c;
+        load_block_raw(r, X + b * ldx + 32 * g, al16);
+        store_span_block<F>(xp, r, g, b, NW);
     }
 }
 
@@ -569,11 +580,18 @@ __global__ __launch_bounds__(kWaves * 64) void gguf_gemv_rows(const uint8_t* __r
         goff[j] = rl * row_bytes + 16 * (c - rl * kSegChunks);
     }
 
-    // The first stage's weights are requested before x is prepared, so their
-    // HBM latency covers the x loads and the barrier.
+    // x for this thread's first span block is requested first, then the first
+    // stage's weights; loads retire in order, so preparing x waits only for x
+    // and overlaps the weights' HBM latency, as does the barrier.
+    const int per_row = NW * kWinBlocks;
+    const int g0 = threadIdx.x % per_row, b0 = threadIdx.x / per_row;
+    const bool has0 = b0 < NB && g0 < (K >> 5);
+    uint32_t xr[16];
+    if (has0) load_block_raw(xr, X + b0 * ldx + 32 * g0, x_al16 != 0);
     uint4 pre[L::kSbChunks];
     if (T > 0) rows_load<F>(pre, W, row_bytes, goff, make_stage<F>(gw, 0, M, S), lane);
-    build_spans<F, NB>(xp, X, ldx, K, NW, x_al16 != 0);
+    if (has0) store_span_block<F>(xp, xr, g0, b0, NW);
+    build_spans_rest<F, NB>(xp, X, ldx, K, NW, x_al16 != 0);
     __syncthreads();
     if (T == 0) return;
 

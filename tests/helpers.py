@@ -91,8 +91,22 @@ def moe_gather(gate, up, down, x_dev, idx_dev, w_dev, group_size, return_workspa
                                              ptr(w_dev), top_k, ptr(y), ptr(ws), ws_bytes, stream()))
     torch.cuda.synchronize()
     if return_workspace:
-        return y, ws[: top_k * 2 * g.out_dim * 2].view(torch.float16).view(top_k, 2, g.out_dim)
+        F = g.out_dim
+        gu = ws[: top_k * 2 * F * 2].view(torch.float16).view(top_k, 2, F)
+        h = ws[top_k * 2 * F * 2: top_k * 3 * F * 2].view(torch.float16).view(top_k, F) if writes_h(g, top_k) else None
+        return y, gu, h
     return y
+
+
+def writes_h(gate: AffineExperts, top_k: int) -> bool:
+    """Whether the gather takes its row-span path, which also stores h = fp16(fp16(silu(g)) * u)
+    after the gate/up outputs in the workspace (hidden % 2048 == 0 and <= 8192, ffn/32 in {16, 32, 64},
+    at most 8 expert slots per lane)."""
+    H, F = gate.in_dim, gate.out_dim
+    cpr = F // 32
+    if H % 2048 or H > 8192 or cpr not in (16, 32, 64):
+        return False
+    return -(-top_k // (64 // cpr)) <= 8
 
 
 def affine_dequant_np(words: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, group_size: int) -> np.ndarray:
@@ -127,5 +141,5 @@ def double_rounding_cases(n: int, seed: int):
 
 __all__ = [
     "gen", "stream", "ptr", "to_np", "on_gpu", "assert_gemv_close", "gguf_gemv", "affine_gemv", "moe_gather",
-    "experts_struct", "affine_dequant_np", "double_rounding_cases", "syn", "oq", "capi", "check",
+    "experts_struct", "writes_h", "affine_dequant_np", "double_rounding_cases", "syn", "oq", "capi", "check",
 ]

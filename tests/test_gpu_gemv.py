@@ -106,12 +106,14 @@ def test_gguf_gemv_closed_forms(gpu):
 
 
 AFFINE_SHAPES = [(1024, 4096, 64), (4096, 1024, 64), (64, 4096, 128), (33, 256, 32), (7, 2048, 64), (5, 96, 32),
+                 # row-span geometries: 3 / 4 chunks per lane, 16 lanes per row, partial last chunk column
+                 (21, 6144, 64), (10, 8192, 128), (19, 512, 32), (13, 3072, 64), (6, 1536, 32),
                  # generic path: in_dim % 32 != 0 or group_size % 32 != 0
                  (9, 104, 8), (6, 128, 16)]
 
 
 @pytest.mark.parametrize("M,K,g", AFFINE_SHAPES, ids=[f"{m}x{k}g{g}" for m, k, g in AFFINE_SHAPES])
-@pytest.mark.parametrize("B", [1, 3, 8])
+@pytest.mark.parametrize("B", [1, 2, 3, 8])
 def test_affine_gemv(gpu, M, K, g, B):
     w, s, b = syn.affine_q4_weights([M, K], g, gen(3000 + M + K + g))
     x = syn.activations(B, K, gen(3001 + B))

@@ -27,16 +27,18 @@ def _expert_fn(pool, g, E):
     return f
 
 
-def _check_moe(y, ws, gate, up, down, x, idx, wts, g, E):
+def _check_moe(y, ws, gate, up, down, x, idx, wts, g, E, hk=None):
     """Three checks.  (1) phase 1: the fp16 gate/up rows in the workspace match
-    the oracle GEMVs under the GEMV tolerance.  (2) phase 2: y matches the
-    oracle's weighted down-projection of h = fp16(fp16(silu(g)) * u) built from
-    the kernel's own fp16 g/u, under the GEMV tolerance.  (3) end to end: y
-    matches the all-oracle result in relative L2 (one-ulp fp16 differences in
-    g/u move h, so the per-row bound is not applied end to end)."""
+    the oracle GEMVs under the GEMV tolerance, and h (when the kernel stores it)
+    is within one fp16 ulp of fp16(fp16(silu(g)) * u) built from those rows.
+    (2) phase 2: y matches the oracle's weighted down-projection of the
+    kernel's h (or of h built from its g/u), under the GEMV tolerance.  (3) end
+    to end: y matches the all-oracle result in relative L2 (one-ulp fp16
+    differences in g/u move h, so the per-row bound is not applied end to end)."""
     xn = to_np(x).reshape(-1)
     gf, uf, dn = _expert_fn(gate, g, E), _expert_fn(up, g, E), _expert_fn(down, g, E)
     wsn = to_np(ws)
+    hkn = to_np(hk) if hk is not None else None
     for k, e in enumerate(idx):
         e = int(e)
         if gf(e) is None:
@@ -51,6 +53,18 @@ def _check_moe(y, ws, gate, up, down, x, idx, wts, g, E):
         if gf(e) is None:
             continue
         h = (oq.silu_fp16(wsn[k, 0]).astype(np.float32) * wsn[k, 1].astype(np.float32)).astype(np.float16)
+        if hkn is not None:
+            # expf on the GPU and numpy's exp may round fp32 exp(-g) differently, which
+            # can move fp16(silu(g)) by one ulp; h = fp16(silu * u) then moves by up to
+            # that ulp times |u| plus its own rounding step
+            sg = oq.silu_fp16(wsn[k, 0])
+            bound = oq.fp16_ulp(sg) * np.abs(wsn[k, 1].astype(np.float64)) + oq.fp16_ulp(h)
+            bad = np.abs(hkn[k].astype(np.float64) - h.astype(np.float64)) > bound
+            if bad.any():
+                i = int(np.argmax(bad))
+                raise AssertionError(f"h k={k}: {int(bad.sum())} of {bad.size} differ; first n={i}: kernel {hkn[k][i]} "
+                                     f"expected {h[i]} from g={wsn[k, 0][i]} u={wsn[k, 1][i]}; bad n: {np.nonzero(bad)[0][:16]}")
+            h = hkn[k]
         wk = float(np.float16(to_np(wts)[k]))
         part = oq.gemv(dn(e), h)[0] * wk
         ref2 = part if ref2 is None else ref2 + part
@@ -65,26 +79,36 @@ def _check_moe(y, ws, gate, up, down, x, idx, wts, g, E):
     return rel2, mx2
 
 
-@pytest.mark.parametrize("E,H,F,g,top_k", [(16, 4096, 1024, 64, 10), (8, 512, 256, 32, 3), (12, 1024, 512, 128, 1)])
+MOE_CASES = [
+    # row-span path: 64 lanes per gate/up row (1-4 chunks each), 16/32/64 lanes per down row, 1-8 slots
+    (16, 4096, 1024, 64, 10), (6, 2048, 512, 64, 5), (10, 8192, 2048, 128, 8), (8, 6144, 1024, 32, 3),
+    (20, 2048, 1024, 64, 16), (4, 2048, 512, 32, 1),
+    # general path
+    (8, 512, 256, 32, 3), (12, 1024, 512, 128, 1), (6, 2048, 256, 64, 4),
+]
+
+
+@pytest.mark.parametrize("E,H,F,g,top_k", MOE_CASES, ids=[f"E{e}_H{h}_F{f}_g{g}_k{k}" for e, h, f, g, k in MOE_CASES])
 def test_moe_gather(gpu, E, H, F, g, top_k):
     gate, up, down = _moe_pool(E, H, F, g, 4000 + E + top_k)
     x = syn.activations(1, H, gen(4100 + E))
     idx = torch.randperm(E, generator=gen(4200 + E))[:top_k].to(torch.int32)
     wts = torch.softmax(torch.randn(top_k, generator=gen(4300)), 0).to(torch.float16)
-    y, ws = moe_gather(tuple(t.to(gpu) for t in gate), tuple(t.to(gpu) for t in up),
-                       tuple(t.to(gpu) for t in down), x.to(gpu), idx.to(gpu), wts.to(gpu), g, return_workspace=True)
-    _check_moe(y, ws, gate, up, down, x, to_np(idx), wts, g, E)
+    y, ws, hk = moe_gather(tuple(t.to(gpu) for t in gate), tuple(t.to(gpu) for t in up),
+                           tuple(t.to(gpu) for t in down), x.to(gpu), idx.to(gpu), wts.to(gpu), g, return_workspace=True)
+    _check_moe(y, ws, gate, up, down, x, to_np(idx), wts, g, E, hk)
 
 
-def test_moe_gather_skips_out_of_range_experts(gpu):
-    E, H, F, g = 6, 512, 256, 64
+@pytest.mark.parametrize("H,F", [(512, 256), (2048, 1024)], ids=["general", "rows"])
+def test_moe_gather_skips_out_of_range_experts(gpu, H, F):
+    E, g = 6, 64
     gate, up, down = _moe_pool(E, H, F, g, 77)
     x = syn.activations(1, H, gen(78))
     idx = torch.tensor([2, -1, 5, 6, 0], dtype=torch.int32)
     wts = torch.tensor([0.3, 0.2, 0.2, 0.2, 0.1], dtype=torch.float16)
-    y, ws = moe_gather(tuple(t.to(gpu) for t in gate), tuple(t.to(gpu) for t in up),
-                       tuple(t.to(gpu) for t in down), x.to(gpu), idx.to(gpu), wts.to(gpu), g, return_workspace=True)
-    _check_moe(y, ws, gate, up, down, x, to_np(idx), wts, g, E)
+    y, ws, hk = moe_gather(tuple(t.to(gpu) for t in gate), tuple(t.to(gpu) for t in up),
+                           tuple(t.to(gpu) for t in down), x.to(gpu), idx.to(gpu), wts.to(gpu), g, return_workspace=True)
+    _check_moe(y, ws, gate, up, down, x, to_np(idx), wts, g, E, hk)
 
 
 def test_moe_gather_cfg2_full_pool(gpu):
@@ -94,11 +118,12 @@ def test_moe_gather_cfg2_full_pool(gpu):
     x = syn.activations(1, H, gen(1003))
     idx = torch.randperm(E, generator=gen(1004))[:top_k].to(torch.int32)
     wts = torch.softmax(torch.randn(top_k, generator=gen(1005)), 0).to(torch.float16)
-    y, ws = moe_gather(gate, up, down, x.to(gpu), idx.to(gpu), wts.to(gpu), g, return_workspace=True)
+    y, ws, hk = moe_gather(gate, up, down, x.to(gpu), idx.to(gpu), wts.to(gpu), g, return_workspace=True)
     sel = sorted(set(int(e) for e in idx))
     remap = {e: i for i, e in enumerate(sel)}
     small = [tuple(t[sel].cpu() for t in pool) for pool in (gate, up, down)]
-    _check_moe(y, ws, *small, x, np.array([remap[int(e)] for e in idx]), wts, g, len(sel))
+    assert hk is not None, "the 512-expert shape must take the row-span path"
+    _check_moe(y, ws, *small, x, np.array([remap[int(e)] for e in idx]), wts, g, len(sel), hk)
     del gate, up, down
     torch.cuda.empty_cache()
 

@@ -334,14 +334,14 @@ __global__ __launch_bounds__(kThreads) void moe_down(gdsllm_affine_experts down,
     }
 }
 
-int blocks_per_cu(const void* fn, size_t lds) {
+int blocks_per_cu(const void* fn, size_t lds, int threads = kThreads) {
     static std::mutex mu;
     static std::vector<std::pair<std::pair<const void*, size_t>, int>> cache;
     std::lock_guard<std::mutex> lock(mu);
     for (auto& e : cache)
         if (e.first.first == fn && e.first.second == lds) return e.second;
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kThreads, lds) != hipSuccess || n <= 0) n = 1;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, threads, lds) != hipSuccess || n <= 0) n = 1;
     cache.push_back({{fn, lds}, n});
     return n;
 }
@@ -693,8 +693,8 @@ __global__ __launch_bounds__(kThreads) void affine_rows(Rows rows, const uint16_
 // row.  h of all selected experts is prepared once per workgroup in LDS
 // (records as in affine_gemv).  A stage is R output rows: R*SLOTS chunk loads
 // per lane, issued before h is prepared for the first stage.
-template <int LR, int SLOTS>
-__global__ __launch_bounds__(kThreads) void moe_down_rows(gdsllm_affine_experts down, const int32_t* __restrict__ idx,
+template <int LR, int SLOTS, int NT>
+__global__ __launch_bounds__(NT) void moe_down_rows(gdsllm_affine_experts down, const int32_t* __restrict__ idx,
                                                           const uint16_t* __restrict__ rw,
                                                           const uint16_t* __restrict__ hbuf, int top_k,
                                                           uint16_t* __restrict__ Y) {
@@ -707,11 +707,35 @@ __global__ __launch_bounds__(kThreads) void moe_down_rows(gdsllm_affine_experts 
     const int CPR = F >> 5, gpr = F / gsize;
     const int lane = threadIdx.x & 63;
     const int li = lane % LR, sub = lane / LR;
+    constexpr int NWV = NT / 64;  // waves per workgroup
     const int stages = (H + R - 1) / R;
-    const int TW = gridDim.x * kWaves;
-    const int gw = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    const int TW = gridDim.x * NWV;
+    const int gw = blockIdx.x * NWV + (threadIdx.x >> 6);
     const int T = gw < stages ? (stages - 1 - gw) / TW + 1 : 0;
     const NibUnpack nu;
+
+    // Request order: expert indices and routing weights, then this thread's
+    // first h items, then (once the indices are in) the first stage's weights;
+    // loads retire in order, so each consumer waits only for what it needs.
+    int eraw[SLOTS];
+    uint32_t wraw[SLOTS];
+#pragma unroll
+    for (int i = 0; i < SLOTS; ++i) {
+        const int k = i * EPI + sub;
+        eraw[i] = k < top_k ? idx[k] : -1;
+        wraw[i] = k < top_k ? rw[k] : 0u;
+    }
+    constexpr int kEarly = 2;
+    const int items = top_k * CPR * 4;
+    uint4 hraw[kEarly];
+#pragma unroll
+    for (int u = 0; u < kEarly; ++u) {
+        const int it = u * NT + threadIdx.x;
+        if (it < items) {
+            const int wq = it & 3, c = (it >> 2) % CPR, k = (it >> 2) / CPR;
+            hraw[u] = *reinterpret_cast<const uint4*>(hbuf + k * F + 32 * c + 8 * wq);
+        }
+    }
 
     // expert slot of each lane: k, routing weight, this lane's chunk of row 0
     int kk[SLOTS];
@@ -722,10 +746,10 @@ __global__ __launch_bounds__(kThreads) void moe_down_rows(gdsllm_affine_experts 
 #pragma unroll
     for (int i = 0; i < SLOTS; ++i) {
         const int k = i * EPI + sub;
-        const int e = k < top_k ? idx[k] : -1;
+        const int e = eraw[i];
         const bool valid = e >= 0 && e < down.num_experts;
         kk[i] = valid ? k : -1;
-        wk[i] = valid ? h2f(rw[k]) : 0.f;
+        wk[i] = valid ? h2f(wraw[i]) : 0.f;
         const int64_t ee = valid ? e : 0;
         wrow[i] = static_cast<const uint8_t*>(down.weight) + ee * down.weight_stride + 16 * li;
         srow[i] = reinterpret_cast<const uint16_t*>(static_cast<const char*>(down.scales) + ee * down.scale_stride) + gi;
@@ -746,28 +770,16 @@ __global__ __launch_bounds__(kThreads) void moe_down_rows(gdsllm_affine_experts 
                 }
         }
     };
-    // prepared h records [top_k][CPR]: the first kEarly items of each thread
-    // are requested before the weights (loads retire in order), the rest after
-    constexpr int kEarly = 4;
-    const int items = top_k * CPR * 4;
-    uint4 hraw[kEarly];
-#pragma unroll
-    for (int u = 0; u < kEarly; ++u) {
-        const int it = u * kThreads + threadIdx.x;
-        if (it < items) {
-            const int wq = it & 3, c = (it >> 2) % CPR, k = (it >> 2) / CPR;
-            hraw[u] = *reinterpret_cast<const uint4*>(hbuf + k * F + 32 * c + 8 * wq);
-        }
-    }
     if (T > 0) issue(gw);
+    // prepared h records [top_k][CPR], one quarter (8 elements) per item
     {
-        for (int base = 0; base < items; base += kThreads) {
+        for (int base = 0; base < items; base += NT) {
             const int it = base + threadIdx.x;
             const bool live = it < items;
             const int wq = it & 3, c = (it >> 2) % CPR, k = (it >> 2) / CPR;
             float corr = 0.f, sum = 0.f;
             uint8_t* rec = smem + (k * CPR + c) * kRec;
-            const int u = base / kThreads;
+            const int u = base / NT;
             if (live) {
                 uint4 v;
                 if (u < kEarly) {
@@ -885,18 +897,22 @@ int dispatch_rows(const Rows& rows, const uint16_t* x, int K, int gsize, int64_t
     }
 }
 
+// Workgroups of 16 waves (8 where 128 registers per lane would spill): every
+// workgroup prepares all of h in LDS, so fewer, larger workgroups prepare it
+// fewer times.
 template <int LR, int SLOTS>
 int launch_moe_down(const gdsllm_affine_experts& down, const int32_t* idx, const uint16_t* rw, const uint16_t* h,
                     int top_k, uint16_t* y, hipStream_t stream) {
-    const void* fn = reinterpret_cast<const void*>(&moe_down_rows<LR, SLOTS>);
+    constexpr int NT = (SLOTS <= 3 || SLOTS == 5) ? 1024 : 512;
+    const void* fn = reinterpret_cast<const void*>(&moe_down_rows<LR, SLOTS, NT>);
     const size_t lds = static_cast<size_t>(top_k) * (down.in_dim / 32) * kRec;
     if (int rc = prepare(fn, lds)) return rc;
     constexpr int R = SLOTS <= 4 ? 2 : 1;
     const int stages = static_cast<int>((down.out_dim + R - 1) / R);
-    const int need = (stages + kWaves - 1) / kWaves;
-    const int cap = blocks_per_cu(fn, lds) * cu_count();
+    const int need = (stages + NT / 64 - 1) / (NT / 64);
+    const int cap = blocks_per_cu(fn, lds, NT) * cu_count();
     const int grid = need < cap ? need : cap;
-    hipLaunchKernelGGL((moe_down_rows<LR, SLOTS>), dim3(grid), dim3(kThreads), lds, stream, down, idx, rw, h, top_k, y);
+    hipLaunchKernelGGL((moe_down_rows<LR, SLOTS, NT>), dim3(grid), dim3(NT), lds, stream, down, idx, rw, h, top_k, y);
     return check_hip(hipGetLastError(), "moe_down_rows launch");
 }
 

@@ -673,6 +673,235 @@ __global__ __launch_bounds__(kWaves * 64) void gguf_gemv_rows(const uint8_t* __r
     }
 }
 
+// ---- MFMA batched GEMV (batch 3..16) ---------------------------------------------
+// With B >= 3 rows of x every weight feeds B dot products and the dot2 path is
+// VALU-bound.  Here the weights are dequantized in registers to exactly the
+// fp16 values the reference's dequant produces ((q - 8) and q are exact in
+// packed fp16, the packed multiply by d rounds once) and enter
+// v_mfma_f32_16x16x32_f16 as A = 16 rows x one 32-weight block; x of up to 16
+// batch rows is B, permuted into the same element order.  Lane group g
+// (lanes 16g..16g+15) covers qs dword g of each block: for Q4_0 the elements
+// 4g..4g+3 (low nibbles) and 16+4g..19+4g (high nibbles), for Q8_0 the
+// elements 8g..8g+7; the MFMA sum over k is order-free, so A and B only have
+// to agree.
+//
+// A wave's stage is 32 rows (2 MFMA row tiles) x 2 super-blocks = 16 blocks:
+// 9216 B (Q4_0) / 17408 B (Q8_0), fetched with coalesced 16-byte loads into a
+// per-wave LDS slot where row r occupies bytes [r*S2, r*S2+S2) (S2 = two
+// super-blocks), i.e. chunk c lands at 16c.  The workgroup's waves split K
+// over the same 32 rows; their partial tiles are summed through LDS.  Each
+// stage's x is requested before the next stage's weights are prefetched, so
+// waiting for x never waits for the prefetch (loads retire in order).
+
+constexpr int kMfmaRows = 32;    // rows per stage (2 tiles of 16)
+constexpr int kMfmaSbs = 2;      // super-blocks per stage
+constexpr int kMfmaWaves = 4;    // waves per workgroup (K split)
+constexpr int kMfmaBlocks = 8 * kMfmaSbs;
+
+template <Fmt F>
+constexpr int mfma_stage_bytes() { return kMfmaRows * kMfmaSbs * Layout<F>::kSbBytes; }
+template <Fmt F>
+constexpr int mfma_chunks_per_lane() { return kMfmaRows * kMfmaSbs * Layout<F>::kSbChunks / 64; }
+
+// B operand (4 dwords) of block `gb` for lane group g and batch row b, from raw x.
+template <Fmt F>
+__device__ __forceinline__ void load_x_b(uint32_t (&r)[4], const uint16_t* __restrict__ xb, int gb, int g) {
+    if constexpr (F == Fmt::Q4_0) {
+        const uint2 lo = *reinterpret_cast<const uint2*>(xb + 32 * gb + 4 * g);
+        const uint2 hi = *reinterpret_cast<const uint2*>(xb + 32 * gb + 16 + 4 * g);
+        r[0] = lo.x; r[1] = lo.y; r[2] = hi.x; r[3] = hi.y;
+    } else {
+        const uint4 v = *reinterpret_cast<const uint4*>(xb + 32 * gb + 8 * g);
+        r[0] = v.x; r[1] = v.y; r[2] = v.z; r[3] = v.w;
+    }
+}
+
+template <Fmt F>
+__device__ __forceinline__ half8_t x_b_operand(const uint32_t (&r)[4]) {
+    uint32_t p[4];
+    if constexpr (F == Fmt::Q4_0) {
+        // (x4g, x4g+2) (x16+4g, x18+4g) (x4g+1, x4g+3) (x17+4g, x19+4g)
+        p[0] = __builtin_amdgcn_perm(r[1], r[0], kSelLo);
+        p[1] = __builtin_amdgcn_perm(r[3], r[2], kSelLo);
+        p[2] = __builtin_amdgcn_perm(r[1], r[0], kSelHi);
+        p[3] = __builtin_amdgcn_perm(r[3], r[2], kSelHi);
+    } else {
+        // (x0, x2) (x1, x3) (x4, x6) (x5, x7) of elements 8g..8g+7
+        p[0] = __builtin_amdgcn_perm(r[1], r[0], kSelLo);
+        p[1] = __builtin_amdgcn_perm(r[1], r[0], kSelHi);
+        p[2] = __builtin_amdgcn_perm(r[3], r[2], kSelLo);
+        p[3] = __builtin_amdgcn_perm(r[3], r[2], kSelHi);
+    }
+    return __builtin_bit_cast(half8_t, make_uint4(p[0], p[1], p[2], p[3]));
+}
+
+// A operand of block j (0..15) of the stage row at `row` (LDS, 4-byte aligned
+// row start) for lane group g: bit-exact fp16 weights in x_b_operand's order.
+template <Fmt F, int J>
+__device__ __forceinline__ half8_t weight_a_operand(const uint32_t* row, int g, const NibUnpack& nu) {
+    using L = Layout<F>;
+    constexpr int kPairDw = L::kBlockBytes / 2;  // dwords of a block pair (9 / 17)
+    constexpr int P = J / 2;
+    const uint32_t* pr = row + kPairDw * P;
+    uint32_t dbits;
+    half2_t h[4];
+    if constexpr (F == Fmt::Q4_0) {
+        uint32_t q;
+        if constexpr (J % 2 == 0) {
+            dbits = pr[0] & 0xFFFFu;
+            q = align2(pr[g], pr[g + 1]);
+        } else {
+            dbits = pr[4] >> 16;
+            q = pr[5 + g];
+        }
+        const half2_t lo_off = {static_cast<half_t>(-1032.0f), static_cast<half_t>(-1032.0f)};
+        const half2_t hi_off = {static_cast<half_t>(-72.0f), static_cast<half_t>(-72.0f)};
+        const uint32_t qs = q >> 8;
+        h[0] = __builtin_bit_cast(half2_t, nu.lo(q)) + lo_off;
+        h[1] = __builtin_bit_cast(half2_t, nu.hi(q)) + hi_off;
+        h[2] = __builtin_bit_cast(half2_t, nu.lo(qs)) + lo_off;
+        h[3] = __builtin_bit_cast(half2_t, nu.hi(qs)) + hi_off;
+    } else {
+        uint32_t q0, q1;
+        if constexpr (J % 2 == 0) {
+            dbits = pr[0] & 0xFFFFu;
+            q0 = align2(pr[2 * g], pr[2 * g + 1]);
+            q1 = align2(pr[2 * g + 1], pr[2 * g + 2]);
+        } else {
+            dbits = pr[8] >> 16;
+            q0 = pr[9 + 2 * g];
+            q1 = pr[10 + 2 * g];
+        }
+        const half2_t off = {static_cast<half_t>(-1152.0f), static_cast<half_t>(-1152.0f)};
+        const uint32_t u0 = q0 ^ 0x80808080u, u1 = q1 ^ 0x80808080u;
+        h[0] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, u0, 0x04020400u)) + off;
+        h[1] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, u0, 0x04030401u)) + off;
+        h[2] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, u1, 0x04020400u)) + off;
+        h[3] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, u1, 0x04030401u)) + off;
+    }
+    const half_t d = __builtin_bit_cast(half_t, static_cast<uint16_t>(dbits));
+    const half2_t dd = {d, d};
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = __builtin_bit_cast(uint32_t, h[i] * dd);
+    return __builtin_bit_cast(half8_t, make_uint4(w[0], w[1], w[2], w[3]));
+}
+
+template <Fmt F>
+__global__ __launch_bounds__(kMfmaWaves * 64) void gguf_gemv_mfma(const uint8_t* __restrict__ W,
+                                                                  const uint16_t* __restrict__ X,
+                                                                  uint16_t* __restrict__ Y, int M, int K, int nb,
+                                                                  int64_t ldx, int64_t ldy) {
+    using L = Layout<F>;
+    constexpr int CPL = mfma_chunks_per_lane<F>();
+    constexpr int kRowChunks = kMfmaSbs * L::kSbChunks;  // chunks of one stage row
+    constexpr int kRowDw = kMfmaSbs * L::kSbBytes / 4;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    uint8_t* stage = smem + wave * mfma_stage_bytes<F>();
+    const int S = K >> 8;                       // super-blocks per row
+    const int NS = (S + kMfmaSbs - 1) / kMfmaSbs;  // stages along K
+    const uint32_t row_bytes = static_cast<uint32_t>(S) * L::kSbBytes;
+    const int r0 = blockIdx.x * kMfmaRows;
+    const int nrows = min(kMfmaRows, M - r0);
+    // this wave's stages: [s_begin, s_end) of the row group's NS
+    const int s_begin = wave * NS / kMfmaWaves, s_end = (wave + 1) * NS / kMfmaWaves;
+    const NibUnpack nu;
+    const int g = lane >> 4, bcol = lane & 15;
+    const bool xlane = bcol < nb;
+    const uint16_t* xrow = X + (xlane ? bcol : 0) * ldx;
+
+    // chunk j of this lane: stage row rl = c / kRowChunks, byte offset goff
+    uint32_t goff[CPL];
+    int rl[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const int c = 64 * j + lane;
+        rl[j] = c / kRowChunks;
+        goff[j] = rl[j] * row_bytes + 16 * (c - rl[j] * kRowChunks);
+    }
+    // A stage s covers super-blocks [2s, 2s+2); the last one may be half (odd S).
+    auto load = [&](uint4 (&pre)[CPL], int s) {
+        const uint8_t* base = W + static_cast<int64_t>(r0) * row_bytes + s * kMfmaSbs * L::kSbBytes;
+        const int nsb = min(kMfmaSbs, S - s * kMfmaSbs);
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const int c = 64 * j + lane;
+            if (rl[j] < nrows && (c - rl[j] * kRowChunks) < nsb * L::kSbChunks) pre[j] = load_nt16(base + goff[j]);
+        }
+    };
+    float4_t acc[2];
+    acc[0] = float4_t{0.f, 0.f, 0.f, 0.f};
+    acc[1] = acc[0];
+    uint4 pre[CPL];
+    if (s_begin < s_end) load(pre, s_begin);
+    for (int s = s_begin; s < s_end; ++s) {
+        // chunks past the rows of M or a half last stage stay stale: they only
+        // feed rows that are not stored or blocks whose x is zero
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) *reinterpret_cast<uint4*>(stage + 16 * (64 * j + lane)) = pre[j];
+        wave_lds_sync();
+        const int nblk = min(kMfmaBlocks, (K >> 5) - s * kMfmaBlocks);
+        uint32_t xr[kMfmaBlocks][4];
+#pragma unroll
+        for (int jb = 0; jb < kMfmaBlocks; ++jb) {
+            if (xlane && jb < nblk) load_x_b<F>(xr[jb], xrow, s * kMfmaBlocks + jb, g);
+            else xr[jb][0] = xr[jb][1] = xr[jb][2] = xr[jb][3] = 0u;
+        }
+        if (s + 1 < s_end) load(pre, s + 1);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const uint32_t* row = reinterpret_cast<const uint32_t*>(stage) + (16 * t + bcol) * kRowDw;
+#pragma unroll
+            for (int jb = 0; jb < kMfmaBlocks; ++jb) {
+                const half8_t a = [&] {
+                    switch (jb) {
+                        case 0: return weight_a_operand<F, 0>(row, g, nu);
+                        case 1: return weight_a_operand<F, 1>(row, g, nu);
+                        case 2: return weight_a_operand<F, 2>(row, g, nu);
+                        case 3: return weight_a_operand<F, 3>(row, g, nu);
+                        case 4: return weight_a_operand<F, 4>(row, g, nu);
+                        case 5: return weight_a_operand<F, 5>(row, g, nu);
+                        case 6: return weight_a_operand<F, 6>(row, g, nu);
+                        case 7: return weight_a_operand<F, 7>(row, g, nu);
+                        case 8: return weight_a_operand<F, 8>(row, g, nu);
+                        case 9: return weight_a_operand<F, 9>(row, g, nu);
+                        case 10: return weight_a_operand<F, 10>(row, g, nu);
+                        case 11: return weight_a_operand<F, 11>(row, g, nu);
+                        case 12: return weight_a_operand<F, 12>(row, g, nu);
+                        case 13: return weight_a_operand<F, 13>(row, g, nu);
+                        case 14: return weight_a_operand<F, 14>(row, g, nu);
+                        default: return weight_a_operand<F, 15>(row, g, nu);
+                    }
+                }();
+                // blocks past K in a half last stage hold stale bytes whose scale may be
+                // Inf/NaN; zero x would not cancel that, so they are skipped
+                if (jb < nblk) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, x_b_operand<F>(xr[jb]), acc[t], 0, 0, 0);
+            }
+        }
+    }
+    // Sum the waves' partial tiles: red[wave][t][v][lane], then one thread per
+    // output (row, batch) adds the kMfmaWaves partials.
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(smem);
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) red[((wave * 2 + t) * 4 + v) * 64 + lane] = acc[t][v];
+    __syncthreads();
+    for (int o = threadIdx.x; o < kMfmaRows * nb; o += kMfmaWaves * 64) {
+        const int r = o / nb, b = o - r * nb;
+        if (r < nrows) {
+            const int t = r >> 4, r16 = r & 15;
+            const int src_lane = 16 * (r16 >> 2) + b, v = r16 & 3;
+            float sum = 0.f;
+#pragma unroll
+            for (int w = 0; w < kMfmaWaves; ++w) sum += red[((w * 2 + t) * 4 + v) * 64 + src_lane];
+            Y[b * ldy + r0 + r] = f2h_bits(sum);
+        }
+    }
+}
+
 // Any in_dim % 32 == 0 and any alignment: one wave per row, one lane per block,
 // byte loads, the reference's per-element order of operations.
 template <Fmt F>
@@ -795,6 +1024,22 @@ int gemv(const char* name, const void* w, const void* x, void* y, int64_t out_di
         (batch == 1 ? rows_lds_bytes<F, 1>(NWr) : rows_lds_bytes<F, 2>(NWr)) <= static_cast<size_t>(max_lds_bytes())) {
         rc = batch == 1 ? launch_rows<F, 1>(w, xp, yp, M, K, ldx, ldy, s) : launch_rows<F, 2>(w, xp, yp, M, K, ldx, ldy, s);
         return rc == GDSLLM_OK ? ok() : rc;
+    }
+    const bool x_al16 = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (ldx % 8 == 0);
+    if (fast && batch >= 5 && K <= (1 << 20) && x_al16) {
+        const size_t lds = static_cast<size_t>(kMfmaWaves) * mfma_stage_bytes<F>();
+        const void* fn = reinterpret_cast<const void*>(&gguf_gemv_mfma<F>);
+        if (lds > 65536) {
+            if (int e = check_hip(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                      static_cast<int>(lds)),
+                                  "hipFuncSetAttribute"))
+                return e;
+        }
+        const int grid = (M + kMfmaRows - 1) / kMfmaRows;
+        hipLaunchKernelGGL(gguf_gemv_mfma<F>, dim3(grid), dim3(kMfmaWaves * 64), lds, s,
+                           static_cast<const uint8_t*>(w), xp, yp, M, K, static_cast<int>(batch), ldx, ldy);
+        if (int e = check_hip(hipGetLastError(), (n + " launch").c_str())) return e;
+        return ok();
     }
     if (fast) {
         const int S = K >> 8;

@@ -23,10 +23,6 @@
 // selected expert into LDS and computes each output row as the weighted sum
 // over experts of the down-projection rows.
 
-#include <mutex>
-#include <utility>
-#include <vector>
-
 #include "common.h"
 
 namespace gdsllm {
@@ -334,25 +330,6 @@ __global__ __launch_bounds__(kThreads) void moe_down(gdsllm_affine_experts down,
     }
 }
 
-int blocks_per_cu(const void* fn, size_t lds, int threads = kThreads) {
-    static std::mutex mu;
-    static std::vector<std::pair<std::pair<const void*, size_t>, int>> cache;
-    std::lock_guard<std::mutex> lock(mu);
-    for (auto& e : cache)
-        if (e.first.first == fn && e.first.second == lds) return e.second;
-    int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, threads, lds) != hipSuccess || n <= 0) n = 1;
-    cache.push_back({{fn, lds}, n});
-    return n;
-}
-
-int prepare(const void* fn, size_t lds) {
-    if (lds > 65536)
-        return check_hip(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)),
-                         "hipFuncSetAttribute");
-    return GDSLLM_OK;
-}
-
 // Lanes per row: the widest power of two <= min(64, chunks per row).
 int lanes_per_row(int cpr) {
     int lr = 64;
@@ -364,10 +341,10 @@ template <int LR, int NB, class Rows>
 int launch_affine_gemv(const Rows& rows, const uint16_t* x, int K, int gsize, int64_t ldx, hipStream_t stream) {
     const void* fn = reinterpret_cast<const void*>(&affine_gemv<LR, NB, Rows>);
     const size_t lds = static_cast<size_t>(NB) * (K / 32) * kRec;
-    if (int rc = prepare(fn, lds)) return rc;
+    if (int rc = prepare_lds(fn, lds)) return rc;
     const int passes = (rows.M + 64 / LR - 1) / (64 / LR);
     const int need = (passes + kWaves - 1) / kWaves;
-    const int cap = blocks_per_cu(fn, lds) * cu_count();
+    const int cap = blocks_per_cu(fn, lds, kThreads) * cu_count();
     const int grid = need < cap ? need : cap;
     const bool al16 = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (ldx % 8 == 0);
     hipLaunchKernelGGL((affine_gemv<LR, NB, Rows>), dim3(grid), dim3(kThreads), lds, stream, rows, x, K, gsize, ldx,
@@ -861,7 +838,7 @@ int launch_affine_rows(const Rows& rows, const uint16_t* x, int K, int gsize, in
     const int rps = 4 * (64 / LR);
     const int stages = (rows.M + rps - 1) / rps;
     const int need = (stages + kWaves - 1) / kWaves;
-    const int cap = blocks_per_cu(fn, 0) * cu_count();
+    const int cap = blocks_per_cu(fn, 0, kThreads) * cu_count();
     const int grid = need < cap ? need : cap;
     const bool al16 = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (ldx % 8 == 0);
     hipLaunchKernelGGL((affine_rows<LR, CPL, NB, Rows>), dim3(grid), dim3(kThreads), 0, stream, rows, x, K, gsize, ldx,
@@ -906,7 +883,7 @@ int launch_moe_down(const gdsllm_affine_experts& down, const int32_t* idx, const
     constexpr int NT = (SLOTS <= 3 || SLOTS == 5) ? 1024 : 512;
     const void* fn = reinterpret_cast<const void*>(&moe_down_rows<LR, SLOTS, NT>);
     const size_t lds = static_cast<size_t>(top_k) * (down.in_dim / 32) * kRec;
-    if (int rc = prepare(fn, lds)) return rc;
+    if (int rc = prepare_lds(fn, lds)) return rc;
     constexpr int R = SLOTS <= 4 ? 2 : 1;
     const int stages = static_cast<int>((down.out_dim + R - 1) / R);
     const int need = (stages + NT / 64 - 1) / (NT / 64);
@@ -1107,10 +1084,10 @@ extern "C" int gdsllm_moe_gather_affine_q4(const gdsllm_affine_experts* gate, co
         case 16: fn = reinterpret_cast<const void*>(&moe_down<16>); break;
         default: fn = reinterpret_cast<const void*>(&moe_down<8>); break;
     }
-    if (int rc = prepare(fn, lds2)) return rc;
+    if (int rc = prepare_lds(fn, lds2)) return rc;
     const int passes = static_cast<int>((H + 64 / lr - 1) / (64 / lr));
     const int need = (passes + kWaves - 1) / kWaves;
-    const int cap = blocks_per_cu(fn, lds2) * cu_count();
+    const int cap = blocks_per_cu(fn, lds2, kThreads) * cu_count();
     const int grid = need < cap ? need : cap;
     auto* yp = static_cast<uint16_t*>(y);
     const auto* wp = static_cast<const uint16_t*>(routing_weights);

@@ -24,6 +24,11 @@ int check_hip(hipError_t err, const char* what);
 int cu_count();
 // Maximum dynamic LDS bytes a workgroup may use on the current device.
 int max_lds_bytes();
+// Allows `fn` to launch with `lds` dynamic LDS bytes (above the 64 KiB default).
+int prepare_lds(const void* fn, size_t lds);
+// Workgroups of `threads` threads of kernel `fn` with `lds` dynamic LDS bytes
+// that fit on one compute unit (at least 1; cached).
+int blocks_per_cu(const void* fn, size_t lds, int threads);
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
@@ -123,12 +128,86 @@ __device__ __forceinline__ float row16_sum(float v) {
     v += dpp_read<0x140>(v);  // row_mirror
     return v;
 }
+// a + b after swapping lanes 32..63 of a with lanes 0..31 of b
+// (v_permlane32_swap_b32): lanes 0..31 get a[l] + a[l+32], lanes 32..63 get
+// b[l-32] + b[l].  swap16 does the same for 16-lane halves within each 32-lane
+// half.  Written as inline asm (with the swap-to-swap wait states) because
+// this toolchain's builtins return both swapped values in one register.
+__device__ __forceinline__ float swap_sum32(float a, float b) {
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+    return a + b;
+}
+__device__ __forceinline__ float swap_sum16(float a, float b) {
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+    return a + b;
+}
+
 // Sum over groups of `width` lanes (power of two <= 64).
 template <int WIDTH>
 __device__ __forceinline__ float group_sum(float v) {
 #pragma unroll
     for (int o = WIDTH / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, WIDTH);
     return v;
+}
+
+// 16 bytes per lane from global memory straight into LDS (global_load_lds_dwordx4,
+// non-temporal): lane l's bytes land at lds + 16*l.  `lds` must be the same for
+// every lane of the wave (it goes to M0).  The transfer is tracked by vmcnt
+// like a load; the data is readable from LDS once a vmcnt wait covers it.
+__device__ __forceinline__ void dma16(const void* g, void* lds) {
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)(lds), 16, 0,
+                                     /*nt*/ 2);
+}
+
+// The same with the default cache policy: for data many workgroups read (the
+// activation vector), which should stay in L2 after its first miss.
+__device__ __forceinline__ void dma16_cached(const void* g, void* lds) {
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)(lds), 16, 0, 0);
+}
+
+// Waits until at most N vector-memory operations of this wave are in flight
+// (s_waitcnt vmcnt(N); expcnt and lgkmcnt untouched).  Vector memory loads
+// retire in issue order, so this waits for all but the last N issued.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+    asm volatile("" ::: "memory");
+}
+
+// LDS accesses written as instructions the compiler does not analyse.  The
+// compiler orders every LDS access it sees after all in-flight LDS DMA
+// transfers it cannot prove disjoint from it, i.e. it waits for every
+// transfer; these let a kernel touch a region no transfer writes (prepared
+// x) while transfers into its stage buffers are in flight.  Reads return
+// unsynchronised: an "s_waitcnt lgkmcnt(0)" that takes their results as
+// operands must follow before they are used.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
+}
+__device__ __forceinline__ void lds_write16_raw(uint32_t addr, u32x4_t v) {
+    asm volatile("ds_write_b128 %0, %1" ::"v"(addr), "v"(v) : "memory");
+}
+__device__ __forceinline__ void lds_write4_raw(uint32_t addr, uint32_t v) {
+    asm volatile("ds_write_b32 %0, %1" ::"v"(addr), "v"(v) : "memory");
+}
+__device__ __forceinline__ u32x4_t lds_read16_raw(uint32_t addr) {
+    u32x4_t v;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+    return v;
+}
+__device__ __forceinline__ uint64_t lds_read8_raw(uint32_t addr) {
+    uint64_t v;
+    asm volatile("ds_read_b64 %0, %1" : "=v"(v) : "v"(addr));
+    return v;
+}
+// Workgroup barrier for LDS data only: this wave's LDS requests complete, then
+// s_barrier.  Unlike __syncthreads it does not wait for outstanding global
+// loads or LDS DMA transfers.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
 }
 
 // Orders this wave's earlier LDS writes before its later LDS reads.  LDS

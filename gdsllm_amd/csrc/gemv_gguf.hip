@@ -25,9 +25,7 @@
 //  * The 16 partial sums of a row are reduced with cross-lane shuffles inside
 //    the 16-lane DPP row; lane 0 of the row writes the fp16 result.
 
-#include <mutex>
-#include <utility>
-#include <vector>
+#include <algorithm>
 
 #include "common.h"
 
@@ -319,16 +317,18 @@ __global__ __launch_bounds__(kWaves * 64) void gguf_gemv_staged(const uint8_t* _
 }
 
 // ---- row-span kernel (batch 1..2) ----------------------------------------------
-// Same stages as gguf_gemv_staged (4 rows x one window of 16 super-blocks =
-// 128 blocks, fetched with coalesced 16-byte loads and transposed through a
-// per-wave LDS slot), but after the transpose lane c owns blocks 2c and 2c+1
-// of the window in all 4 rows.  Its slice of x (64 elements per batch row) is
-// the same for every row it touches, so it sits in registers: the workgroup
-// prepares x once in LDS (fp16 pairs in the order the unpacked nibbles come
-// out in, plus each block's offset correction) while the first stage's
-// weights are in flight, and a wave reloads its slice only when its window
-// changes.  The 8 (row, block) dot-product chains of a stage are interleaved,
-// and the 4 row sums of a wave reduce in 3 cross-lane swaps + 4 DPP steps.
+// Stages of 4 rows x one window of 16 super-blocks (128 blocks), moved from
+// HBM straight into a per-wave LDS buffer by 16-byte-per-lane DMA transfers
+// (no staging registers, no LDS store instructions); from there lane c owns
+// blocks 2c and 2c+1 of the window in all 4 rows.  A stage is consumed in two
+// halves, rows 0-1 as soon as the transfers holding them have retired, and
+// with two buffers per wave the next stage is in flight meanwhile.  The lane's
+// slice of x (blocks 2c, 2c+1 of the window: 64 elements per batch row) is the
+// same for every row it touches, so it sits in registers, permuted once per
+// window into the pair order the unpacked nibbles come out in, with each
+// block's offset correction.  The 4 (row, block) chains of a
+// half stage are interleaved, and the 4 row sums of a wave reduce in 3
+// cross-lane swaps + 4 DPP steps.
 
 constexpr int kWinBlocks = kSbPerWindow * 8;  // blocks per row in one stage
 
@@ -339,26 +339,25 @@ constexpr uint32_t kPair1032 = 0x64086408u;
 constexpr uint32_t kPair72 = 0x54805480u;
 constexpr uint32_t kPair1152 = 0x64806480u;
 
-// Prepared x of one lane span (2 blocks = 64 elements of one batch row): 16
-// packed pairs per block, then the two corrections.  The 144-byte stride (36
-// dwords) puts 8 consecutive lanes' ds_read_b128 on distinct bank quads.
-constexpr int kSpanRec = 144;
-
-template <int NB>
-struct XSlice {
-    uint32_t p[NB][2][16];  // packed fp16 pairs of blocks 2c, 2c+1, per batch row
-    float c[NB][2];         // offset correction of each block
-};
-
 // (lo, hi) = low halves / high halves of (u, v): v_perm_b32 selectors with
 // S0 = v, S1 = u.
 constexpr uint32_t kSelLo = 0x05040100u;
 constexpr uint32_t kSelHi = 0x07060302u;
 
+// A lane's x slice: fp16 pairs of blocks 2c, 2c+1 of the window in the order
+// the unpacked nibbles come out in (p[b][k]: block k), and each block's offset
+// correction: 1032*sum(x[0..16)) + 72*sum(x[16..32)) (Q4_0) or 1152*sum(x)
+// (Q8_0), so a block reduces to d * (S - c).
+template <int NB>
+struct XSlice {
+    uint32_t p[NB][2][16];
+    float c[NB][2];
+};
+
 // 32 raw fp16 of one block (r[i] = elements 2i, 2i+1) -> 16 pairs in unpack
-// order (p) and the block's offset correction (returned).
+// order and the block's offset correction (returned).
 template <Fmt F>
-__device__ __forceinline__ float permute_block(const uint32_t (&r)[16], uint32_t (&p)[16]) {
+__device__ __forceinline__ float permute_block(const uint32_t* r, uint32_t* p) {
     float c = 0.f;
     if constexpr (F == Fmt::Q4_0) {
         // qs dword dd: low nibbles = elements 4dd..4dd+3, high = 16+4dd..19+4dd;
@@ -371,10 +370,10 @@ __device__ __forceinline__ float permute_block(const uint32_t (&r)[16], uint32_t
             p[4 * dd + 1] = __builtin_amdgcn_perm(vh, uh, kSelLo);
             p[4 * dd + 2] = __builtin_amdgcn_perm(v, u, kSelHi);
             p[4 * dd + 3] = __builtin_amdgcn_perm(vh, uh, kSelHi);
-            c = dot2(p[4 * dd + 0], kPair1032, c);
-            c = dot2(p[4 * dd + 2], kPair1032, c);
-            c = dot2(p[4 * dd + 1], kPair72, c);
-            c = dot2(p[4 * dd + 3], kPair72, c);
+            c = dot2(u, kPair1032, c);
+            c = dot2(v, kPair1032, c);
+            c = dot2(uh, kPair72, c);
+            c = dot2(vh, kPair72, c);
         }
     } else {
         // qs dword dd = elements 4dd..4dd+3: pairs (bytes 0,2) (bytes 1,3)
@@ -383,77 +382,60 @@ __device__ __forceinline__ float permute_block(const uint32_t (&r)[16], uint32_t
             const uint32_t u = r[2 * dd], v = r[2 * dd + 1];
             p[2 * dd] = __builtin_amdgcn_perm(v, u, kSelLo);
             p[2 * dd + 1] = __builtin_amdgcn_perm(v, u, kSelHi);
-            c = dot2(p[2 * dd], kPair1152, c);
-            c = dot2(p[2 * dd + 1], kPair1152, c);
+            c = dot2(u, kPair1152, c);
+            c = dot2(v, kPair1152, c);
         }
     }
     return c;
 }
 
-// The workgroup writes the prepared spans of every window for NB batch rows:
-// record (b, w, c) at xp + ((b*NW + w)*64 + c)*kSpanRec.  One item = one block
-// (32 fp16 of one batch row).
-__device__ __forceinline__ void load_block_raw(uint32_t (&r)[16], const uint16_t* __restrict__ src, bool al16) {
-    if (al16) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const uint4 v = *reinterpret_cast<const uint4*>(src + 8 * k);
-            r[4 * k] = v.x;
-            r[4 * k + 1] = v.y;
-            r[4 * k + 2] = v.z;
-            r[4 * k + 3] = v.w;
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) r[i] = static_cast<uint32_t>(src[2 * i]) | (static_cast<uint32_t>(src[2 * i + 1]) << 16);
-    }
-}
-
-template <Fmt F>
-__device__ __forceinline__ void store_span_block(uint8_t* xp, const uint32_t (&r)[16], int g, int b, int NW) {
-    uint32_t pr[16];
-    const float c = permute_block<F>(r, pr);
-    const int w = g / kWinBlocks, cb = g % kWinBlocks;
-    uint8_t* rec = xp + ((b * NW + w) * 64 + (cb >> 1)) * kSpanRec;
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-        *reinterpret_cast<uint4*>(rec + 64 * (cb & 1) + 16 * k) = make_uint4(pr[4 * k], pr[4 * k + 1], pr[4 * k + 2], pr[4 * k + 3]);
-    *reinterpret_cast<float*>(rec + 128 + 4 * (cb & 1)) = c;
-}
-
-// Items after each thread's first one (rows longer than one window of blocks
-// per thread); the first item is handled by the caller around the weight loads.
-template <Fmt F, int NB>
-__device__ void build_spans_rest(uint8_t* xp, const uint16_t* __restrict__ X, int64_t ldx, int K, int NW, bool al16) {
-    const int nblk = K >> 5;
-    const int per_row = NW * kWinBlocks;
-    for (int it = threadIdx.x + kWaves * 64; it < NB * per_row; it += kWaves * 64) {
-        const int g = it % per_row, b = it / per_row;
-        if (g >= nblk) continue;  // past the end of the row: its lanes never compute
-        uint32_t r[16];
-        load_block_raw(r, X + b * ldx + 32 * g, al16);
-        store_span_block<F>(xp, r, g, b, NW);
-    }
-}
+// Raw x in LDS, laid out for the slices: record (b, w) = batch row b, window w
+// is 8 KiB; its 16-byte slot 64i + c holds elements [64c + 8i, 64c + 8i + 8)
+// of the window, so reading chunk i of every lane's slice is one
+// conflict-free 1 KiB row.  The workgroup fills it with DMA transfers (slot
+// row i of record (b, w) = transfer (b*NW + w)*8 + i), which the compiler
+// does not count when it waits for an ordinary load issued before them: x
+// loaded into registers ahead of the weight transfers would wait for all of
+// them.
+__host__ __device__ inline int rows_xraw_bytes(int nb, int nw) { return nb * nw * 8192; }
 
 template <int NB>
-__device__ __forceinline__ void load_span(XSlice<NB>& xs, const uint8_t* xp, int NW, int w, int lane) {
+__device__ __forceinline__ void rows_xraw_issue(uint8_t* xraw, const uint16_t* __restrict__ X, int64_t ldx, int K,
+                                                int NW, int wave, int wpg, int lane) {
+    const int n = NB * NW * 8;
+    for (int t = wave; t < n; t += wpg) {
+        const int i = t & 7, w = (t >> 3) % NW, b = (t >> 3) / NW;
+        const int e = 4096 * w + 64 * lane + 8 * i;  // first element of the slot
+        dma16_cached(e < K ? X + b * ldx + e : X, xraw + 1024 * t);
+    }
+}
+
+// The slice of window w, read with the raw LDS helpers (no weight transfer
+// ever targets the x region), permuted into unpack order, with corrections.
+template <Fmt F, int NB>
+__device__ __forceinline__ void load_slice(XSlice<NB>& xs, const uint8_t* xraw, int NW, int w, int lane) {
+    u32x4_t v[NB][8];
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-        const uint8_t* rec = xp + ((b * NW + w) * 64 + lane) * kSpanRec;
+        const uint32_t rec = lds_addr(xraw + (b * NW + w) * 8192 + 16 * lane);
 #pragma unroll
-        for (int blk = 0; blk < 2; ++blk)
+        for (int i = 0; i < 8; ++i) v[b][i] = lds_read16_raw(rec + 1024 * i);
+    }
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const uint4 v = *reinterpret_cast<const uint4*>(rec + 64 * blk + 16 * k);
-                xs.p[b][blk][4 * k] = v.x;
-                xs.p[b][blk][4 * k + 1] = v.y;
-                xs.p[b][blk][4 * k + 2] = v.z;
-                xs.p[b][blk][4 * k + 3] = v.w;
-            }
-        const float2 c = *reinterpret_cast<const float2*>(rec + 128);
-        xs.c[b][0] = c.x;
-        xs.c[b][1] = c.y;
+    for (int b = 0; b < NB; ++b) {
+        // the wait takes the raw reads' results, so nothing uses them earlier
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(v[b][0]), "+v"(v[b][1]), "+v"(v[b][2]), "+v"(v[b][3]), "+v"(v[b][4]), "+v"(v[b][5]),
+                       "+v"(v[b][6]), "+v"(v[b][7]));
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            uint32_t r[16];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) r[4 * i + e] = v[b][4 * k + i][e];
+            xs.c[b][k] = permute_block<F>(r, xs.p[b][k]);
+        }
     }
 }
 
@@ -476,94 +458,121 @@ __device__ __forceinline__ float dword_dot(uint32_t q, const uint32_t* xp, int d
 }
 
 // Sums acc[0..3] over the 64 lanes of the wave.  Lane L ends up holding the
-// total of row 2*(L>>5) + ((L>>4)&1): lanes 0-15 row 0, 16-31 row 1, 32-47
-// row 2, 48-63 row 3.
-__device__ __forceinline__ float reduce_rows4(const float (&acc)[4], int lane) {
-    const bool h32 = lane & 32;
-    float k0 = h32 ? acc[2] : acc[0], k1 = h32 ? acc[3] : acc[1];
-    const float s0 = h32 ? acc[0] : acc[2], s1 = h32 ? acc[1] : acc[3];
-    k0 += __shfl_xor(s0, 32);
-    k1 += __shfl_xor(s1, 32);
-    const bool h16 = lane & 16;
-    float k = h16 ? k1 : k0;
-    k += __shfl_xor(h16 ? k0 : k1, 16);
-    return row16_sum(k);
+// total of row L >> 4: lanes 0-15 row 0, 16-31 row 1, 32-47 row 2, 48-63 row 3
+// (two lane-half swaps, then the 16-lane DPP sum).
+__device__ __forceinline__ float reduce_rows4(const float (&acc)[4]) {
+    const float k02 = swap_sum32(acc[0], acc[2]);  // rows 0 | 2 over lanes l, l+32
+    const float k13 = swap_sum32(acc[1], acc[3]);  // rows 1 | 3
+    return row16_sum(swap_sum16(k02, k13));
 }
 
-// Stage loads and LDS stores.  A full stage (4 rows x 16 super-blocks) has the
-// same per-lane chunk offsets every time, so they are computed once per kernel
-// (goff) and each load is a uniform stage base + a per-lane 32-bit offset; its
-// rows are contiguous in LDS, so chunk c goes to byte 16c.  Partial stages
-// (the last rows of M, the last window of a row) take the predicated path.
-// Offsets stay in 32 bits and the multiplies in 24 bits: in_dim <= 2^20.
-template <Fmt F>
-__device__ __forceinline__ void rows_load(uint4 (&pre)[Layout<F>::kSbChunks], const uint8_t* __restrict__ W,
-                                          uint32_t row_bytes, const uint32_t (&goff)[Layout<F>::kSbChunks],
-                                          const Stage& st, int lane) {
+// Stage transfers, global memory straight to LDS.  Slot s = 64j + lane of a
+// wave's stage buffer (bytes [16s, 16s+16)) holds chunk s % kSegChunks of the
+// stage's row s / kSegChunks, so the rows of a stage sit kSegBytes apart in LDS
+// whatever its width.  A full stage (4 rows x 16 super-blocks) has the same
+// per-lane offsets every time (goff, computed once); a partial one (the last
+// rows of M, the last window of a row) points the slots it does not cover at
+// its first chunk.  `live == false` sends every slot to the first 16 bytes of
+// x, a dummy transfer that keeps each wave's count of transfers fixed.
+// Transfers [J0, J1) of the stage; offsets stay in 32 bits: in_dim <= 2^20.
+template <Fmt F, int J0, int J1>
+__device__ __forceinline__ void rows_issue(uint8_t* buf, const uint8_t* __restrict__ W, const void* dummy,
+                                           uint32_t row_bytes, const uint32_t (&goff)[Layout<F>::kSbChunks],
+                                           const Stage& st, bool live, int lane) {
     using L = Layout<F>;
+    constexpr int kSegChunks = kSbPerWindow * L::kSbChunks;
     const uint8_t* base = W + static_cast<int64_t>(st.r0) * row_bytes + st.sb0 * L::kSbBytes;
-    if (st.nrows == kRowsPerStage && st.nsb == kSbPerWindow) {
+    if (!live) {
 #pragma unroll
-        for (int j = 0; j < L::kSbChunks; ++j) pre[j] = load_nt16(base + goff[j]);
+        for (int j = J0; j < J1; ++j) dma16(dummy, buf + 1024 * j);
+    } else if (st.nrows == kRowsPerStage && st.nsb == kSbPerWindow) {
+#pragma unroll
+        for (int j = J0; j < J1; ++j) dma16(base + goff[j], buf + 1024 * j);
     } else {
-        const int total = st.nrows * st.seg_chunks;
 #pragma unroll
-        for (int j = 0; j < L::kSbChunks; ++j) {
-            const int c = 64 * j + lane;
-            if (c < total) {
-                const uint32_t rl = __umul24(c, st.magic) >> 20;
-                const uint32_t off = c - __umul24(rl, st.seg_chunks);
-                pre[j] = load_nt16(base + (__umul24(rl, row_bytes) + 16 * off));
-            }
+        for (int j = J0; j < J1; ++j) {
+            const uint32_t s = 64 * j + lane;
+            const uint32_t rl = s / kSegChunks, off = s - rl * kSegChunks;
+            const bool in = rl < static_cast<uint32_t>(st.nrows) && off < static_cast<uint32_t>(st.seg_chunks);
+            dma16(base + (in ? __umul24(rl, row_bytes) + 16 * off : 0u), buf + 1024 * j);
         }
     }
 }
 
-template <Fmt F>
-__device__ __forceinline__ void rows_store(const uint4 (&pre)[Layout<F>::kSbChunks], uint8_t* stage, const Stage& st,
-                                           int lane) {
+// LDS of the row-span kernel (all dynamic): one stage buffer per wave, then raw x.
+template <Fmt F, int NB>
+size_t rows_lds_bytes(int nw, int wpg) {
+    return static_cast<size_t>(wpg) * stage_bytes<F>() + static_cast<size_t>(rows_xraw_bytes(NB, nw));
+}
+
+// Rows R0 and R0+1 of a stage in LDS: lane c's blocks 2c, 2c+1 of each row
+// against its x slice, added to acc[b][R0], acc[b][R0+1].  The 2 rows x 2
+// blocks x NB dot-product chains interleave.
+template <Fmt F, int NB, int R0>
+__device__ __forceinline__ void rows_pair(const uint8_t* buf, const XSlice<NB>& xs, float (&acc)[NB][4],
+                                          const NibUnpack& nu, int lane) {
     using L = Layout<F>;
     constexpr int kSegBytes = kSbPerWindow * L::kSbBytes;
-    if (st.nrows == kRowsPerStage && st.nsb == kSbPerWindow) {
+    constexpr int kSpanDw = L::kBlockBytes / 2;  // dwords of a lane's 2 blocks
+    constexpr int kQd = (L::kBlockBytes - 2) / 4;  // qs dwords per block
+    uint32_t D[2][kSpanDw];
 #pragma unroll
-        for (int j = 0; j < L::kSbChunks; ++j) *reinterpret_cast<uint4*>(stage + 16 * (64 * j + lane)) = pre[j];
-    } else {
-        const int total = st.nrows * st.seg_chunks;
+    for (int r = 0; r < 2; ++r) {
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(buf + (R0 + r) * kSegBytes) + kSpanDw * lane;
 #pragma unroll
-        for (int j = 0; j < L::kSbChunks; ++j) {
-            const int c = 64 * j + lane;
-            if (c < total) {
-                const uint32_t rl = __umul24(c, st.magic) >> 20;
-                const uint32_t off = c - __umul24(rl, st.seg_chunks);
-                *reinterpret_cast<uint4*>(stage + __umul24(rl, kSegBytes) + 16 * off) = pre[j];
+        for (int i = 0; i < kSpanDw; ++i) D[r][i] = src[i];
+    }
+    // block 2c: scale = bytes 0-1, qs from byte 2; block 2c+1 starts at byte
+    // kBlockBytes (dword-aligned halfway point: scale in the high half)
+    float Sx[NB][2][2];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int r = 0; r < 2; ++r) Sx[b][r][0] = Sx[b][r][1] = 0.f;
+#pragma unroll
+    for (int dd = 0; dd < kQd; ++dd)
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const uint32_t q0 = align2(D[r][dd], D[r][dd + 1]);
+            const uint32_t q1 = D[r][kQd + 1 + dd];
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                Sx[b][r][0] = dword_dot<F>(q0, xs.p[b][0], dd, Sx[b][r][0], nu);
+                Sx[b][r][1] = dword_dot<F>(q1, xs.p[b][1], dd, Sx[b][r][1], nu);
             }
+        }
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const float d0 = h2f(D[r][0] & 0xFFFFu), d1 = h2f(D[r][kQd] >> 16);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            acc[b][R0 + r] = __builtin_fmaf(d0, Sx[b][r][0] - xs.c[b][0], acc[b][R0 + r]);
+            acc[b][R0 + r] = __builtin_fmaf(d1, Sx[b][r][1] - xs.c[b][1], acc[b][R0 + r]);
         }
     }
 }
 
-template <Fmt F, int NB>
-size_t rows_lds_bytes(int nw) {
-    return static_cast<size_t>(kWaves) * stage_bytes<F>() + static_cast<size_t>(NB) * nw * 64 * kSpanRec;
-}
-
+// x must be 16-byte aligned with ldx % 8 == 0.  Workgroups of kWaves waves;
+// LDS (dynamic): the waves' stage buffers, then raw x.  One buffer per wave: after rows 0-1 of a stage are consumed, the next
+// stage's transfers that land in their slots only (kEarly) are issued, the
+// rest after rows 2-3.
 template <Fmt F, int NB>
 __global__ __launch_bounds__(kWaves * 64) void gguf_gemv_rows(const uint8_t* __restrict__ W,
                                                               const uint16_t* __restrict__ X,
                                                               uint16_t* __restrict__ Y, int M, int K, int64_t ldx,
-                                                              int64_t ldy, int x_al16) {
+                                                              int64_t ldy) {
     using L = Layout<F>;
-    constexpr int kSegBytes = kSbPerWindow * L::kSbBytes;  // one row of a stage
+    constexpr int C = L::kSbChunks;                        // transfers per stage
     constexpr int kSegChunks = kSbPerWindow * L::kSbChunks;
-    constexpr int kSpanDw = L::kBlockBytes / 2;             // dwords of a lane's 2 blocks
-    constexpr int kQd = (L::kBlockBytes - 2) / 4;           // qs dwords per block
-    constexpr int kRowsIlp = F == Fmt::Q4_0 ? 4 : 2;        // rows whose chains interleave
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    constexpr int kHalf = (2 * kSegChunks + 63) / 64;      // transfers that complete rows 0-1
+    constexpr int kEarly = (2 * kSegChunks) / 64;          // transfers within rows 0-1 only
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int S = K >> 8;
     const uint32_t row_bytes = static_cast<uint32_t>(S) * L::kSbBytes;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    uint8_t* stage = smem + wave * stage_bytes<F>();
-    uint8_t* xp = smem + kWaves * stage_bytes<F>();
+    uint8_t* buf = lds + wave * stage_bytes<F>();
+    uint8_t* xp = lds + kWaves * stage_bytes<F>();
     const int RG = (M + kRowsPerStage - 1) / kRowsPerStage;
     const int NW = (S + kSbPerWindow - 1) / kSbPerWindow;
     const int total_waves = gridDim.x * kWaves;
@@ -571,32 +580,28 @@ __global__ __launch_bounds__(kWaves * 64) void gguf_gemv_rows(const uint8_t* __r
     const int my_rgs = gw < RG ? (RG - 1 - gw) / total_waves + 1 : 0;
     const int T = my_rgs * NW;
     const NibUnpack nu;
+    auto stage_at = [&](int t) { return make_stage<F>(gw + (t / NW) * total_waves, t % NW, M, S); };
 
-    uint32_t goff[L::kSbChunks];
+    uint32_t goff[C];
 #pragma unroll
-    for (int j = 0; j < L::kSbChunks; ++j) {
+    for (int j = 0; j < C; ++j) {
         const uint32_t c = 64 * j + lane;
         const uint32_t rl = c / kSegChunks;
         goff[j] = rl * row_bytes + 16 * (c - rl * kSegChunks);
     }
 
-    // x for this thread's first span block is requested first, then the first
-    // stage's weights; loads retire in order, so preparing x waits only for x
-    // and overlaps the weights' HBM latency, as does the barrier.
-    const int per_row = NW * kWinBlocks;
-    const int g0 = threadIdx.x % per_row, b0 = threadIdx.x / per_row;
-    const bool has0 = b0 < NB && g0 < (K >> 5);
-    uint32_t xr[16];
-    if (has0) load_block_raw(xr, X + b0 * ldx + 32 * g0, x_al16 != 0);
-    uint4 pre[L::kSbChunks];
-    if (T > 0) rows_load<F>(pre, W, row_bytes, goff, make_stage<F>(gw, 0, M, S), lane);
-    if (has0) store_span_block<F>(xp, xr, g0, b0, NW);
-    build_spans_rest<F, NB>(xp, X, ldx, K, NW, x_al16 != 0);
-    __syncthreads();
-    if (T == 0) return;
+    // Request order: raw x, then the first stage of weights (always issued,
+    // dummy when the wave has no stage); waiting for all but the weight
+    // transfers then waits for x only.  A compute unit returns its requests in
+    // order, so every wave's x is requested before any wave's weights.
+    rows_xraw_issue<NB>(xp, X, ldx, K, NW, wave, kWaves, lane);
+    __builtin_amdgcn_s_barrier();
+    rows_issue<F, 0, C>(buf, W, X, row_bytes, goff, stage_at(0), T > 0, lane);
+    wait_vmcnt<C>();
+    lds_barrier();  // every wave's share of x has landed
 
     XSlice<NB> xs;
-    load_span<NB>(xs, xp, NW, 0, lane);
+    if (T > 0) load_slice<F, NB>(xs, xp, NW, 0, lane);
     int xwin = 0;
     float acc[NB][4];
 #pragma unroll
@@ -606,71 +611,43 @@ __global__ __launch_bounds__(kWaves * 64) void gguf_gemv_rows(const uint8_t* __r
 
     for (int t = 0; t < T; ++t) {
         const int win = t % NW;
-        const Stage st = make_stage<F>(gw + (t / NW) * total_waves, win, M, S);
-        rows_store<F>(pre, stage, st, lane);
-        wave_lds_sync();
-        if (t + 1 < T) {
-            const int t1 = t + 1;
-            rows_load<F>(pre, W, row_bytes, goff, make_stage<F>(gw + (t1 / NW) * total_waves, t1 % NW, M, S), lane);
-        }
+        const Stage st = stage_at(t);
+        const bool next = t + 1 < T;
         if (win != xwin) {
-            load_span<NB>(xs, xp, NW, win, lane);
+            load_slice<F, NB>(xs, xp, NW, win, lane);
             xwin = win;
         }
-        // Lanes past the end of a partial window, and rows past M, compute on
-        // stale stage bytes; their sums are never stored.
-        if (lane < st.nsb * 4) {
-#pragma unroll
-            for (int r0 = 0; r0 < kRowsPerStage; r0 += kRowsIlp) {
-                uint32_t D[kRowsIlp][kSpanDw];
-#pragma unroll
-                for (int r = 0; r < kRowsIlp; ++r) {
-                    const uint32_t* src =
-                        reinterpret_cast<const uint32_t*>(stage + (r0 + r) * kSegBytes) + kSpanDw * lane;
-#pragma unroll
-                    for (int i = 0; i < kSpanDw; ++i) D[r][i] = src[i];
-                }
-                // block 2c: scale = bytes 0-1, qs from byte 2; block 2c+1 starts at
-                // byte kBlockBytes (dword-aligned halfway point: scale in the high half)
-                float Sx[NB][kRowsIlp][2];
-#pragma unroll
-                for (int b = 0; b < NB; ++b)
-#pragma unroll
-                    for (int r = 0; r < kRowsIlp; ++r) Sx[b][r][0] = Sx[b][r][1] = 0.f;
-#pragma unroll
-                for (int dd = 0; dd < kQd; ++dd)
-#pragma unroll
-                    for (int r = 0; r < kRowsIlp; ++r) {
-                        const uint32_t q0 = align2(D[r][dd], D[r][dd + 1]);
-                        const uint32_t q1 = D[r][kQd + 1 + dd];
-#pragma unroll
-                        for (int b = 0; b < NB; ++b) {
-                            Sx[b][r][0] = dword_dot<F>(q0, xs.p[b][0], dd, Sx[b][r][0], nu);
-                            Sx[b][r][1] = dword_dot<F>(q1, xs.p[b][1], dd, Sx[b][r][1], nu);
-                        }
-                    }
-#pragma unroll
-                for (int r = 0; r < kRowsIlp; ++r) {
-                    const float d0 = h2f(D[r][0] & 0xFFFFu), d1 = h2f(D[r][kQd] >> 16);
-#pragma unroll
-                    for (int b = 0; b < NB; ++b) {
-                        acc[b][r0 + r] = __builtin_fmaf(d0, Sx[b][r][0] - xs.c[b][0], acc[b][r0 + r]);
-                        acc[b][r0 + r] = __builtin_fmaf(d1, Sx[b][r][1] - xs.c[b][1], acc[b][r0 + r]);
-                    }
-                }
-            }
+        // Lanes past the end of a partial window skip; rows past M compute on
+        // filler bytes and are never stored.  In flight here: this stage only.
+        const bool active = lane < st.nsb * 4;
+        wait_vmcnt<C - kHalf>();
+        if (active) rows_pair<F, NB, 0>(buf, xs, acc, nu, lane);
+        // refill slots of rows 0-1 once their reads have returned
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        const Stage nx = stage_at(t + 1);
+        if (next) {
+            rows_issue<F, 0, kEarly>(buf, W, X, row_bytes, goff, nx, true, lane);
+            wait_vmcnt<kEarly>();
+        } else {
+            wait_vmcnt<0>();
         }
+        if (active) rows_pair<F, NB, 2>(buf, xs, acc, nu, lane);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (next) rows_issue<F, kEarly, C>(buf, W, X, row_bytes, goff, nx, true, lane);
         if (win == NW - 1) {
-            const int row = 2 * (lane >> 5) + ((lane >> 4) & 1);
+            const int row = lane >> 4;
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
-                const float v = reduce_rows4(acc[b], lane);
+                const float v = reduce_rows4(acc[b]);
                 if ((lane & 15) == 0 && row < st.nrows) Y[b * ldy + st.r0 + row] = f2h_bits(v);
 #pragma unroll
                 for (int r = 0; r < 4; ++r) acc[b][r] = 0.f;
             }
         }
     }
+    // no transfer into this workgroup's LDS may outlive it (a wave with no
+    // stage issued dummy ones; every other transfer was waited for above)
+    if (T == 0) wait_vmcnt<0>();
 }
 
 // ---- MFMA batched GEMV (batch 3..16) ---------------------------------------------
@@ -938,19 +915,6 @@ __global__ __launch_bounds__(256) void gguf_gemv_generic(const uint8_t* __restri
     }
 }
 
-// Occupancy of a kernel instantiation at a given dynamic LDS size (cached).
-int blocks_per_cu(const void* fn, size_t lds) {
-    static std::mutex mu;
-    static std::vector<std::pair<std::pair<const void*, size_t>, int>> cache;
-    std::lock_guard<std::mutex> lock(mu);
-    for (auto& e : cache)
-        if (e.first.first == fn && e.first.second == lds) return e.second;
-    int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kWaves * 64, lds) != hipSuccess || n <= 0) n = 1;
-    cache.push_back({{fn, lds}, n});
-    return n;
-}
-
 template <Fmt F, int NB>
 int launch_staged(const void* w, const uint16_t* x, uint16_t* y, int M, int K, int64_t ldx, int64_t ldy,
                   hipStream_t stream) {
@@ -965,7 +929,7 @@ int launch_staged(const void* w, const uint16_t* x, uint16_t* y, int M, int K, i
     }
     const int RG = (M + kRowsPerStage - 1) / kRowsPerStage;
     const int need = (RG + kWaves - 1) / kWaves;
-    const int cap = blocks_per_cu(fn, lds) * cu_count();
+    const int cap = blocks_per_cu(fn, lds, kWaves * 64) * cu_count();
     const int grid = need < cap ? need : cap;
     const bool x_al8 = (reinterpret_cast<uintptr_t>(x) % 8 == 0) && (ldx % 4 == 0);
     hipLaunchKernelGGL((gguf_gemv_staged<F, NB>), dim3(grid), dim3(kWaves * 64), lds, stream,
@@ -973,25 +937,30 @@ int launch_staged(const void* w, const uint16_t* x, uint16_t* y, int M, int K, i
     return check_hip(hipGetLastError(), "gguf_gemv launch");
 }
 
+// Launch geometry of the row-span kernel: 4-wave workgroups, as many as the
+// row groups need (one stage or more per wave), capped at the resident count.
+// Measured on MI355X: two stage buffers per wave, or workgroups filling a
+// compute unit on their own, lose to more 4-wave workgroups at one buffer
+// each.  Returns false when no geometry fits (the caller takes another kernel).
 template <Fmt F, int NB>
-int launch_rows(const void* w, const uint16_t* x, uint16_t* y, int M, int K, int64_t ldx, int64_t ldy,
+bool plan_rows(int M, int K, int& grid) {
+    const int NW = ((K >> 8) + kSbPerWindow - 1) / kSbPerWindow;
+    const int RG = (M + kRowsPerStage - 1) / kRowsPerStage;
+    const size_t lds = rows_lds_bytes<F, NB>(NW, kWaves);
+    if (lds > static_cast<size_t>(max_lds_bytes())) return false;
+    const void* fn = reinterpret_cast<const void*>(&gguf_gemv_rows<F, NB>);
+    if (prepare_lds(fn, lds) != GDSLLM_OK) return false;
+    grid = std::min((RG + kWaves - 1) / kWaves, blocks_per_cu(fn, lds, kWaves * 64) * cu_count());
+    return true;
+}
+
+template <Fmt F, int NB>
+int launch_rows(const void* w, const uint16_t* x, uint16_t* y, int M, int K, int64_t ldx, int64_t ldy, int grid,
                 hipStream_t stream) {
     const int NW = ((K >> 8) + kSbPerWindow - 1) / kSbPerWindow;
-    const size_t lds = rows_lds_bytes<F, NB>(NW);
-    const void* fn = reinterpret_cast<const void*>(&gguf_gemv_rows<F, NB>);
-    if (lds > 65536) {
-        if (int rc = check_hip(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                   static_cast<int>(lds)),
-                               "hipFuncSetAttribute"))
-            return rc;
-    }
-    const int RG = (M + kRowsPerStage - 1) / kRowsPerStage;
-    const int need = (RG + kWaves - 1) / kWaves;
-    const int cap = blocks_per_cu(fn, lds) * cu_count();
-    const int grid = need < cap ? need : cap;
-    const bool x_al16 = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (ldx % 8 == 0);
+    const size_t lds = rows_lds_bytes<F, NB>(NW, kWaves);
     hipLaunchKernelGGL((gguf_gemv_rows<F, NB>), dim3(grid), dim3(kWaves * 64), lds, stream,
-                       static_cast<const uint8_t*>(w), x, y, M, K, ldx, ldy, x_al16 ? 1 : 0);
+                       static_cast<const uint8_t*>(w), x, y, M, K, ldx, ldy);
     return check_hip(hipGetLastError(), "gguf_gemv launch");
 }
 
@@ -1019,13 +988,14 @@ int gemv(const char* name, const void* w, const void* x, void* y, int64_t out_di
     auto* yp = static_cast<uint16_t*>(y);
     const bool fast = (K % 256 == 0) && (reinterpret_cast<uintptr_t>(w) % 16 == 0);
     int rc = GDSLLM_OK;
-    const int NWr = ((K >> 8) + kSbPerWindow - 1) / kSbPerWindow;
-    if (fast && batch <= 2 && K <= (1 << 20) &&
-        (batch == 1 ? rows_lds_bytes<F, 1>(NWr) : rows_lds_bytes<F, 2>(NWr)) <= static_cast<size_t>(max_lds_bytes())) {
-        rc = batch == 1 ? launch_rows<F, 1>(w, xp, yp, M, K, ldx, ldy, s) : launch_rows<F, 2>(w, xp, yp, M, K, ldx, ldy, s);
+    const bool x_al16 = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (ldx % 8 == 0 || batch == 1);
+    int rgrid = 0;
+    if (fast && batch <= 2 && K <= (1 << 20) && x_al16 &&
+        (batch == 1 ? plan_rows<F, 1>(M, K, rgrid) : plan_rows<F, 2>(M, K, rgrid))) {
+        rc = batch == 1 ? launch_rows<F, 1>(w, xp, yp, M, K, ldx, ldy, rgrid, s)
+                        : launch_rows<F, 2>(w, xp, yp, M, K, ldx, ldy, rgrid, s);
         return rc == GDSLLM_OK ? ok() : rc;
     }
-    const bool x_al16 = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (ldx % 8 == 0);
     if (fast && batch >= 5 && K <= (1 << 20) && x_al16) {
         const size_t lds = static_cast<size_t>(kMfmaWaves) * mfma_stage_bytes<F>();
         const void* fn = reinterpret_cast<const void*>(&gguf_gemv_mfma<F>);

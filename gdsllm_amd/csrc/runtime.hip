@@ -11,6 +11,9 @@
 #include <cerrno>
 #include <cstring>
 
+#include <mutex>
+#include <vector>
+
 #include "common.h"
 
 namespace gdsllm {
@@ -51,6 +54,29 @@ int cu_count() { return device_attr(g_cu_count, hipDeviceAttributeMultiprocessor
 
 int max_lds_bytes() {
     return device_attr(g_lds_bytes, hipDeviceAttributeMaxSharedMemoryPerBlock, 65536);
+}
+
+int prepare_lds(const void* fn, size_t lds) {
+    if (lds <= 65536) return GDSLLM_OK;
+    return check_hip(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)),
+                     "hipFuncSetAttribute");
+}
+
+int blocks_per_cu(const void* fn, size_t lds, int threads) {
+    struct Entry {
+        const void* fn;
+        size_t lds;
+        int threads, n;
+    };
+    static std::mutex mu;
+    static std::vector<Entry> cache;
+    std::lock_guard<std::mutex> lock(mu);
+    for (const Entry& e : cache)
+        if (e.fn == fn && e.lds == lds && e.threads == threads) return e.n;
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, threads, lds) != hipSuccess || n <= 0) n = 1;
+    cache.push_back({fn, lds, threads, n});
+    return n;
 }
 
 }  // namespace gdsllm

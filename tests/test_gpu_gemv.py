@@ -13,6 +13,8 @@ pytestmark = pytest.mark.gpu
 
 GGUF_SHAPES = [
     (1, 256), (5, 256), (64, 512), (33, 4096), (4096, 4096), (300, 11008), (130, 8192), (17, 28672),
+    # more row groups than resident waves at one window per row: two stage buffers per wave
+    (16001, 2048),
     # in_dim % 256 != 0: generic path
     (10, 32), (7, 96), (9, 4128),
 ]
@@ -36,7 +38,7 @@ def test_gguf_gemv_b1(gpu, fmt, M, K):
 
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
 @pytest.mark.parametrize("B", [2, 3, 4, 8])
-@pytest.mark.parametrize("M,K", [(70, 4096), (33, 11008), (20, 96), (24, 8192), (9, 28672)])
+@pytest.mark.parametrize("M,K", [(70, 4096), (33, 11008), (20, 96), (24, 8192), (9, 28672), (13003, 1024)])
 def test_gguf_gemv_batched(gpu, fmt, B, M, K):
     w, x, deq = _gguf_case(fmt, M, K, B, 2000 + B + M)
     y = gguf_gemv(fmt, w.to(gpu), x.to(gpu), M, K)

@@ -11,9 +11,10 @@ timed steps are replayed from HIP graphs of `--chunk` launches, bracketed by
 HIP events on the launch stream.
 
 Also reported (same JSON line): the LLaMA-7B Q4_0 decode weight sweep, all 32
-layers resident (7 projection GEMVs per layer + lm_head 32000 x 4096 = 225
-launches per token, one HIP graph per token) as tokens/s, and the CPU baseline
-(torch restatement of dequant -> F.linear in fp32 on the host cores).
+layers resident (7 projection GEMVs per layer + lm_head 32000 x 4096, one HIP
+graph per token) as tokens/s, fused (q/k/v grouped, gate+up+SiLU in one
+launch: 129 launches) and unfused (225 launches), and the CPU baseline (torch
+restatement of dequant -> F.linear in fp32 on the host cores).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -131,40 +132,55 @@ def bench_gemv(args, dev):
 
 
 def bench_decode_sweep(args, dev):
-    """LLaMA-7B Q4_0 decode weight sweep: 225 GEMVs per token, one graph."""
+    """LLaMA-7B Q4_0 decode weight sweep, one HIP graph per token, timed two ways.
+
+    unfused: 225 single GEMV launches (7 per layer + lm_head), every GEMV
+    reading a synthetic x of its in_dim.
+    fused: 129 launches with the reference layer's data flow (llama.py:212-256):
+    q/k/v in one grouped launch on x_attn, o on x_o, gate+up+SiLU in one launch
+    on x_mlp writing h, down on that h; lm_head last.  Same weights, same
+    224 + 1 projections.  Returns (ms fused, ms unfused, weights)."""
+    import ctypes
+
     import torch
 
+    from gdsllm_amd import capi, check
     from gdsllm_amd import synthetic as syn
 
     gemv = Q4Gemv()
+    lib = capi()
     gen = torch.Generator(device=dev).manual_seed(2004)
     layers = [[syn.q4_0_weights(m, k, gen) for m, k in LAYER_SHAPES] for _ in range(N_LAYERS)]
     lm_head = syn.q4_0_weights(*LM_HEAD, gen)
     xs = {k: syn.activations(1, k, gen) for k in (4096, 11008)}
     ys = {m: torch.empty(1, m, dtype=torch.float16, device=dev) for m in (4096, 11008, 32000)}
+    x_attn, x_o, x_mlp = (syn.activations(1, 4096, gen) for _ in range(3))
+    y_qkv = [torch.empty(1, 4096, dtype=torch.float16, device=dev) for _ in range(3)]
+    y_o, y_down = torch.empty(1, 4096, dtype=torch.float16, device=dev), torch.empty(1, 4096, dtype=torch.float16, device=dev)
+    h = torch.empty(1, 11008, dtype=torch.float16, device=dev)
+    qkv_w = [(ctypes.c_void_p * 3)(*[w.data_ptr() for w in lw[:3]]) for lw in layers]
+    qkv_y = (ctypes.c_void_p * 3)(*[y.data_ptr() for y in y_qkv])
+    qkv_m = (ctypes.c_int64 * 3)(4096, 4096, 4096)
 
-    def token():
+    def token_unfused():
         for lw in layers:
             for w, (m, k) in zip(lw, LAYER_SHAPES):
                 gemv(w, xs[k], ys[m], m, k)
         gemv(lm_head, xs[LM_HEAD[1]], ys[LM_HEAD[0]], *LM_HEAD)
 
-    token()
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        token()
-    for _ in range(3):
-        graph.replay()
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(args.sweep_tokens):
-        graph.replay()
-    end.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / args.sweep_tokens
-    return ms, (layers, lm_head)
+    def token_fused():
+        st = torch.cuda.current_stream().cuda_stream
+        for li, lw in enumerate(layers):
+            check(lib.gdsllm_fused_q4_0_gemv_group(3, qkv_w[li], qkv_y, qkv_m, x_attn.data_ptr(), 4096, 1, 4096, st))
+            gemv(lw[3], x_o, y_o, 4096, 4096)
+            check(lib.gdsllm_fused_q4_0_gate_up_silu(lw[4].data_ptr(), lw[5].data_ptr(), x_mlp.data_ptr(),
+                                                     h.data_ptr(), 11008, 4096, 1, 4096, 11008, st))
+            gemv(lw[6], h, y_down, 4096, 11008)
+        gemv(lm_head, x_attn, ys[LM_HEAD[0]], *LM_HEAD)
+
+    ms_unfused = _replay_ms(token_unfused, args.sweep_tokens)
+    ms_fused = _replay_ms(token_fused, args.sweep_tokens)
+    return ms_fused, ms_unfused, (layers, lm_head)
 
 
 def _replay_ms(capture, reps: int, warm: int = 3) -> float:
@@ -407,12 +423,15 @@ def main() -> int:
 
     sweep, sweep_weights = None, None
     if args.sweep_tokens > 0:
-        ms_tok, sweep_weights = bench_decode_sweep(args, dev)
+        ms_tok, ms_unf, sweep_weights = bench_decode_sweep(args, dev)
         sb = sweep_bytes()
-        sweep = {"tok_s": round(1e3 / ms_tok, 1), "ms_per_token": round(ms_tok, 4), "launches_per_token": 225,
-                 "bytes_per_token": sb, "GB_s": round(sb / (ms_tok * 1e-3) / 1e9, 1)}
-        print(f"# 7B decode sweep: {ms_tok:.4f} ms/token, {sweep['tok_s']} tok/s, {sweep['GB_s']} GB/s",
-              file=sys.stderr, flush=True)
+        sweep = {"tok_s": round(1e3 / ms_tok, 1), "ms_per_token": round(ms_tok, 4), "launches_per_token": 129,
+                 "bytes_per_token": sb, "GB_s": round(sb / (ms_tok * 1e-3) / 1e9, 1),
+                 "fusion": "q/k/v grouped launch; gate+up+SiLU launch writing h; o, down, lm_head single",
+                 "unfused": {"tok_s": round(1e3 / ms_unf, 1), "ms_per_token": round(ms_unf, 4),
+                             "launches_per_token": 225, "GB_s": round(sb / (ms_unf * 1e-3) / 1e9, 1)}}
+        print(f"# 7B decode sweep: {ms_tok:.4f} ms/token, {sweep['tok_s']} tok/s, {sweep['GB_s']} GB/s "
+              f"(unfused 225 launches: {sweep['unfused']['tok_s']} tok/s)", file=sys.stderr, flush=True)
 
     wanted = {c.strip() for c in args.configs.split(",") if c.strip()}
     unknown = wanted - {"q8", "moe", "70b", "prefill"}

@@ -43,6 +43,10 @@ SIGNATURES = {
     "gdsllm_dequant_affine_q4": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp]),
     "gdsllm_fused_q4_0_gemv": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp]),
     "gdsllm_fused_q8_0_gemv": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp]),
+    "gdsllm_fused_q4_0_gemv_group": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(_c_vp), ctypes.POINTER(_c_vp), ctypes.POINTER(_c_i64), _c_vp, _c_i64, _c_i64, _c_i64, _c_vp]),
+    "gdsllm_fused_q8_0_gemv_group": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(_c_vp), ctypes.POINTER(_c_vp), ctypes.POINTER(_c_i64), _c_vp, _c_i64, _c_i64, _c_i64, _c_vp]),
+    "gdsllm_fused_q4_0_gate_up_silu": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp]),
+    "gdsllm_fused_q8_0_gate_up_silu": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp]),
     "gdsllm_fused_affine_q4_gemv": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp]),
     "gdsllm_moe_gather_workspace_size": (ctypes.c_size_t, [_c_i64, _c_i64]),
     "gdsllm_moe_gather_affine_q4": (ctypes.c_int, [ctypes.POINTER(AffineExperts)] * 3 + [_c_vp, _c_vp, _c_vp, _c_i64, _c_vp, _c_vp, ctypes.c_size_t, _c_vp]),

@@ -544,14 +544,6 @@ struct GateUpPairs {
 template <class Rows> struct IsGateUp { static constexpr bool value = false; };
 template <> struct IsGateUp<GateUpPairs> { static constexpr bool value = true; };
 
-__device__ __forceinline__ uint16_t silu_mul_h(float g, float u) {
-    // torch semantics on fp16 tensors: silu in fp32 rounded to fp16, then the
-    // fp16 product (computed in fp32, rounded once)
-    const float gh = h2f(f2h_bits(g));
-    const float sg = h2f(f2h_bits(gh / (1.0f + expf(-gh))));
-    return f2h_bits(sg * h2f(f2h_bits(u)));
-}
-
 template <int LR, int CPL, int NB, class Rows>
 __global__ __launch_bounds__(kThreads) void affine_rows(Rows rows, const uint16_t* __restrict__ X, int K, int gsize,
                                                         int64_t ldx, int x_al16) {

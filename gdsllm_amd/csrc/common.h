@@ -141,6 +141,20 @@ __device__ __forceinline__ float swap_sum16(float a, float b) {
     asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
     return a + b;
 }
+// The swap itself: afterwards a = [a lanes 0..31, b lanes 0..31] and
+// b = [a lanes 32..63, b lanes 32..63].
+__device__ __forceinline__ void swap32(float& a, float& b) {
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+
+// SwiGLU input h = silu(gate) * up with torch semantics on fp16 tensors: the
+// gate and up sums are fp16 values; silu is computed in fp32 and rounded to
+// fp16, then the fp16 product is computed in fp32 and rounded once.
+__device__ __forceinline__ uint16_t silu_mul_h(float g, float u) {
+    const float gh = h2f(f2h_bits(g));
+    const float sg = h2f(f2h_bits(gh / (1.0f + expf(-gh))));
+    return f2h_bits(sg * h2f(f2h_bits(u)));
+}
 
 // Sum over groups of `width` lanes (power of two <= 64).
 template <int WIDTH>

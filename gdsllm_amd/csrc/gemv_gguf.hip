@@ -466,35 +466,120 @@ __device__ __forceinline__ float reduce_rows4(const float (&acc)[4]) {
     return row16_sum(swap_sum16(k02, k13));
 }
 
+// Where a row-span launch reads weights and writes results.  Plain: up to 4
+// matrices of the same in_dim sharing x, each served by its own range of
+// workgroups (gb_end); row r of matrix m for batch row b goes to
+// y[m][b*ldy[m] + r].  Gate/up pairing: w[0] = gate, w[1] = up,
+// both m[0] rows; row group g holds gate rows 2g, 2g+1 (stage rows 0-1) and up
+// rows 2g, 2g+1 (stage rows 2-3), and y[0][b*ldy[0] + r] receives
+// h = fp16(silu(fp16 gate) * fp16 up), the SwiGLU input of the down projection.
+constexpr int kMaxGroup = 4;
+struct RowsTarget {
+    const uint8_t* w[kMaxGroup];
+    uint16_t* y[kMaxGroup];
+    int64_t ldy[kMaxGroup];
+    int m[kMaxGroup];
+    int gb_end[kMaxGroup];  // groups: workgroups [gb_end[i-1], gb_end[i]) serve matrix i
+    int n;
+};
+
+// One stage: stage row 0 of window super-block sb0 starts at base0 (pairing:
+// rows 0-1 at base0, rows 2-3 at base1), nrows valid rows (per matrix when
+// paired), nsb super-blocks.
+struct RowsStage {
+    const uint8_t* base0;
+    const uint8_t* base1;
+    uint16_t* y;
+    int64_t ldy;
+    int r0, nrows, nsb, seg_chunks;
+};
+
+// The fields of this workgroup's matrix (pair), copied once into SGPRs (an
+// empty asm pins them there; otherwise the compiler re-reads the kernel
+// argument inside the loop and waits for it).  first_block/blocks: this
+// matrix's workgroup range.
+struct TargetRegs {
+    const uint8_t *w0, *w1;
+    uint16_t* y;
+    int64_t ldy;
+    int m, first_block, blocks;
+    // MODE 0: one matrix; 1: a group (matrix chosen by workgroup); 2: gate/up.
+    template <int MODE>
+    __device__ __forceinline__ void load(const RowsTarget& tg) {
+        if constexpr (MODE != 1) {
+            w0 = tg.w[0], w1 = MODE == 2 ? tg.w[1] : tg.w[0], y = tg.y[0], ldy = tg.ldy[0], m = tg.m[0];
+            first_block = 0;
+            blocks = gridDim.x;
+        } else {
+            const int bx = blockIdx.x;
+            const int i = (tg.n > 1 && bx >= tg.gb_end[0]) + (tg.n > 2 && bx >= tg.gb_end[1]) +
+                          (tg.n > 3 && bx >= tg.gb_end[2]);
+            switch (i) {
+                case 0: w0 = tg.w[0], y = tg.y[0], ldy = tg.ldy[0], m = tg.m[0], first_block = 0; break;
+                case 1: w0 = tg.w[1], y = tg.y[1], ldy = tg.ldy[1], m = tg.m[1], first_block = tg.gb_end[0]; break;
+                case 2: w0 = tg.w[2], y = tg.y[2], ldy = tg.ldy[2], m = tg.m[2], first_block = tg.gb_end[1]; break;
+                default: w0 = tg.w[3], y = tg.y[3], ldy = tg.ldy[3], m = tg.m[3], first_block = tg.gb_end[2]; break;
+            }
+            blocks = (i == 0 ? tg.gb_end[0] : i == 1 ? tg.gb_end[1] : i == 2 ? tg.gb_end[2] : tg.gb_end[3]) -
+                     first_block;
+            w1 = w0;
+        }
+        asm volatile("" : "+s"(w0), "+s"(w1), "+s"(y), "+s"(ldy), "+s"(m), "+s"(first_block), "+s"(blocks));
+    }
+};
+
+template <Fmt F, bool PAIRED>
+__device__ __forceinline__ RowsStage rows_stage(const TargetRegs& tg, int rg, int win, int S, uint32_t row_bytes) {
+    using L = Layout<F>;
+    RowsStage st;
+    const int sb0 = win * kSbPerWindow;
+    st.nsb = min(kSbPerWindow, S - sb0);
+    st.seg_chunks = st.nsb * L::kSbChunks;
+    const int64_t col = static_cast<int64_t>(sb0) * L::kSbBytes;
+    st.r0 = (PAIRED ? 2 : kRowsPerStage) * rg;
+    st.nrows = min(PAIRED ? 2 : kRowsPerStage, tg.m - st.r0);
+    st.base0 = tg.w0 + st.r0 * static_cast<int64_t>(row_bytes) + col;
+    st.base1 = tg.w1 + st.r0 * static_cast<int64_t>(row_bytes) + col;
+    st.y = tg.y;
+    st.ldy = tg.ldy;
+    return st;
+}
+
 // Stage transfers, global memory straight to LDS.  Slot s = 64j + lane of a
 // wave's stage buffer (bytes [16s, 16s+16)) holds chunk s % kSegChunks of the
 // stage's row s / kSegChunks, so the rows of a stage sit kSegBytes apart in LDS
-// whatever its width.  A full stage (4 rows x 16 super-blocks) has the same
-// per-lane offsets every time (goff, computed once); a partial one (the last
-// rows of M, the last window of a row) points the slots it does not cover at
-// its first chunk.  `live == false` sends every slot to the first 16 bytes of
-// x, a dummy transfer that keeps each wave's count of transfers fixed.
-// Transfers [J0, J1) of the stage; offsets stay in 32 bits: in_dim <= 2^20.
-template <Fmt F, int J0, int J1>
-__device__ __forceinline__ void rows_issue(uint8_t* buf, const uint8_t* __restrict__ W, const void* dummy,
-                                           uint32_t row_bytes, const uint32_t (&goff)[Layout<F>::kSbChunks],
-                                           const Stage& st, bool live, int lane) {
+// whatever its width.  A full stage (16 super-blocks, every row valid) has the
+// same per-lane offsets every time (goff, computed once; with pairing, bit 31
+// selects base1); a partial one (the last rows, the last window of a row)
+// points the slots it does not cover at its first chunk.  `live == false`
+// sends every slot to the first 16 bytes of x, a dummy transfer that keeps
+// each wave's count of transfers fixed.  Transfers [J0, J1) of the stage;
+// offsets stay in 32 bits: in_dim <= 2^20.
+template <Fmt F, int J0, int J1, bool PAIRED>
+__device__ __forceinline__ void rows_issue(uint8_t* buf, const RowsStage& st, const void* dummy, uint32_t row_bytes,
+                                           const uint32_t (&goff)[Layout<F>::kSbChunks], bool live, int lane) {
     using L = Layout<F>;
     constexpr int kSegChunks = kSbPerWindow * L::kSbChunks;
-    const uint8_t* base = W + static_cast<int64_t>(st.r0) * row_bytes + st.sb0 * L::kSbBytes;
     if (!live) {
 #pragma unroll
         for (int j = J0; j < J1; ++j) dma16(dummy, buf + 1024 * j);
-    } else if (st.nrows == kRowsPerStage && st.nsb == kSbPerWindow) {
+    } else if (st.nrows == (PAIRED ? 2 : kRowsPerStage) && st.nsb == kSbPerWindow) {
 #pragma unroll
-        for (int j = J0; j < J1; ++j) dma16(base + goff[j], buf + 1024 * j);
+        for (int j = J0; j < J1; ++j) {
+            if constexpr (PAIRED)
+                dma16(((goff[j] >> 31) ? st.base1 : st.base0) + (goff[j] & 0x7FFFFFFFu), buf + 1024 * j);
+            else
+                dma16(st.base0 + goff[j], buf + 1024 * j);
+        }
     } else {
 #pragma unroll
         for (int j = J0; j < J1; ++j) {
             const uint32_t s = 64 * j + lane;
             const uint32_t rl = s / kSegChunks, off = s - rl * kSegChunks;
-            const bool in = rl < static_cast<uint32_t>(st.nrows) && off < static_cast<uint32_t>(st.seg_chunks);
-            dma16(base + (in ? __umul24(rl, row_bytes) + 16 * off : 0u), buf + 1024 * j);
+            const uint32_t rr = PAIRED ? (rl & 1) : rl;  // row within its matrix
+            const bool in = rr < static_cast<uint32_t>(st.nrows) && off < static_cast<uint32_t>(st.seg_chunks);
+            const uint8_t* base = (PAIRED && rl >= 2) ? st.base1 : st.base0;
+            dma16(base + (in ? __umul24(rr, row_bytes) + 16 * off : 0u), buf + 1024 * j);
         }
     }
 }
@@ -552,15 +637,15 @@ __device__ __forceinline__ void rows_pair(const uint8_t* buf, const XSlice<NB>& 
     }
 }
 
-// x must be 16-byte aligned with ldx % 8 == 0.  Workgroups of kWaves waves;
-// LDS (dynamic): the waves' stage buffers, then raw x.  One buffer per wave: after rows 0-1 of a stage are consumed, the next
+// Rows of `target` times x (MODE 0: one matrix; 1: a group; 2: gate/up pairs); x must be 16-byte aligned
+// with ldx % 8 == 0.  Workgroups of kWaves waves; LDS (dynamic): the waves'
+// stage buffers, then raw x.  One buffer per wave: after rows 0-1 of a stage are consumed, the next
 // stage's transfers that land in their slots only (kEarly) are issued, the
 // rest after rows 2-3.
-template <Fmt F, int NB>
-__global__ __launch_bounds__(kWaves * 64) void gguf_gemv_rows(const uint8_t* __restrict__ W,
-                                                              const uint16_t* __restrict__ X,
-                                                              uint16_t* __restrict__ Y, int M, int K, int64_t ldx,
-                                                              int64_t ldy) {
+template <Fmt F, int NB, int MODE>
+__global__ __launch_bounds__(kWaves * 64) void gguf_gemv_rows(const RowsTarget target, const uint16_t* __restrict__ X,
+                                                              int K, int64_t ldx) {
+    constexpr bool PAIRED = MODE == 2;
     using L = Layout<F>;
     constexpr int C = L::kSbChunks;                        // transfers per stage
     constexpr int kSegChunks = kSbPerWindow * L::kSbChunks;
@@ -573,21 +658,24 @@ __global__ __launch_bounds__(kWaves * 64) void gguf_gemv_rows(const uint8_t* __r
     const int lane = threadIdx.x & 63;
     uint8_t* buf = lds + wave * stage_bytes<F>();
     uint8_t* xp = lds + kWaves * stage_bytes<F>();
-    const int RG = (M + kRowsPerStage - 1) / kRowsPerStage;
+    TargetRegs tg;
+    tg.load<MODE>(target);
+    const int RG = (tg.m + (PAIRED ? 1 : kRowsPerStage - 1)) / (PAIRED ? 2 : kRowsPerStage);
     const int NW = (S + kSbPerWindow - 1) / kSbPerWindow;
-    const int total_waves = gridDim.x * kWaves;
-    const int gw = blockIdx.x * kWaves + wave;
+    const int total_waves = tg.blocks * kWaves;
+    const int gw = (blockIdx.x - tg.first_block) * kWaves + wave;
     const int my_rgs = gw < RG ? (RG - 1 - gw) / total_waves + 1 : 0;
     const int T = my_rgs * NW;
     const NibUnpack nu;
-    auto stage_at = [&](int t) { return make_stage<F>(gw + (t / NW) * total_waves, t % NW, M, S); };
+    auto stage_at = [&](int t) { return rows_stage<F, PAIRED>(tg, gw + (t / NW) * total_waves, t % NW, S, row_bytes); };
 
     uint32_t goff[C];
 #pragma unroll
     for (int j = 0; j < C; ++j) {
         const uint32_t c = 64 * j + lane;
         const uint32_t rl = c / kSegChunks;
-        goff[j] = rl * row_bytes + 16 * (c - rl * kSegChunks);
+        const uint32_t rr = PAIRED ? (rl & 1) : rl;
+        goff[j] = ((PAIRED && rl >= 2) ? 0x80000000u : 0u) | (rr * row_bytes + 16 * (c - rl * kSegChunks));
     }
 
     // Request order: raw x, then the first stage of weights (always issued,
@@ -596,7 +684,7 @@ __global__ __launch_bounds__(kWaves * 64) void gguf_gemv_rows(const uint8_t* __r
     // order, so every wave's x is requested before any wave's weights.
     rows_xraw_issue<NB>(xp, X, ldx, K, NW, wave, kWaves, lane);
     __builtin_amdgcn_s_barrier();
-    rows_issue<F, 0, C>(buf, W, X, row_bytes, goff, stage_at(0), T > 0, lane);
+    rows_issue<F, 0, C, PAIRED>(buf, stage_at(0), X, row_bytes, goff, T > 0, lane);
     wait_vmcnt<C>();
     lds_barrier();  // every wave's share of x has landed
 
@@ -611,7 +699,7 @@ __global__ __launch_bounds__(kWaves * 64) void gguf_gemv_rows(const uint8_t* __r
 
     for (int t = 0; t < T; ++t) {
         const int win = t % NW;
-        const Stage st = stage_at(t);
+        const RowsStage st = stage_at(t);
         const bool next = t + 1 < T;
         if (win != xwin) {
             load_slice<F, NB>(xs, xp, NW, win, lane);
@@ -624,22 +712,30 @@ __global__ __launch_bounds__(kWaves * 64) void gguf_gemv_rows(const uint8_t* __r
         if (active) rows_pair<F, NB, 0>(buf, xs, acc, nu, lane);
         // refill slots of rows 0-1 once their reads have returned
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        const Stage nx = stage_at(t + 1);
+        const RowsStage nx = stage_at(t + 1);
         if (next) {
-            rows_issue<F, 0, kEarly>(buf, W, X, row_bytes, goff, nx, true, lane);
+            rows_issue<F, 0, kEarly, PAIRED>(buf, nx, X, row_bytes, goff, true, lane);
             wait_vmcnt<kEarly>();
         } else {
             wait_vmcnt<0>();
         }
         if (active) rows_pair<F, NB, 2>(buf, xs, acc, nu, lane);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        if (next) rows_issue<F, kEarly, C>(buf, W, X, row_bytes, goff, nx, true, lane);
+        if (next) rows_issue<F, kEarly, C, PAIRED>(buf, nx, X, row_bytes, goff, true, lane);
         if (win == NW - 1) {
             const int row = lane >> 4;
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
                 const float v = reduce_rows4(acc[b]);
-                if ((lane & 15) == 0 && row < st.nrows) Y[b * ldy + st.r0 + row] = f2h_bits(v);
+                if constexpr (PAIRED) {
+                    // lanes 0-31: gate rows r0, r0+1 in g, the matching up rows in u
+                    float g = v, u = v;
+                    swap32(g, u);
+                    if (lane < 32 && (lane & 15) == 0 && row < st.nrows)
+                        st.y[b * st.ldy + st.r0 + row] = silu_mul_h(g, u);
+                } else {
+                    if ((lane & 15) == 0 && row < st.nrows) st.y[b * st.ldy + st.r0 + row] = f2h_bits(v);
+                }
 #pragma unroll
                 for (int r = 0; r < 4; ++r) acc[b][r] = 0.f;
             }
@@ -942,42 +1038,98 @@ int launch_staged(const void* w, const uint16_t* x, uint16_t* y, int M, int K, i
 // Measured on MI355X: two stage buffers per wave, or workgroups filling a
 // compute unit on their own, lose to more 4-wave workgroups at one buffer
 // each.  Returns false when no geometry fits (the caller takes another kernel).
-template <Fmt F, int NB>
-bool plan_rows(int M, int K, int& grid) {
+// Sets tg.gb_end: workgroups per matrix, as many as its row groups need while
+// all fit at once, else the resident count shared in proportion to row groups.
+template <Fmt F, int NB, int MODE>
+bool plan_rows(RowsTarget& tg, int K, int& grid) {
+    constexpr bool PAIRED = MODE == 2;
     const int NW = ((K >> 8) + kSbPerWindow - 1) / kSbPerWindow;
-    const int RG = (M + kRowsPerStage - 1) / kRowsPerStage;
     const size_t lds = rows_lds_bytes<F, NB>(NW, kWaves);
     if (lds > static_cast<size_t>(max_lds_bytes())) return false;
-    const void* fn = reinterpret_cast<const void*>(&gguf_gemv_rows<F, NB>);
+    const void* fn = reinterpret_cast<const void*>(&gguf_gemv_rows<F, NB, MODE>);
     if (prepare_lds(fn, lds) != GDSLLM_OK) return false;
-    grid = std::min((RG + kWaves - 1) / kWaves, blocks_per_cu(fn, lds, kWaves * 64) * cu_count());
-    return true;
+    const int resident = blocks_per_cu(fn, lds, kWaves * 64) * cu_count();
+    const int parts = PAIRED ? 1 : tg.n;
+    int need[kMaxGroup], total = 0, rg_all = 0;
+    for (int i = 0; i < parts; ++i) {
+        const int rg = PAIRED ? (tg.m[0] + 1) / 2 : (tg.m[i] + kRowsPerStage - 1) / kRowsPerStage;
+        need[i] = (rg + kWaves - 1) / kWaves;
+        total += need[i];
+        rg_all += rg;
+    }
+    grid = 0;
+    for (int i = 0; i < parts; ++i) {
+        int g = need[i];
+        if (total > resident) {
+            const int rg = PAIRED ? (tg.m[0] + 1) / 2 : (tg.m[i] + kRowsPerStage - 1) / kRowsPerStage;
+            g = std::max(rg > 0 ? 1 : 0, static_cast<int>(static_cast<int64_t>(resident) * rg / rg_all));
+            g = std::min(g, need[i]);
+        }
+        grid += g;
+        tg.gb_end[i] = grid;
+    }
+    for (int i = parts; i < kMaxGroup; ++i) tg.gb_end[i] = grid;
+    return grid > 0;
 }
 
-template <Fmt F, int NB>
-int launch_rows(const void* w, const uint16_t* x, uint16_t* y, int M, int K, int64_t ldx, int64_t ldy, int grid,
-                hipStream_t stream) {
+template <Fmt F, int NB, int MODE>
+int launch_rows(const RowsTarget& tg, const uint16_t* x, int K, int64_t ldx, int grid, hipStream_t stream) {
     const int NW = ((K >> 8) + kSbPerWindow - 1) / kSbPerWindow;
     const size_t lds = rows_lds_bytes<F, NB>(NW, kWaves);
-    hipLaunchKernelGGL((gguf_gemv_rows<F, NB>), dim3(grid), dim3(kWaves * 64), lds, stream,
-                       static_cast<const uint8_t*>(w), x, y, M, K, ldx, ldy);
+    hipLaunchKernelGGL((gguf_gemv_rows<F, NB, MODE>), dim3(grid), dim3(kWaves * 64), lds, stream, tg, x, K, ldx);
     return check_hip(hipGetLastError(), "gguf_gemv launch");
 }
 
-template <Fmt F>
-int gemv(const char* name, const void* w, const void* x, void* y, int64_t out_dim, int64_t in_dim,
-         int64_t batch, int64_t ldx, int64_t ldy, void* stream) {
-    const std::string n(name);
+// The row-span kernel serves batch <= 2 with in_dim % 256 == 0 (in_dim <=
+// 2^20), 16-byte aligned weights, x 16-byte aligned with ldx % 8 == 0.
+// Returns GDSLLM_OK after launching, -1 when the request does not qualify (or
+// no geometry fits), else an error code.
+template <Fmt F, int MODE>
+int try_rows(RowsTarget tg, const void* x, int K, int64_t batch, int64_t ldx, hipStream_t s) {
+    bool w_al16 = true;
+    for (int i = 0; i < tg.n; ++i) w_al16 = w_al16 && reinterpret_cast<uintptr_t>(tg.w[i]) % 16 == 0;
+    const bool x_al16 = reinterpret_cast<uintptr_t>(x) % 16 == 0 && (ldx % 8 == 0 || batch == 1);
+    if (batch > 2 || K % 256 != 0 || K > (1 << 20) || !w_al16 || !x_al16) return -1;
+    const auto* xp = static_cast<const uint16_t*>(x);
+    int grid = 0;
+    if (batch == 1) {
+        if (!plan_rows<F, 1, MODE>(tg, K, grid)) return -1;
+        return launch_rows<F, 1, MODE>(tg, xp, K, ldx, grid, s);
+    }
+    if (!plan_rows<F, 2, MODE>(tg, K, grid)) return -1;
+    return launch_rows<F, 2, MODE>(tg, xp, K, ldx, grid, s);
+}
+
+RowsTarget single_target(const void* w, void* y, int M, int64_t ldy) {
+    RowsTarget tg{};
+    tg.w[0] = static_cast<const uint8_t*>(w);
+    tg.y[0] = static_cast<uint16_t*>(y);
+    tg.ldy[0] = ldy;
+    tg.m[0] = M;
+    tg.n = 1;
+    return tg;
+}
+
+// Shape checks shared by the GEMV entry points.
+int check_gemv_args(const std::string& n, int64_t out_dim, int64_t in_dim, int64_t batch) {
     if (out_dim < 0 || in_dim < 0) return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": negative dimension");
     if (in_dim % 32 != 0)
         return set_error(GDSLLM_ERR_INVALID_ARGUMENT,
                          n + ": in_dim must be a multiple of 32, got " + std::to_string(in_dim));
     if (batch < 1 || batch > 8)
         return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": batch must be in [1, 8], got " + std::to_string(batch));
-    if (out_dim == 0 || in_dim == 0) return ok();  // silent no-op, as the reference launchers
-    if (!w || !x || !y) return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": null pointer");
     if (out_dim > (int64_t(1) << 30) || in_dim > (int64_t(1) << 24))
         return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": dimension too large");
+    return GDSLLM_OK;
+}
+
+template <Fmt F>
+int gemv(const char* name, const void* w, const void* x, void* y, int64_t out_dim, int64_t in_dim,
+         int64_t batch, int64_t ldx, int64_t ldy, void* stream) {
+    const std::string n(name);
+    if (int rc = check_gemv_args(n, out_dim, in_dim, batch)) return rc;
+    if (out_dim == 0 || in_dim == 0) return ok();  // silent no-op, as the reference launchers
+    if (!w || !x || !y) return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": null pointer");
     if (batch > 1 && (ldx < in_dim || ldy < out_dim))
         return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": ldx/ldy smaller than the row length");
     if (reinterpret_cast<uintptr_t>(x) % 2 || reinterpret_cast<uintptr_t>(y) % 2)
@@ -987,15 +1139,10 @@ int gemv(const char* name, const void* w, const void* x, void* y, int64_t out_di
     const auto* xp = static_cast<const uint16_t*>(x);
     auto* yp = static_cast<uint16_t*>(y);
     const bool fast = (K % 256 == 0) && (reinterpret_cast<uintptr_t>(w) % 16 == 0);
-    int rc = GDSLLM_OK;
-    const bool x_al16 = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (ldx % 8 == 0 || batch == 1);
-    int rgrid = 0;
-    if (fast && batch <= 2 && K <= (1 << 20) && x_al16 &&
-        (batch == 1 ? plan_rows<F, 1>(M, K, rgrid) : plan_rows<F, 2>(M, K, rgrid))) {
-        rc = batch == 1 ? launch_rows<F, 1>(w, xp, yp, M, K, ldx, ldy, rgrid, s)
-                        : launch_rows<F, 2>(w, xp, yp, M, K, ldx, ldy, rgrid, s);
-        return rc == GDSLLM_OK ? ok() : rc;
-    }
+    int rc = try_rows<F, 0>(single_target(w, y, M, ldy), x, K, batch, ldx, s);
+    if (rc != -1) return rc == GDSLLM_OK ? ok() : rc;
+    rc = GDSLLM_OK;
+    const bool x_al16 = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (ldx % 8 == 0);
     if (fast && batch >= 5 && K <= (1 << 20) && x_al16) {
         const size_t lds = static_cast<size_t>(kMfmaWaves) * mfma_stage_bytes<F>();
         const void* fn = reinterpret_cast<const void*>(&gguf_gemv_mfma<F>);
@@ -1039,10 +1186,96 @@ int gemv(const char* name, const void* w, const void* x, void* y, int64_t out_di
     return ok();
 }
 
+// n matrices sharing x (q/k/v of one layer): one launch when the row-span
+// kernel serves the shape, else one GEMV per matrix.
+template <Fmt F>
+int gemv_group(const char* name, int n, const void* const* w, void* const* y, const int64_t* out_dims,
+               const void* x, int64_t in_dim, int64_t batch, int64_t ldx, void* stream) {
+    const std::string nm(name);
+    if (n < 1 || n > kMaxGroup)
+        return set_error(GDSLLM_ERR_INVALID_ARGUMENT, nm + ": n must be in [1, 4], got " + std::to_string(n));
+    if (!w || !y || !out_dims) return set_error(GDSLLM_ERR_INVALID_ARGUMENT, nm + ": null pointer");
+    RowsTarget tg{};
+    tg.n = n;
+    bool any = false;
+    for (int i = 0; i < n; ++i) {
+        if (int rc = check_gemv_args(nm, out_dims[i], in_dim, batch)) return rc;
+        if (out_dims[i] > 0 && in_dim > 0 && (!w[i] || !y[i] || !x))
+            return set_error(GDSLLM_ERR_INVALID_ARGUMENT, nm + ": null pointer");
+        if (reinterpret_cast<uintptr_t>(y[i]) % 2) return set_error(GDSLLM_ERR_INVALID_ARGUMENT, nm + ": y must be 2-byte aligned");
+        any = any || out_dims[i] > 0;
+        tg.w[i] = static_cast<const uint8_t*>(w[i]);
+        tg.y[i] = static_cast<uint16_t*>(y[i]);
+        tg.ldy[i] = out_dims[i];
+        tg.m[i] = static_cast<int>(out_dims[i]);
+    }
+    if (!any || in_dim == 0) return ok();
+    if (batch > 1 && ldx < in_dim) return set_error(GDSLLM_ERR_INVALID_ARGUMENT, nm + ": ldx smaller than in_dim");
+    if (reinterpret_cast<uintptr_t>(x) % 2) return set_error(GDSLLM_ERR_INVALID_ARGUMENT, nm + ": x must be 2-byte aligned");
+    const int rc = n == 1 ? try_rows<F, 0>(tg, x, static_cast<int>(in_dim), batch, ldx, as_stream(stream))
+                          : try_rows<F, 1>(tg, x, static_cast<int>(in_dim), batch, ldx, as_stream(stream));
+    if (rc != -1) return rc == GDSLLM_OK ? ok() : rc;
+    for (int i = 0; i < n; ++i)
+        if (int e = gemv<F>(name, w[i], x, y[i], out_dims[i], in_dim, batch, ldx, out_dims[i], stream)) return e;
+    return ok();
+}
+
+// h = fp16(silu(gate x) * (up x)) in one launch (the row-span kernel with
+// gate/up pairing).
+template <Fmt F>
+int gate_up_silu(const char* name, const void* w_gate, const void* w_up, const void* x, void* h, int64_t out_dim,
+                 int64_t in_dim, int64_t batch, int64_t ldx, int64_t ldh, void* stream) {
+    const std::string nm(name);
+    if (int rc = check_gemv_args(nm, out_dim, in_dim, batch)) return rc;
+    if (out_dim == 0 || in_dim == 0) return ok();
+    if (!w_gate || !w_up || !x || !h) return set_error(GDSLLM_ERR_INVALID_ARGUMENT, nm + ": null pointer");
+    if (batch > 1 && (ldx < in_dim || ldh < out_dim))
+        return set_error(GDSLLM_ERR_INVALID_ARGUMENT, nm + ": ldx/ldh smaller than the row length");
+    if (reinterpret_cast<uintptr_t>(h) % 2) return set_error(GDSLLM_ERR_INVALID_ARGUMENT, nm + ": h must be 2-byte aligned");
+    RowsTarget tg{};
+    tg.n = 2;
+    tg.w[0] = static_cast<const uint8_t*>(w_gate);
+    tg.w[1] = static_cast<const uint8_t*>(w_up);
+    tg.y[0] = static_cast<uint16_t*>(h);
+    tg.ldy[0] = ldh;
+    tg.m[0] = tg.m[1] = static_cast<int>(out_dim);
+    const int rc = try_rows<F, 2>(tg, x, static_cast<int>(in_dim), batch, ldx, as_stream(stream));
+    if (rc == -1)
+        return set_error(GDSLLM_ERR_UNSUPPORTED,
+                         nm + ": needs batch <= 2, in_dim % 256 == 0, 16-byte aligned weights and x (ldx % 8 == 0)");
+    return rc == GDSLLM_OK ? ok() : rc;
+}
+
 }  // namespace
 }  // namespace gdsllm
 
 using namespace gdsllm;
+
+extern "C" int gdsllm_fused_q4_0_gemv_group(int n, const void* const* weights, void* const* ys,
+                                            const int64_t* out_dims, const void* x, int64_t in_dim, int64_t batch,
+                                            int64_t ldx, void* stream) {
+    return gemv_group<Fmt::Q4_0>("fused_q4_0_gemv_group", n, weights, ys, out_dims, x, in_dim, batch, ldx, stream);
+}
+
+extern "C" int gdsllm_fused_q8_0_gemv_group(int n, const void* const* weights, void* const* ys,
+                                            const int64_t* out_dims, const void* x, int64_t in_dim, int64_t batch,
+                                            int64_t ldx, void* stream) {
+    return gemv_group<Fmt::Q8_0>("fused_q8_0_gemv_group", n, weights, ys, out_dims, x, in_dim, batch, ldx, stream);
+}
+
+extern "C" int gdsllm_fused_q4_0_gate_up_silu(const void* w_gate, const void* w_up, const void* x, void* h,
+                                              int64_t out_dim, int64_t in_dim, int64_t batch, int64_t ldx,
+                                              int64_t ldh, void* stream) {
+    return gate_up_silu<Fmt::Q4_0>("fused_q4_0_gate_up_silu", w_gate, w_up, x, h, out_dim, in_dim, batch, ldx, ldh,
+                                   stream);
+}
+
+extern "C" int gdsllm_fused_q8_0_gate_up_silu(const void* w_gate, const void* w_up, const void* x, void* h,
+                                              int64_t out_dim, int64_t in_dim, int64_t batch, int64_t ldx,
+                                              int64_t ldh, void* stream) {
+    return gate_up_silu<Fmt::Q8_0>("fused_q8_0_gate_up_silu", w_gate, w_up, x, h, out_dim, in_dim, batch, ldx, ldh,
+                                   stream);
+}
 
 extern "C" int gdsllm_fused_q4_0_gemv(const void* weight, const void* x, void* y, int64_t out_dim,
                                       int64_t in_dim, int64_t batch, int64_t ldx, int64_t ldy, void* stream) {

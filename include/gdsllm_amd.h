@@ -92,6 +92,34 @@ int gdsllm_fused_q4_0_gemv(const void* weight, const void* x, void* y,
 int gdsllm_fused_q8_0_gemv(const void* weight, const void* x, void* y,
                            int64_t out_dim, int64_t in_dim, int64_t batch,
                            int64_t ldx, int64_t ldy, void* stream);
+/* ----------------------------------------------------- decode-step fusions --
+ * No counterpart in the reference, which issues one dequant_linear per
+ * projection: q/k/v of one layer read the same x (runtime/llama.py:212-214),
+ * and the MLP computes F.silu(gate) * up before the down projection
+ * (runtime/llama.py:253-256).  For decode loops that want fewer launches.     */
+
+/* n (1..4) GEMVs sharing x and in_dim in one launch: ys[i] receives
+ * fp16[batch][out_dims[i]] (row-contiguous) = W_i x.  Same numerics as
+ * gdsllm_fused_q4_0_gemv / gdsllm_fused_q8_0_gemv on each matrix; shapes the
+ * single-launch kernel does not serve fall back to one launch per matrix.    */
+int gdsllm_fused_q4_0_gemv_group(int n, const void* const* weights, void* const* ys,
+                                 const int64_t* out_dims, const void* x, int64_t in_dim,
+                                 int64_t batch, int64_t ldx, void* stream);
+int gdsllm_fused_q8_0_gemv_group(int n, const void* const* weights, void* const* ys,
+                                 const int64_t* out_dims, const void* x, int64_t in_dim,
+                                 int64_t batch, int64_t ldx, void* stream);
+/* h[b][r] = fp16(silu(g) * u) with g = fp16((W_gate x_b)[r]), u = fp16((W_up x_b)[r])
+ * and torch's fp16 semantics (silu in fp32 rounded to fp16, then the product
+ * rounded to fp16), in one launch; gate and up outputs never reach memory.
+ * Needs batch <= 2, in_dim % 256 == 0, 16-byte aligned weights and x with
+ * ldx % 8 == 0 (else GDSLLM_ERR_UNSUPPORTED).                                */
+int gdsllm_fused_q4_0_gate_up_silu(const void* w_gate, const void* w_up, const void* x, void* h,
+                                   int64_t out_dim, int64_t in_dim, int64_t batch, int64_t ldx,
+                                   int64_t ldh, void* stream);
+int gdsllm_fused_q8_0_gate_up_silu(const void* w_gate, const void* w_up, const void* x, void* h,
+                                   int64_t out_dim, int64_t in_dim, int64_t batch, int64_t ldx,
+                                   int64_t ldh, void* stream);
+
 /* Replaces launch_fused_affine_q4_gemv (runtime/affine_q4_dequant.h:41-44,
  * runtime/affine_q4_dequant.cu:160-187).                                     */
 int gdsllm_fused_affine_q4_gemv(const void* weight, const void* scales, const void* biases,

@@ -93,6 +93,34 @@ def test_dequant_validation():
     assert a(None, None, None, None, 0, 64, 64, None) == 0
 
 
+def test_gemv_group_validation():
+    lib = capi()
+    for name in ("gdsllm_fused_q4_0_gemv_group", "gdsllm_fused_q8_0_gemv_group"):
+        fn = getattr(lib, name)
+        w = (ctypes.c_void_p * 5)(*([16] * 5))
+        y = (ctypes.c_void_p * 5)(*([16] * 5))
+        dims = (ctypes.c_int64 * 5)(*([4] * 5))
+        assert fn(0, w, y, dims, 16, 64, 1, 64, None) == 1 and "n must be" in _err()
+        assert fn(5, w, y, dims, 16, 64, 1, 64, None) == 1
+        assert fn(2, None, y, dims, 16, 64, 1, 64, None) == 1 and "null" in _err()
+        assert fn(2, w, y, dims, 16, 48, 1, 48, None) == 1 and "multiple of 32" in _err()
+        assert fn(2, w, y, dims, 16, 64, 9, 64, None) == 1 and "batch" in _err()
+        zero = (ctypes.c_int64 * 2)(0, 0)
+        assert fn(2, w, y, zero, 16, 64, 1, 64, None) == 0  # nothing to compute
+
+
+def test_gate_up_silu_validation():
+    lib = capi()
+    for name in ("gdsllm_fused_q4_0_gate_up_silu", "gdsllm_fused_q8_0_gate_up_silu"):
+        fn = getattr(lib, name)
+        assert fn(16, 16, 16, 16, 4, 48, 1, 48, 4, None) == 1 and "multiple of 32" in _err()
+        assert fn(None, 16, 16, 16, 4, 256, 1, 256, 4, None) == 1 and "null" in _err()
+        assert fn(16, 16, 16, 16, 4, 256, 3, 256, 4, None) == 2 and "batch <= 2" in _err()
+        assert fn(16, 16, 18, 16, 4, 256, 1, 256, 4, None) == 2  # x off the 16-byte grid
+        assert fn(16, 16, 16, 16, 4, 96, 1, 96, 4, None) == 2  # in_dim % 256 != 0
+        assert fn(None, None, None, None, 0, 256, 1, 256, 0, None) == 0
+
+
 def test_gemm_validation():
     g = capi().gdsllm_dequant_gemm_q4_0
     assert g(16, 16, 16, 4, 96, 2, 96, 4, None) == 2 and "multiple of 64" in _err()

@@ -133,3 +133,71 @@ def test_capi_rejects_bad_shapes_before_launch(gpu):
     assert lib.gdsllm_fused_affine_q4_gemv(ptr(y), ptr(y), ptr(y), ptr(y), ptr(y), 4, 96, 64, 1, 96, 4, stream()) == 1
     # zero-sized problems are no-ops, as in the reference launchers
     assert lib.gdsllm_fused_q4_0_gemv(None, None, None, 0, 64, 1, 64, 0, stream()) == 0
+
+
+GROUP_CASES = [((256, 64, 64), 512, 1), ((4096, 1024, 1024), 4096, 1), ((33, 7, 129), 1024, 2), ((100,), 256, 1),
+               ((8, 16, 24, 40), 2048, 2), ((5, 0, 9), 512, 1)]
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("Ms,K,B", GROUP_CASES, ids=[f"{'-'.join(map(str, m))}x{k}_b{b}" for m, k, b in GROUP_CASES])
+def test_gemv_group(gpu, fmt, Ms, K, B):
+    """n matrices sharing x in one call: each output matches the oracle, and is
+    bit-identical to the single-matrix GEMV of the same matrix (the rows of a
+    group are computed exactly like the rows of one matrix)."""
+    import ctypes
+
+    make = syn.q4_0_weights if fmt == "q4_0" else syn.q8_0_weights
+    dq = oq.dequant_q4_0 if fmt == "q4_0" else oq.dequant_q8_0
+    ws = [make(M, K, gen(6000 + 17 * i + M)) if M else torch.empty(0, dtype=torch.uint8) for i, M in enumerate(Ms)]
+    x = syn.activations(B, K, gen(6100 + K + B))
+    xd = x.to(gpu)
+    wd = [w.to(gpu) for w in ws]
+    ys = [torch.full((B, max(M, 1)), 7.0, dtype=torch.float16, device=gpu) for M in Ms]
+    n = len(Ms)
+    fn = capi().gdsllm_fused_q4_0_gemv_group if fmt == "q4_0" else capi().gdsllm_fused_q8_0_gemv_group
+    arr_w = (ctypes.c_void_p * n)(*[ptr(w) if M else None for w, M in zip(wd, Ms)])
+    arr_y = (ctypes.c_void_p * n)(*[ptr(y) for y in ys])
+    dims = (ctypes.c_int64 * n)(*Ms)
+    check(fn(n, arr_w, arr_y, dims, ptr(xd), K, B, K, stream()))
+    torch.cuda.synchronize()
+    for i, M in enumerate(Ms):
+        if M == 0:
+            assert np.all(to_np(ys[i]) == 7.0), "an empty matrix must not be written"
+            continue
+        y = to_np(ys[i])
+        assert_gemv_close(y, dq(to_np(ws[i])).reshape(M, K), to_np(x), f"{fmt} group[{i}] {M}x{K} B{B}")
+        assert np.array_equal(y, to_np(gguf_gemv(fmt, wd[i], xd, M, K))), f"group[{i}] differs from the single GEMV"
+
+
+GATE_UP_CASES = [(300, 1024, 1), (11008, 4096, 1), (7, 256, 2), (1025, 2048, 2), (4096, 11008, 1), (16001, 1024, 1)]
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("M,K,B", GATE_UP_CASES, ids=[f"{m}x{k}_b{b}" for m, k, b in GATE_UP_CASES])
+def test_gate_up_silu(gpu, fmt, M, K, B):
+    """h = fp16(silu(g) * u) in one call.  (1) Against g, u from the single
+    GEMV (same per-row sums, bit for bit): h within one fp16 ulp of silu times
+    |u| plus one ulp of h, the room the device's expf leaves against numpy's.
+    (2) End to end against the oracle's g, u: relative L2 of h."""
+    make = syn.q4_0_weights if fmt == "q4_0" else syn.q8_0_weights
+    dq = oq.dequant_q4_0 if fmt == "q4_0" else oq.dequant_q8_0
+    wg, wu = make(M, K, gen(7000 + M)), make(M, K, gen(7001 + K))
+    x = syn.activations(B, K, gen(7002 + B))
+    wgd, wud, xd = wg.to(gpu), wu.to(gpu), x.to(gpu)
+    h = torch.empty(B, M, dtype=torch.float16, device=gpu)
+    fn = capi().gdsllm_fused_q4_0_gate_up_silu if fmt == "q4_0" else capi().gdsllm_fused_q8_0_gate_up_silu
+    check(fn(ptr(wgd), ptr(wud), ptr(xd), ptr(h), M, K, B, K, M, stream()))
+    torch.cuda.synchronize()
+    hk = to_np(h).astype(np.float64)
+    g, u = to_np(gguf_gemv(fmt, wgd, xd, M, K)), to_np(gguf_gemv(fmt, wud, xd, M, K))
+    sg = oq.silu_fp16(g)
+    href = (sg.astype(np.float32) * u.astype(np.float32)).astype(np.float16)
+    bound = oq.fp16_ulp(sg) * np.abs(u.astype(np.float64)) + oq.fp16_ulp(href)
+    bad = np.abs(hk - href.astype(np.float64)) > bound
+    assert not bad.any(), f"{int(bad.sum())} of {bad.size} h values off; first at {np.argwhere(bad)[0]}"
+    gq = oq.gemv(dq(to_np(wg)).reshape(M, K), to_np(x)).astype(np.float16)
+    uq = oq.gemv(dq(to_np(wu)).reshape(M, K), to_np(x)).astype(np.float16)
+    h_oracle = (oq.silu_fp16(gq).astype(np.float32) * uq.astype(np.float32)).astype(np.float64)
+    rel = float(np.linalg.norm(hk - h_oracle) / np.linalg.norm(h_oracle))
+    assert rel <= oq.GEMV_REL_L2, f"h end-to-end rel L2 {rel:.3e}"

@@ -193,9 +193,11 @@ __device__ __forceinline__ void wait_vmcnt() {
 // compiler orders every LDS access it sees after all in-flight LDS DMA
 // transfers it cannot prove disjoint from it, i.e. it waits for every
 // transfer; these let a kernel touch a region no transfer writes (prepared
-// x) while transfers into its stage buffers are in flight.  Reads return
-// unsynchronised: an "s_waitcnt lgkmcnt(0)" that takes their results as
-// operands must follow before they are used.
+// x, a dequantized tile) while transfers into other buffers are in flight.
+// Each read helper issues its reads and "s_waitcnt lgkmcnt(0)" in ONE asm
+// statement: the results exist only when the statement ends, so no copy the
+// register allocator places after it can see a register the read has not
+// yet filled (a separate wait statement cannot rule such copies out).
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
 }
@@ -205,15 +207,49 @@ __device__ __forceinline__ void lds_write16_raw(uint32_t addr, u32x4_t v) {
 __device__ __forceinline__ void lds_write4_raw(uint32_t addr, uint32_t v) {
     asm volatile("ds_write_b32 %0, %1" ::"v"(addr), "v"(v) : "memory");
 }
-__device__ __forceinline__ u32x4_t lds_read16_raw(uint32_t addr) {
+// 16 bytes at addr (16-byte aligned).
+__device__ __forceinline__ u32x4_t lds_read16_sync(uint32_t addr) {
     u32x4_t v;
-    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+    asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr));
     return v;
 }
-__device__ __forceinline__ uint64_t lds_read8_raw(uint32_t addr) {
-    uint64_t v;
-    asm volatile("ds_read_b64 %0, %1" : "=v"(v) : "v"(addr));
-    return v;
+// 16 bytes at each of addr + STRIDE * i, i < 4 (16-byte aligned).
+template <int STRIDE>
+__device__ __forceinline__ void lds_read16x4_sync(uint32_t addr, u32x4_t (&v)[4]) {
+    static_assert(STRIDE % 16 == 0 && 3 * STRIDE < 65536, "ds offset range");
+    asm volatile(
+        "ds_read_b128 %0, %4\n\t"
+        "ds_read_b128 %1, %4 offset:%5\n\t"
+        "ds_read_b128 %2, %4 offset:%6\n\t"
+        "ds_read_b128 %3, %4 offset:%7\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3])
+        : "v"(addr), "i"(STRIDE), "i"(2 * STRIDE), "i"(3 * STRIDE));
+}
+// 16 bytes at each of addr + 1024 * i, i < 8 (16-byte aligned).
+__device__ __forceinline__ void lds_read16x8_sync(uint32_t addr, u32x4_t (&v)[8]) {
+    asm volatile(
+        "ds_read_b128 %0, %8\n\t"
+        "ds_read_b128 %1, %8 offset:1024\n\t"
+        "ds_read_b128 %2, %8 offset:2048\n\t"
+        "ds_read_b128 %3, %8 offset:3072\n\t"
+        "ds_read_b128 %4, %8 offset:4096\n\t"
+        "ds_read_b128 %5, %8 offset:5120\n\t"
+        "ds_read_b128 %6, %8 offset:6144\n\t"
+        "ds_read_b128 %7, %8 offset:7168\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]), "=&v"(v[7])
+        : "v"(addr));
+}
+// 24 bytes at addr (only 4-byte aligned), as three dword pairs.
+__device__ __forceinline__ void lds_read4x6_sync(uint32_t addr, uint64_t (&v)[3]) {
+    asm volatile(
+        "ds_read2_b32 %0, %3 offset1:1\n\t"
+        "ds_read2_b32 %1, %3 offset0:2 offset1:3\n\t"
+        "ds_read2_b32 %2, %3 offset0:4 offset1:5\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2])
+        : "v"(addr));
 }
 // Workgroup barrier for LDS data only: this wave's LDS requests complete, then
 // s_barrier.  Unlike __syncthreads it does not wait for outstanding global

@@ -416,17 +416,9 @@ template <Fmt F, int NB>
 __device__ __forceinline__ void load_slice(XSlice<NB>& xs, const uint8_t* xraw, int NW, int w, int lane) {
     u32x4_t v[NB][8];
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
-        const uint32_t rec = lds_addr(xraw + (b * NW + w) * 8192 + 16 * lane);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[b][i] = lds_read16_raw(rec + 1024 * i);
-    }
+    for (int b = 0; b < NB; ++b) lds_read16x8_sync(lds_addr(xraw + (b * NW + w) * 8192 + 16 * lane), v[b]);
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-        // the wait takes the raw reads' results, so nothing uses them earlier
-        asm volatile("s_waitcnt lgkmcnt(0)"
-                     : "+v"(v[b][0]), "+v"(v[b][1]), "+v"(v[b][2]), "+v"(v[b][3]), "+v"(v[b][4]), "+v"(v[b][5]),
-                       "+v"(v[b][6]), "+v"(v[b][7]));
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
             uint32_t r[16];

@@ -123,8 +123,8 @@ def test_gate_up_silu_validation():
 
 def test_gemm_validation():
     g = capi().gdsllm_dequant_gemm_q4_0
-    assert g(16, 16, 16, 4, 96, 2, 96, 4, None) == 2 and "multiple of 64" in _err()
-    assert g(16, 16, 16, 4, 48, 2, 48, 4, None) == 1
+    assert g(16, 16, 16, 4, 96, 2, 100, 4, None) == 2 and "aligned" in _err()
+    assert g(16, 16, 16, 4, 48, 2, 48, 4, None) == 1 and "multiple of 32" in _err()
     assert g(16, 16, 16, 4, 64, 2, 32, 4, None) == 1 and "ldx" in _err()
     assert g(16, 24, 16, 4, 64, 2, 64, 4, None) == 2 and "aligned" in _err()
     assert g(None, None, None, 4, 64, 0, 64, 4, None) == 0

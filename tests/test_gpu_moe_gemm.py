@@ -128,8 +128,11 @@ def test_moe_gather_cfg2_full_pool(gpu):
     torch.cuda.empty_cache()
 
 
-GEMM_CASES = [(1, 128, 64), (7, 300, 256), (64, 128, 4096), (100, 260, 1024), (512, 4096, 4096), (33, 11008, 4096),
-              (512, 512, 11008)]
+# (T, M, K): single step (K = 32), K not a multiple of 64, ragged token and row
+# tiles, and shapes large enough for the 256-token workgroup tiles
+# (1100 x 8200 and 2048 x 4096 give at least one tile per CU).
+GEMM_CASES = [(1, 128, 64), (3, 130, 32), (7, 300, 256), (40, 200, 96), (64, 128, 4096), (100, 260, 1024),
+              (512, 4096, 4096), (33, 11008, 4096), (512, 512, 11008), (1100, 8200, 512), (2048, 4096, 4096)]
 
 
 @pytest.mark.parametrize("T,M,K", GEMM_CASES, ids=[f"T{t}_{m}x{k}" for t, m, k in GEMM_CASES])
@@ -144,7 +147,23 @@ def test_dequant_gemm_q4_0(gpu, T, M, K):
     assert_gemv_close(to_np(y), deq, to_np(x), f"gemm T{T} {M}x{K}")
 
 
+def test_dequant_gemm_strided(gpu):
+    """x rows and y rows with leading dimensions wider than the rows."""
+    T, M, K, ldx, ldy = 70, 390, 512, 520, 397
+    w = syn.q4_0_weights(M, K, gen(5100))
+    xfull = syn.activations(T, ldx, gen(5101))
+    x = xfull[:, :K]
+    deq = oq.dequant_q4_0(to_np(w)).reshape(M, K)
+    xd = xfull.to(gpu)
+    y = torch.full((T, ldy), 7.0, dtype=torch.float16, device=gpu)
+    check(capi().gdsllm_dequant_gemm_q4_0(ptr(w.to(gpu)), ptr(xd), ptr(y), M, K, T, ldx, ldy, stream()))
+    torch.cuda.synchronize()
+    yh = to_np(y)
+    assert_gemv_close(yh[:, :M].copy(), deq, to_np(x).copy(), "gemm strided")
+    assert (yh[:, M:] == 7.0).all(), "padding columns of y were written"
+
+
 def test_dequant_gemm_rejects_unsupported(gpu):
     y = torch.empty(8, dtype=torch.float16, device=gpu)
-    assert capi().gdsllm_dequant_gemm_q4_0(ptr(y), ptr(y), ptr(y), 4, 96, 2, 96, 4, stream()) == 2
-    assert b"multiple of 64" in capi().gdsllm_last_error()
+    assert capi().gdsllm_dequant_gemm_q4_0(ptr(y), ptr(y), ptr(y), 4, 96, 2, 100, 4, stream()) == 2
+    assert b"aligned" in capi().gdsllm_last_error()

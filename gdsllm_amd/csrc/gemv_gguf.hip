@@ -26,6 +26,7 @@
 //    the 16-lane DPP row; lane 0 of the row writes the fp16 result.
 
 #include <algorithm>
+#include <utility>
 
 #include "common.h"
 
@@ -750,74 +751,114 @@ __global__ __launch_bounds__(kWaves * 64) void gguf_gemv_rows(const RowsTarget t
 // elements 8g..8g+7; the MFMA sum over k is order-free, so A and B only have
 // to agree.
 //
-// A wave's stage is 32 rows (2 MFMA row tiles) x 2 super-blocks = 16 blocks:
-// 9216 B (Q4_0) / 17408 B (Q8_0), fetched with coalesced 16-byte loads into a
-// per-wave LDS slot where row r occupies bytes [r*S2, r*S2+S2) (S2 = two
-// super-blocks), i.e. chunk c lands at 16c.  The workgroup's waves split K
-// over the same 32 rows; their partial tiles are summed through LDS.  Each
-// stage's x is requested before the next stage's weights are prefetched, so
-// waiting for x never waits for the prefetch (loads retire in order).
+// Row tiles of 16*RT rows (RT = 1 or 2 MFMA tiles) are dealt to a resident
+// grid of workgroups (tile blockIdx.x, then + gridDim.x, ...).  Within a tile
+// the kMfmaWaves waves take the super-blocks of K in turn (wave w: w, w + 8,
+// ...), so at any moment they read 8 adjacent super-blocks of the same rows.
+// A stage is one wave's super-block of the tile's rows (RT*2304 B for Q4_0,
+// RT*4352 B for Q8_0).  Each wave keeps kMfmaDepth stages and their x in
+// flight in registers across tile boundaries (ordinary loads, so the compiler
+// tracks every wait), copies the oldest into its LDS slot, where row r occupies
+// bytes [r*SB, r*SB + SB), and feeds the MFMAs from there.  At the end of a
+// tile the waves' partial tiles are summed through LDS in wave order (so the
+// result does not depend on timing) behind an LDS-only barrier that leaves the
+// next tile's loads in flight.
 
-constexpr int kMfmaRows = 32;    // rows per stage (2 tiles of 16)
-constexpr int kMfmaSbs = 2;      // super-blocks per stage
-constexpr int kMfmaWaves = 4;    // waves per workgroup (K split)
-constexpr int kMfmaBlocks = 8 * kMfmaSbs;
+constexpr int kMfmaWaves = 8;  // waves per workgroup, interleaved over K
+constexpr int kMfmaDepth = 2;  // stages in flight per wave
 
-template <Fmt F>
-constexpr int mfma_stage_bytes() { return kMfmaRows * kMfmaSbs * Layout<F>::kSbBytes; }
-template <Fmt F>
-constexpr int mfma_chunks_per_lane() { return kMfmaRows * kMfmaSbs * Layout<F>::kSbChunks / 64; }
+// LDS slot of one wave: the stage rounded up to whole 1 KB rows of 64 chunks,
+// so every lane stores every chunk it holds without a bounds test.
+template <Fmt F, int RT>
+constexpr int mfma_slot_bytes() { return (16 * RT * Layout<F>::kSbChunks + 63) / 64 * 1024; }
+// partial tiles of all waves: [wave][t][chain][v][lane] fp32
+template <int RT>
+constexpr int mfma_red_bytes() { return kMfmaWaves * RT * 2 * 4 * 64 * 4; }
+template <Fmt F, int RT>
+constexpr int mfma_lds_bytes() { return kMfmaWaves * mfma_slot_bytes<F, RT>() + 2 * mfma_red_bytes<RT>(); }
 
-// B operand (4 dwords) of block `gb` for lane group g and batch row b, from raw x.
+// Raw x of block `gb` for lane group g, kept in the register pairs the loads
+// fill (regrouping them costs a copy of every pair).
+struct XRaw {
+    uint2 a, b;
+};
 template <Fmt F>
-__device__ __forceinline__ void load_x_b(uint32_t (&r)[4], const uint16_t* __restrict__ xb, int gb, int g) {
+__device__ __forceinline__ XRaw load_x_b(const uint16_t* __restrict__ xb, int gb, int g) {
     if constexpr (F == Fmt::Q4_0) {
-        const uint2 lo = *reinterpret_cast<const uint2*>(xb + 32 * gb + 4 * g);
-        const uint2 hi = *reinterpret_cast<const uint2*>(xb + 32 * gb + 16 + 4 * g);
-        r[0] = lo.x; r[1] = lo.y; r[2] = hi.x; r[3] = hi.y;
+        // elements 4g..4g+3 and 16+4g..19+4g
+        return {*reinterpret_cast<const uint2*>(xb + 32 * gb + 4 * g),
+                *reinterpret_cast<const uint2*>(xb + 32 * gb + 16 + 4 * g)};
     } else {
+        // elements 8g..8g+7
         const uint4 v = *reinterpret_cast<const uint4*>(xb + 32 * gb + 8 * g);
-        r[0] = v.x; r[1] = v.y; r[2] = v.z; r[3] = v.w;
+        return {make_uint2(v.x, v.y), make_uint2(v.z, v.w)};
     }
 }
 
+// B operand of a block from its raw x, in weight_a_operand's element order.
 template <Fmt F>
-__device__ __forceinline__ half8_t x_b_operand(const uint32_t (&r)[4]) {
+__device__ __forceinline__ half8_t x_b_operand(const XRaw& r) {
     uint32_t p[4];
     if constexpr (F == Fmt::Q4_0) {
         // (x4g, x4g+2) (x16+4g, x18+4g) (x4g+1, x4g+3) (x17+4g, x19+4g)
-        p[0] = __builtin_amdgcn_perm(r[1], r[0], kSelLo);
-        p[1] = __builtin_amdgcn_perm(r[3], r[2], kSelLo);
-        p[2] = __builtin_amdgcn_perm(r[1], r[0], kSelHi);
-        p[3] = __builtin_amdgcn_perm(r[3], r[2], kSelHi);
+        p[0] = __builtin_amdgcn_perm(r.a.y, r.a.x, kSelLo);
+        p[1] = __builtin_amdgcn_perm(r.b.y, r.b.x, kSelLo);
+        p[2] = __builtin_amdgcn_perm(r.a.y, r.a.x, kSelHi);
+        p[3] = __builtin_amdgcn_perm(r.b.y, r.b.x, kSelHi);
     } else {
         // (x0, x2) (x1, x3) (x4, x6) (x5, x7) of elements 8g..8g+7
-        p[0] = __builtin_amdgcn_perm(r[1], r[0], kSelLo);
-        p[1] = __builtin_amdgcn_perm(r[1], r[0], kSelHi);
-        p[2] = __builtin_amdgcn_perm(r[3], r[2], kSelLo);
-        p[3] = __builtin_amdgcn_perm(r[3], r[2], kSelHi);
+        p[0] = __builtin_amdgcn_perm(r.a.y, r.a.x, kSelLo);
+        p[1] = __builtin_amdgcn_perm(r.a.y, r.a.x, kSelHi);
+        p[2] = __builtin_amdgcn_perm(r.b.y, r.b.x, kSelLo);
+        p[3] = __builtin_amdgcn_perm(r.b.y, r.b.x, kSelHi);
     }
     return __builtin_bit_cast(half8_t, make_uint4(p[0], p[1], p[2], p[3]));
 }
 
-// A operand of block j (0..15) of the stage row at `row` (LDS, 4-byte aligned
-// row start) for lane group g: bit-exact fp16 weights in x_b_operand's order.
-template <Fmt F, int J>
-__device__ __forceinline__ half8_t weight_a_operand(const uint32_t* row, int g, const NibUnpack& nu) {
-    using L = Layout<F>;
-    constexpr int kPairDw = L::kBlockBytes / 2;  // dwords of a block pair (9 / 17)
-    constexpr int P = J / 2;
-    const uint32_t* pr = row + kPairDw * P;
+// The dwords of a block pair (blocks 2P, 2P+1 of a stage row, 4-byte aligned)
+// that lane group g needs: Q4_0 {d word of each block, qs dwords g and g+1 of
+// the even block (unaligned by 2), qs dword g of the odd block}; Q8_0 {d words,
+// qs dwords 2g..2g+2 of the even block, 2g and 2g+1 of the odd one}.
+template <Fmt F>
+struct PairWords {
+    static constexpr int N = F == Fmt::Q4_0 ? 5 : 7;
+    uint32_t w[N];
+};
+template <Fmt F>
+__device__ __forceinline__ PairWords<F> pair_words(const uint32_t* pr, int g) {
+    PairWords<F> p;
+    if constexpr (F == Fmt::Q4_0) {
+        p.w[0] = pr[0];
+        p.w[1] = pr[4];
+        p.w[2] = pr[g];
+        p.w[3] = pr[g + 1];
+        p.w[4] = pr[5 + g];
+    } else {
+        p.w[0] = pr[0];
+        p.w[1] = pr[8];
+        p.w[2] = pr[2 * g];
+        p.w[3] = pr[2 * g + 1];
+        p.w[4] = pr[2 * g + 2];
+        p.w[5] = pr[9 + 2 * g];
+        p.w[6] = pr[10 + 2 * g];
+    }
+    return p;
+}
+
+// A operand of block ODD of a pair for lane group g: bit-exact fp16 weights in
+// x_b_operand's order.
+template <Fmt F, int ODD>
+__device__ __forceinline__ half8_t weight_a_operand(const PairWords<F>& p, const NibUnpack& nu) {
     uint32_t dbits;
     half2_t h[4];
     if constexpr (F == Fmt::Q4_0) {
         uint32_t q;
-        if constexpr (J % 2 == 0) {
-            dbits = pr[0] & 0xFFFFu;
-            q = align2(pr[g], pr[g + 1]);
+        if constexpr (ODD == 0) {
+            dbits = p.w[0] & 0xFFFFu;
+            q = align2(p.w[2], p.w[3]);
         } else {
-            dbits = pr[4] >> 16;
-            q = pr[5 + g];
+            dbits = p.w[1] >> 16;
+            q = p.w[4];
         }
         const half2_t lo_off = {static_cast<half_t>(-1032.0f), static_cast<half_t>(-1032.0f)};
         const half2_t hi_off = {static_cast<half_t>(-72.0f), static_cast<half_t>(-72.0f)};
@@ -828,14 +869,14 @@ __device__ __forceinline__ half8_t weight_a_operand(const uint32_t* row, int g, 
         h[3] = __builtin_bit_cast(half2_t, nu.hi(qs)) + hi_off;
     } else {
         uint32_t q0, q1;
-        if constexpr (J % 2 == 0) {
-            dbits = pr[0] & 0xFFFFu;
-            q0 = align2(pr[2 * g], pr[2 * g + 1]);
-            q1 = align2(pr[2 * g + 1], pr[2 * g + 2]);
+        if constexpr (ODD == 0) {
+            dbits = p.w[0] & 0xFFFFu;
+            q0 = align2(p.w[2], p.w[3]);
+            q1 = align2(p.w[3], p.w[4]);
         } else {
-            dbits = pr[8] >> 16;
-            q0 = pr[9 + 2 * g];
-            q1 = pr[10 + 2 * g];
+            dbits = p.w[1] >> 16;
+            q0 = p.w[5];
+            q1 = p.w[6];
         }
         const half2_t off = {static_cast<half_t>(-1152.0f), static_cast<half_t>(-1152.0f)};
         const uint32_t u0 = q0 ^ 0x80808080u, u1 = q1 ^ 0x80808080u;
@@ -852,119 +893,185 @@ __device__ __forceinline__ half8_t weight_a_operand(const uint32_t* row, int g, 
     return __builtin_bit_cast(half8_t, make_uint4(w[0], w[1], w[2], w[3]));
 }
 
-template <Fmt F>
+// acc += the 8 blocks of one super-block row tile (A from the pair words, B
+// from xb), one block at a time: the scheduling barrier after each MFMA keeps
+// the compiler from building all eight operands first, which would cost the
+// registers that hold the stages in flight.
+template <Fmt F, int J>
+__device__ __forceinline__ void mfma_block(float4_t (&acc)[2], const PairWords<F> (&pw)[4], const NibUnpack& nu,
+                                           const half8_t (&xb)[4]) {
+    acc[J % 2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(weight_a_operand<F, J % 2>(pw[J / 2], nu), xb[J / 2],
+                                                        acc[J % 2], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+}
+template <Fmt F, int... J>
+__device__ __forceinline__ void mfma_superblock(float4_t (&acc)[2], const PairWords<F> (&pw)[4], const NibUnpack& nu,
+                                                const half8_t (&xb)[4], std::integer_sequence<int, J...>) {
+    (mfma_block<F, J>(acc, pw, nu, xb), ...);
+}
+
+template <Fmt F, int RT>
 __global__ __launch_bounds__(kMfmaWaves * 64) void gguf_gemv_mfma(const uint8_t* __restrict__ W,
                                                                   const uint16_t* __restrict__ X,
                                                                   uint16_t* __restrict__ Y, int M, int K, int nb,
                                                                   int64_t ldx, int64_t ldy) {
     using L = Layout<F>;
-    constexpr int CPL = mfma_chunks_per_lane<F>();
-    constexpr int kRowChunks = kMfmaSbs * L::kSbChunks;  // chunks of one stage row
-    constexpr int kRowDw = kMfmaSbs * L::kSbBytes / 4;
+    constexpr int kRows = 16 * RT;
+    constexpr int kChunks = kRows * L::kSbChunks;  // 16-byte chunks of a stage
+    constexpr int CPL = (kChunks + 63) / 64;
+    constexpr int kRowDw = L::kSbBytes / 4;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    uint8_t* stage = smem + wave * mfma_stage_bytes<F>();
-    const int S = K >> 8;                       // super-blocks per row
-    const int NS = (S + kMfmaSbs - 1) / kMfmaSbs;  // stages along K
-    const uint32_t row_bytes = static_cast<uint32_t>(S) * L::kSbBytes;
-    const int r0 = blockIdx.x * kMfmaRows;
-    const int nrows = min(kMfmaRows, M - r0);
-    // this wave's stages: [s_begin, s_end) of the row group's NS
-    const int s_begin = wave * NS / kMfmaWaves, s_end = (wave + 1) * NS / kMfmaWaves;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    uint8_t* stage = smem + wave * mfma_slot_bytes<F, RT>();
+    float* red0 = reinterpret_cast<float*>(smem + kMfmaWaves * mfma_slot_bytes<F, RT>());
+    const int S = K >> 8;  // super-blocks per row
+    const int64_t row_bytes = static_cast<int64_t>(S) * L::kSbBytes;
+    const int ntiles = (M + kRows - 1) / kRows;
+    const int T = (ntiles - static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) - 1) / static_cast<int>(gridDim.x);
+    const int nst = S > wave ? (S - 1 - wave) / kMfmaWaves + 1 : 0;  // stages of this wave per tile
     const NibUnpack nu;
     const int g = lane >> 4, bcol = lane & 15;
-    const bool xlane = bcol < nb;
-    const uint16_t* xrow = X + (xlane ? bcol : 0) * ldx;
 
-    // chunk j of this lane: stage row rl = c / kRowChunks, byte offset goff
-    uint32_t goff[CPL];
-    int rl[CPL];
+    // With nb <= 8 one B operand carries two blocks: columns 0-7 hold tokens
+    // 0-7 of block 2i, columns 8-15 the same tokens of block 2i+1.  Even blocks
+    // accumulate into chain 0, whose valid columns are 0-7, odd blocks into
+    // chain 1, valid in columns 8-15; the other half of each chain is never read.
+    // Lanes of tokens past nb read x row 0; lanes of chunks past the stage or
+    // past row M read the stage's first chunk.  Every load is valid and
+    // unconditional (a load under a branch makes the compiler wait for all
+    // loads in flight), and what the extra lanes bring only reaches MFMA
+    // columns and rows that are never read: an MFMA row depends on its A row
+    // only, a column on its B column only, so LDS rows past M (duplicate
+    // bytes, scale possibly Inf/NaN) and columns past nb stay apart.
+    const int tok = bcol & 7, half = bcol >> 3;
+    const uint16_t* xrow = X + (tok < nb ? tok : 0) * ldx;
+    // chunk j of this lane: stage row c / kSbChunks, chunk c % kSbChunks of it
+    int crow[CPL];
+    uint32_t coff[CPL];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
         const int c = 64 * j + lane;
-        rl[j] = c / kRowChunks;
-        goff[j] = rl[j] * row_bytes + 16 * (c - rl[j] * kRowChunks);
+        crow[j] = c < kChunks ? c / L::kSbChunks : 0;
+        coff[j] = c < kChunks ? 16 * (c - crow[j] * L::kSbChunks) : 0u;
     }
-    // A stage s covers super-blocks [2s, 2s+2); the last one may be half (odd S).
-    auto load = [&](uint4 (&pre)[CPL], int s) {
-        const uint8_t* base = W + static_cast<int64_t>(r0) * row_bytes + s * kMfmaSbs * L::kSbBytes;
-        const int nsb = min(kMfmaSbs, S - s * kMfmaSbs);
+
+    uint4 pre[kMfmaDepth][CPL];
+    XRaw xr[kMfmaDepth][4];
+    float4_t acc[RT][2];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) acc[t][0] = acc[t][1] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    // next stage to load: tile lk of this workgroup, stage li of this wave;
+    // past the last one the last stage is loaded again (never computed)
+    int lk = 0, li = 0;
+    auto load = [&](auto slot) {
+        constexpr int sl = decltype(slot)::value;
+        const bool past = lk >= T;
+        const int r0 = kRows * (static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) * (past ? T - 1 : lk));
+        const int sb = wave + kMfmaWaves * (past ? nst - 1 : li);
+        const int nrows = min(kRows, M - r0);
+        const uint8_t* src = W + static_cast<int64_t>(r0) * row_bytes + static_cast<int64_t>(sb) * L::kSbBytes;
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
-            const int c = 64 * j + lane;
-            if (rl[j] < nrows && (c - rl[j] * kRowChunks) < nsb * L::kSbChunks) pre[j] = load_nt16(base + goff[j]);
+            const int64_t off = crow[j] < nrows ? crow[j] * row_bytes + coff[j] : 0;
+            pre[sl][j] = load_nt16(src + off);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xr[sl][i] = load_x_b<F>(xrow, 8 * sb + 2 * i + half, g);
+        if (++li == nst) {
+            li = 0;
+            ++lk;
         }
     };
-    float4_t acc[2];
-    acc[0] = float4_t{0.f, 0.f, 0.f, 0.f};
-    acc[1] = acc[0];
-    uint4 pre[CPL];
-    if (s_begin < s_end) load(pre, s_begin);
-    for (int s = s_begin; s < s_end; ++s) {
-        // chunks past the rows of M or a half last stage stay stale: they only
-        // feed rows that are not stored or blocks whose x is zero
+    // End of tile ck: sum the waves' partial tiles in wave order and store the
+    // rows (one output per thread).  red alternates between two buffers: the
+    // barrier of the next tile separates this tile's reads of one buffer from
+    // its next writes.
+    int ck = 0;
+    auto finish_tile = [&]() {
+        float* red = red0 + (ck & 1) * (mfma_red_bytes<RT>() / 4);
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) *reinterpret_cast<uint4*>(stage + 16 * (64 * j + lane)) = pre[j];
-        wave_lds_sync();
-        const int nblk = min(kMfmaBlocks, (K >> 5) - s * kMfmaBlocks);
-        uint32_t xr[kMfmaBlocks][4];
+        for (int t = 0; t < RT; ++t)
 #pragma unroll
-        for (int jb = 0; jb < kMfmaBlocks; ++jb) {
-            if (xlane && jb < nblk) load_x_b<F>(xr[jb], xrow, s * kMfmaBlocks + jb, g);
-            else xr[jb][0] = xr[jb][1] = xr[jb][2] = xr[jb][3] = 0u;
-        }
-        if (s + 1 < s_end) load(pre, s + 1);
+            for (int c = 0; c < 2; ++c) {
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const uint32_t* row = reinterpret_cast<const uint32_t*>(stage) + (16 * t + bcol) * kRowDw;
-#pragma unroll
-            for (int jb = 0; jb < kMfmaBlocks; ++jb) {
-                const half8_t a = [&] {
-                    switch (jb) {
-                        case 0: return weight_a_operand<F, 0>(row, g, nu);
-                        case 1: return weight_a_operand<F, 1>(row, g, nu);
-                        case 2: return weight_a_operand<F, 2>(row, g, nu);
-                        case 3: return weight_a_operand<F, 3>(row, g, nu);
-                        case 4: return weight_a_operand<F, 4>(row, g, nu);
-                        case 5: return weight_a_operand<F, 5>(row, g, nu);
-                        case 6: return weight_a_operand<F, 6>(row, g, nu);
-                        case 7: return weight_a_operand<F, 7>(row, g, nu);
-                        case 8: return weight_a_operand<F, 8>(row, g, nu);
-                        case 9: return weight_a_operand<F, 9>(row, g, nu);
-                        case 10: return weight_a_operand<F, 10>(row, g, nu);
-                        case 11: return weight_a_operand<F, 11>(row, g, nu);
-                        case 12: return weight_a_operand<F, 12>(row, g, nu);
-                        case 13: return weight_a_operand<F, 13>(row, g, nu);
-                        case 14: return weight_a_operand<F, 14>(row, g, nu);
-                        default: return weight_a_operand<F, 15>(row, g, nu);
-                    }
-                }();
-                // blocks past K in a half last stage hold stale bytes whose scale may be
-                // Inf/NaN; zero x would not cancel that, so they are skipped
-                if (jb < nblk) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, x_b_operand<F>(xr[jb]), acc[t], 0, 0, 0);
+                for (int v = 0; v < 4; ++v) red[(((wave * RT + t) * 2 + c) * 4 + v) * 64 + lane] = acc[t][c][v];
+                acc[t][c] = float4_t{0.f, 0.f, 0.f, 0.f};
             }
-        }
-    }
-    // Sum the waves' partial tiles: red[wave][t][v][lane], then one thread per
-    // output (row, batch) adds the kMfmaWaves partials.
-    __syncthreads();
-    float* red = reinterpret_cast<float*>(smem);
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) red[((wave * 2 + t) * 4 + v) * 64 + lane] = acc[t][v];
-    __syncthreads();
-    for (int o = threadIdx.x; o < kMfmaRows * nb; o += kMfmaWaves * 64) {
-        const int r = o / nb, b = o - r * nb;
-        if (r < nrows) {
+        lds_barrier();
+        const int r0 = kRows * (static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) * ck);
+        const int r = static_cast<int>(threadIdx.x) / nb, b = static_cast<int>(threadIdx.x) - r * nb;
+        if (r < min(kRows, M - r0)) {
             const int t = r >> 4, r16 = r & 15;
             const int src_lane = 16 * (r16 >> 2) + b, v = r16 & 3;
             float sum = 0.f;
 #pragma unroll
-            for (int w = 0; w < kMfmaWaves; ++w) sum += red[((w * 2 + t) * 4 + v) * 64 + src_lane];
+            for (int w = 0; w < kMfmaWaves; ++w)
+                sum += red[(((w * RT + t) * 2 + 0) * 4 + v) * 64 + src_lane] +
+                       red[(((w * RT + t) * 2 + 1) * 4 + v) * 64 + src_lane + 8];
             Y[b * ldy + r0 + r] = f2h_bits(sum);
         }
+        ++ck;
+    };
+    // next stage to compute: stage ci of the current tile
+    int ci = 0;
+    auto compute = [&](auto slot) {
+        constexpr int sl = decltype(slot)::value;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) *reinterpret_cast<uint4*>(stage + 16 * (64 * j + lane)) = pre[sl][j];
+        wave_lds_sync();
+        half8_t xb[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xb[i] = x_b_operand<F>(xr[sl][i]);
+        // every LDS word of the stage this lane needs, read before any is used,
+        // so the stage waits for LDS once
+        PairWords<F> pw[RT][4];
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+            const uint32_t* row = reinterpret_cast<const uint32_t*>(stage) + (16 * t + bcol) * kRowDw;
+#pragma unroll
+            for (int P = 0; P < 4; ++P) pw[t][P] = pair_words<F>(row + P * (Layout<F>::kBlockBytes / 2), g);
+        }
+#pragma unroll
+        for (int t = 0; t < RT; ++t) mfma_superblock<F>(acc[t], pw[t], nu, xb, std::make_integer_sequence<int, 8>{});
+        if (++ci == nst) {
+            ci = 0;
+            finish_tile();
+        }
+    };
+    static_assert(kRows * 8 <= kMfmaWaves * 64, "one output per thread per tile");
+
+    if (nst == 0) {
+        // K has fewer super-blocks than the workgroup has waves: this wave
+        // adds zero partials to every tile's sum
+        for (int k = 0; k < T; ++k) finish_tile();
+        return;
     }
+    const int Q = T * nst;  // stages of this wave in all its tiles
+    // slots cycle 0 .. kMfmaDepth-1; the steady loop issues every load
+    // unconditionally and the tail only computes
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    static_assert(kMfmaDepth == 2 || kMfmaDepth == 3, "two or three slots");
+    load(I0{});
+    load(I1{});
+    if constexpr (kMfmaDepth == 3) load(I2{});
+    int q = 0;
+    for (; q + kMfmaDepth < Q; q += kMfmaDepth) {
+        compute(I0{});
+        load(I0{});
+        compute(I1{});
+        load(I1{});
+        if constexpr (kMfmaDepth == 3) {
+            compute(I2{});
+            load(I2{});
+        }
+    }
+    if (q < Q) compute(I0{});
+    if (q + 1 < Q) compute(I1{});
+    if constexpr (kMfmaDepth == 3)
+        if (q + 2 < Q) compute(I2{});
 }
 
 // Any in_dim % 32 == 0 and any alignment: one wave per row, one lane per block,
@@ -1001,6 +1108,21 @@ __global__ __launch_bounds__(256) void gguf_gemv_generic(const uint8_t* __restri
         acc = group_sum<64>(acc);
         if (lane == 0) Y[b * ldy + row] = f2h_bits(acc);
     }
+}
+
+template <Fmt F, int RT>
+int launch_mfma(const void* w, const uint16_t* x, uint16_t* y, int M, int K, int64_t batch, int64_t ldx, int64_t ldy,
+                hipStream_t stream) {
+    const size_t lds = mfma_lds_bytes<F, RT>();
+    const void* fn = reinterpret_cast<const void*>(&gguf_gemv_mfma<F, RT>);
+    if (int rc = prepare_lds(fn, lds)) return rc;
+    const int tiles = (M + 16 * RT - 1) / (16 * RT);
+    const int resident = blocks_per_cu(fn, lds, kMfmaWaves * 64) * cu_count();
+    if (resident < 1) return set_error(GDSLLM_ERR_UNSUPPORTED, "gguf_gemv_mfma: no workgroup fits a compute unit");
+    const int grid = tiles < resident ? tiles : resident;
+    hipLaunchKernelGGL((gguf_gemv_mfma<F, RT>), dim3(grid), dim3(kMfmaWaves * 64), lds, stream,
+                       static_cast<const uint8_t*>(w), x, y, M, K, static_cast<int>(batch), ldx, ldy);
+    return check_hip(hipGetLastError(), "gguf_gemv_mfma launch");
 }
 
 template <Fmt F, int NB>
@@ -1135,20 +1257,13 @@ int gemv(const char* name, const void* w, const void* x, void* y, int64_t out_di
     if (rc != -1) return rc == GDSLLM_OK ? ok() : rc;
     rc = GDSLLM_OK;
     const bool x_al16 = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (ldx % 8 == 0);
-    if (fast && batch >= 5 && K <= (1 << 20) && x_al16) {
-        const size_t lds = static_cast<size_t>(kMfmaWaves) * mfma_stage_bytes<F>();
-        const void* fn = reinterpret_cast<const void*>(&gguf_gemv_mfma<F>);
-        if (lds > 65536) {
-            if (int e = check_hip(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                      static_cast<int>(lds)),
-                                  "hipFuncSetAttribute"))
-                return e;
-        }
-        const int grid = (M + kMfmaRows - 1) / kMfmaRows;
-        hipLaunchKernelGGL(gguf_gemv_mfma<F>, dim3(grid), dim3(kMfmaWaves * 64), lds, s,
-                           static_cast<const uint8_t*>(w), xp, yp, M, K, static_cast<int>(batch), ldx, ldy);
-        if (int e = check_hip(hipGetLastError(), (n + " launch").c_str())) return e;
-        return ok();
+    if (fast && batch >= 3 && K <= (1 << 20) && x_al16) {
+        // Q4_0: two row tiles per workgroup while that still gives every CU
+        // one; Q8_0 stages are twice as large and take one tile
+        const int rc2 = F == Fmt::Q4_0 && (M + 31) / 32 >= cu_count()
+                            ? launch_mfma<F, 2>(w, xp, yp, M, K, batch, ldx, ldy, s)
+                            : launch_mfma<F, 1>(w, xp, yp, M, K, batch, ldx, ldy, s);
+        return rc2 == GDSLLM_OK ? ok() : rc2;
     }
     if (fast) {
         const int S = K >> 8;

@@ -36,9 +36,15 @@ def test_gguf_gemv_b1(gpu, fmt, M, K):
     assert_gemv_close(to_np(y), deq, to_np(x), f"{fmt} {M}x{K}")
 
 
+# K = 256 (one super-block: most waves of a batched workgroup have no stage),
+# ragged row tiles at both tile heights (8200 rows: 32-row tiles with a part
+# tile), in_dim % 256 != 0 (generic kernel)
+BATCHED_SHAPES = [(70, 4096), (33, 11008), (20, 96), (24, 8192), (9, 28672), (13003, 1024), (40, 256), (8200, 512)]
+
+
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
-@pytest.mark.parametrize("B", [2, 3, 4, 8])
-@pytest.mark.parametrize("M,K", [(70, 4096), (33, 11008), (20, 96), (24, 8192), (9, 28672), (13003, 1024)])
+@pytest.mark.parametrize("B", [2, 3, 4, 5, 7, 8])
+@pytest.mark.parametrize("M,K", BATCHED_SHAPES, ids=[f"{m}x{k}" for m, k in BATCHED_SHAPES])
 def test_gguf_gemv_batched(gpu, fmt, B, M, K):
     w, x, deq = _gguf_case(fmt, M, K, B, 2000 + B + M)
     y = gguf_gemv(fmt, w.to(gpu), x.to(gpu), M, K)
@@ -54,20 +60,23 @@ def test_q4_0_gemv_cfg0_full(gpu):
 
 
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
-def test_gguf_gemv_misaligned_inputs(gpu, fmt):
+@pytest.mark.parametrize("B", [2, 4])
+@pytest.mark.parametrize("w_off", [2, 0])
+def test_gguf_gemv_misaligned_inputs(gpu, fmt, B, w_off):
     """Weights off the 16-byte grid take the generic kernel; x off the 8-byte grid
-    takes the element-wise staging; both must agree with the oracle."""
+    takes the element-wise staging (batch 3-8: the staged kernel instead of the
+    MFMA one); both must agree with the oracle."""
     M, K = 40, 512
-    w, x, deq = _gguf_case(fmt, M, K, 2, 77)
-    wd = on_gpu(w, gpu, pad_front=2)
-    xbuf = torch.zeros(2 * K + 8, dtype=torch.float16, device=gpu)
-    xd = xbuf[1:1 + 2 * K]
+    w, x, deq = _gguf_case(fmt, M, K, B, 77 + B)
+    wd = on_gpu(w, gpu, pad_front=w_off)
+    xbuf = torch.zeros(B * K + 8, dtype=torch.float16, device=gpu)
+    xd = xbuf[1:1 + B * K]
     xd.copy_(x.reshape(-1).to(gpu))
-    y = torch.empty(2, M, dtype=torch.float16, device=gpu)
+    y = torch.empty(B, M, dtype=torch.float16, device=gpu)
     fn = capi().gdsllm_fused_q4_0_gemv if fmt == "q4_0" else capi().gdsllm_fused_q8_0_gemv
-    check(fn(ptr(wd), ptr(xd), ptr(y), M, K, 2, K, M, stream()))
+    check(fn(ptr(wd), ptr(xd), ptr(y), M, K, B, K, M, stream()))
     torch.cuda.synchronize()
-    assert_gemv_close(to_np(y), deq, to_np(x), f"{fmt} misaligned")
+    assert_gemv_close(to_np(y), deq, to_np(x), f"{fmt} misaligned B={B}")
 
 
 @pytest.mark.parametrize("B", [2, 3])

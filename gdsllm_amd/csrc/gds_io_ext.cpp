@@ -416,6 +416,68 @@ torch::Tensor fused_dequant_gemm(const Handle& h, torch::Tensor x, std::vector<i
     return out;
 }
 
+// ---- on-device MoE routing and epilogue (no counterpart op in the reference's
+// module: they replace the torch calls of runtime/qwen_moe.py:408-412, 505-513)
+
+void check_fp16_cuda(const torch::Tensor& t, const char* what, const char* where) {
+    if (!t.is_cuda() || t.scalar_type() != torch::kFloat16)
+        throw std::runtime_error(std::string(where) + ": " + what + " must be a float16 GPU tensor");
+}
+
+torch::Tensor gemv_f16(torch::Tensor weight, torch::Tensor x) {
+    const char* where = "gemv_f16";
+    check_fp16_cuda(weight, "weight", where);
+    check_fp16_cuda(x, "x", where);
+    if (weight.dim() != 2) throw std::runtime_error(std::string(where) + ": weight must be [out_dim, in_dim]");
+    torch::Tensor w = weight.contiguous(), xf = x.contiguous();
+    const int64_t out_dim = w.size(0), in_dim = w.size(1);
+    if (xf.size(-1) != in_dim)
+        throw std::runtime_error(std::string(where) + ": last dim of x must equal in_dim " + std::to_string(in_dim));
+    const int64_t rows = in_dim ? xf.numel() / in_dim : 0;
+    auto out_shape = xf.sizes().vec();
+    out_shape.back() = out_dim;
+    torch::Tensor out = torch::empty(out_shape, w.options());
+    const int dev = w.get_device();
+    for (int64_t r0 = 0; r0 < rows; r0 += 8) {
+        const int64_t nb = std::min<int64_t>(8, rows - r0);
+        check(gdsllm_gemv_f16(w.data_ptr(), static_cast<const at::Half*>(xf.data_ptr()) + r0 * in_dim,
+                              static_cast<at::Half*>(out.data_ptr()) + r0 * out_dim, out_dim, in_dim, nb, in_dim,
+                              out_dim, stream_of(dev)),
+              where);
+    }
+    return out;
+}
+
+py::tuple moe_route_topk(torch::Tensor logits, int64_t top_k) {
+    const char* where = "moe_route_topk";
+    check_fp16_cuda(logits, "logits", where);
+    torch::Tensor l = logits.contiguous();
+    const int64_t E = l.size(-1), n = E ? l.numel() / E : 0;
+    auto shape = l.sizes().vec();
+    shape.back() = top_k;
+    torch::Tensor idx = torch::empty(shape, l.options().dtype(torch::kInt32));
+    torch::Tensor w = torch::empty(shape, l.options());
+    check(gdsllm_moe_route_topk(l.data_ptr(), E, n, E, top_k, idx.data_ptr<int32_t>(), w.data_ptr(),
+                                stream_of(l.get_device())),
+          where);
+    return py::make_tuple(idx, w);
+}
+
+torch::Tensor moe_combine(torch::Tensor expert_out, torch::Tensor shared_out, torch::Tensor shared_gate_logit) {
+    const char* where = "moe_combine";
+    check_fp16_cuda(expert_out, "expert_out", where);
+    check_fp16_cuda(shared_out, "shared_out", where);
+    check_fp16_cuda(shared_gate_logit, "shared_gate_logit", where);
+    torch::Tensor e = expert_out.contiguous(), s = shared_out.contiguous(), g = shared_gate_logit.contiguous();
+    if (!e.sizes().equals(s.sizes())) throw std::runtime_error(std::string(where) + ": expert_out and shared_out differ in shape");
+    const int64_t H = e.size(-1), n = H ? e.numel() / H : 0;
+    if (g.numel() != n) throw std::runtime_error(std::string(where) + ": one gate logit per row expected");
+    torch::Tensor y = torch::empty_like(e);
+    check(gdsllm_moe_combine(e.data_ptr(), s.data_ptr(), g.data_ptr(), y.data_ptr(), H, n, stream_of(e.get_device())),
+          where);
+    return y;
+}
+
 Handle from_tensor(const torch::Tensor& t) { return std::make_shared<GdsBufferHandle>(t); }
 
 }  // namespace
@@ -470,4 +532,10 @@ PYBIND11_MODULE(gds_io_ext, m) {
           py::arg("top_k_indices"), py::arg("top_k_weights"));
     m.def("fused_dequant_gemm", &fused_dequant_gemm, "Prefill Q4_0 dequant-GEMM on MFMA: x [T, K] -> [T, M].",
           py::arg("handle"), py::arg("x"), py::arg("weight_shape"), py::arg("gguf_type"), py::arg("offset"));
+    m.def("gemv_f16", &gemv_f16, "fp16-weight GEMV (router, shared-expert gate): x [..., K] -> [..., M].",
+          py::arg("weight"), py::arg("x"));
+    m.def("moe_route_topk", &moe_route_topk, "Top-k experts and fp16(softmax_fp32) weights from fp16 logits.",
+          py::arg("logits"), py::arg("top_k"));
+    m.def("moe_combine", &moe_combine, "clamp(expert_out + sigmoid(gate) * shared_out) with torch fp16 semantics.",
+          py::arg("expert_out"), py::arg("shared_out"), py::arg("shared_gate_logit"));
 }

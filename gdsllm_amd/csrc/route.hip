@@ -1,0 +1,225 @@
+// On-device MoE routing and the MoE output epilogue.
+//
+// The reference routes a Qwen-MoE token on the host side of a sync: router
+// logits by F.linear on the fp16 router matrix, torch.topk, a float32 softmax
+// of the k logits cast back to fp16, then .tolist() of the picks
+// (runtime/qwen_moe.py:386-416); after the experts it adds the shared expert
+// scaled by sigmoid(shared_expert_gate . x) and clamps to the fp16 range
+// (runtime/qwen_moe.py:496-513).  These kernels keep all of it on the device:
+//  * gemv_f16: y = fp16(sum_k w[r][k] * x[k]) for fp16 weights (the router
+//    and the shared-expert gate; the converter stores unquantized tensors as
+//    fp16, tools/convert_qwen_moe.py:177-189), fp32 accumulation;
+//  * route_topk: the k largest logits per token in descending order (ties:
+//    lower expert index first; NaN above every number, as torch.topk), and
+//    fp16(softmax_fp32(those logits));
+//  * moe_combine: y = clamp(expert_out + fp16(fp16(sigmoid(gate)) * shared_out))
+//    with torch's fp16 elementwise semantics (each op in fp32, rounded to fp16).
+
+#include <algorithm>
+
+#include "common.h"
+
+namespace gdsllm {
+namespace {
+
+constexpr int kF16Waves = 4;      // waves per workgroup of the fp16 GEMV
+constexpr int kMaxBatch = 8;
+constexpr int kMaxExperts = 4096;  // logits of one token held in LDS
+constexpr int kMaxTopK = 64;       // one pick per lane
+
+// One wave per row, rows dealt round-robin over the grid's waves.  Vector
+// path: each lane takes 8 consecutive weights of every 512-column chunk as one
+// 16-byte load (the row length is a multiple of 8 and every row start is
+// 16-byte aligned).  Scalar path: one element per lane per 64 columns.
+template <bool VEC>
+__global__ __launch_bounds__(kF16Waves * 64) void gemv_f16(const uint16_t* __restrict__ W,
+                                                           const uint16_t* __restrict__ X, uint16_t* __restrict__ Y,
+                                                           int M, int K, int nb, int64_t ldx, int64_t ldy) {
+    const int lane = threadIdx.x & 63;
+    const int nwaves = static_cast<int>(gridDim.x) * kF16Waves;
+    for (int r = static_cast<int>(blockIdx.x) * kF16Waves + (threadIdx.x >> 6); r < M; r += nwaves) {
+        const uint16_t* wr = W + static_cast<int64_t>(r) * K;
+        float acc[kMaxBatch];
+#pragma unroll
+        for (int b = 0; b < kMaxBatch; ++b) acc[b] = 0.f;
+        if constexpr (VEC) {
+            for (int c = 8 * lane; c < K; c += 512) {
+                const uint4 w = load_nt16(wr + c);
+#pragma unroll
+                for (int b = 0; b < kMaxBatch; ++b) {
+                    if (b < nb) {
+                        const uint4 xv = *reinterpret_cast<const uint4*>(X + b * ldx + c);
+                        acc[b] = dot2(w.x, xv.x, acc[b]);
+                        acc[b] = dot2(w.y, xv.y, acc[b]);
+                        acc[b] = dot2(w.z, xv.z, acc[b]);
+                        acc[b] = dot2(w.w, xv.w, acc[b]);
+                    }
+                }
+            }
+        } else {
+            for (int c = lane; c < K; c += 64) {
+                const float w = h2f(wr[c]);
+#pragma unroll
+                for (int b = 0; b < kMaxBatch; ++b)
+                    if (b < nb) acc[b] = fmaf(w, h2f(X[b * ldx + c]), acc[b]);
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < kMaxBatch; ++b) {
+            if (b < nb) {
+                const float s = group_sum<64>(acc[b]);
+                if (lane == 0) Y[b * ldy + r] = f2h_bits(s);
+            }
+        }
+    }
+}
+
+// Order key of an fp16 logit: a larger key is picked earlier.  The key is
+// monotone in the value (the fp32 bit pattern with negative numbers inverted
+// and positive ones offset above them), -0 and +0 get the same key (torch.topk
+// sees them as equal), and every NaN ranks above +inf.  The smallest key, -inf,
+// is 0x007FFFFF, so 0 never occurs and marks a logit already taken.
+__device__ __forceinline__ uint32_t logit_key(uint32_t h) {
+    const float v = h2f(h);
+    if (v != v) return 0xFFFFFFFFu;
+    const uint32_t u = v == 0.f ? 0u : __builtin_bit_cast(uint32_t, v);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// One wave per token: k rounds of a wave-wide arg-max over the untaken
+// logits (composite key: logit key, then the lower index), then the softmax
+// of the picks in fp32: exp(l - max) / sum, rounded to fp16.
+__global__ __launch_bounds__(64) void route_topk(const uint16_t* __restrict__ logits, int E, int64_t ld, int k,
+                                                int32_t* __restrict__ idx, uint16_t* __restrict__ wts) {
+    __shared__ uint32_t key[kMaxExperts];
+    const int lane = threadIdx.x;
+    const uint16_t* L = logits + static_cast<int64_t>(blockIdx.x) * ld;
+    for (int e = lane; e < E; e += 64) key[e] = logit_key(L[e]);
+    __syncthreads();
+    int my_idx = 0;
+    float my_val = 0.f;
+    for (int i = 0; i < k; ++i) {
+        uint64_t best = 0;  // (key << 32) | ~index: max = largest key, then lowest index
+        for (int e = lane; e < E; e += 64) {
+            const uint64_t c = (static_cast<uint64_t>(key[e]) << 32) | static_cast<uint32_t>(~e);
+            best = c > best ? c : best;
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const uint64_t other = __shfl_xor(best, o, 64);
+            best = other > best ? other : best;
+        }
+        const int e = static_cast<int>(~static_cast<uint32_t>(best));
+        if (lane == i) {
+            my_idx = e;
+            my_val = h2f(L[e]);
+        }
+        // the winner's slot is marked taken before the next round reads it
+        if (lane == (e & 63)) key[e] = 0u;
+        __syncthreads();
+    }
+    const float m = __shfl(my_val, 0, 64);
+    const float ex = lane < k ? expf(fp32_rounded(my_val - m)) : 0.f;
+    const float sum = group_sum<64>(ex);
+    if (lane < k) {
+        idx[static_cast<int64_t>(blockIdx.x) * k + lane] = my_idx;
+        wts[static_cast<int64_t>(blockIdx.x) * k + lane] = f2h_bits(fp32_rounded(ex / sum));
+    }
+}
+
+// y = clamp(e + fp16(fp16(sigmoid(g)) * s), -65504, 65504) elementwise, g per token.
+__global__ __launch_bounds__(256) void moe_combine(const uint16_t* __restrict__ eo, const uint16_t* __restrict__ so,
+                                                   const uint16_t* __restrict__ gl, uint16_t* __restrict__ y,
+                                                   int64_t H, int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float g = h2f(gl[i / H]);
+    const float sw = h2f(f2h_bits(fp32_rounded(1.0f / fp32_rounded(1.0f + expf(-g)))));
+    const float s = h2f(f2h_bits(fp32_rounded(sw * h2f(so[i]))));
+    float r = h2f(f2h_bits(fp32_rounded(h2f(eo[i]) + s)));
+    if (r > 65504.0f) r = 65504.0f;   // NaN compares false both ways and stays NaN
+    if (r < -65504.0f) r = -65504.0f;
+    y[i] = f2h_bits(r);
+}
+
+}  // namespace
+}  // namespace gdsllm
+
+using namespace gdsllm;
+
+extern "C" int gdsllm_gemv_f16(const void* weight, const void* x, void* y, int64_t out_dim, int64_t in_dim,
+                               int64_t batch, int64_t ldx, int64_t ldy, void* stream) {
+    const std::string n = "gemv_f16";
+    if (out_dim < 0 || in_dim < 0) return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": negative dimension");
+    if (batch < 1 || batch > kMaxBatch)
+        return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": batch must be in [1, 8], got " + std::to_string(batch));
+    if (out_dim > (int64_t(1) << 30) || in_dim > (int64_t(1) << 24))
+        return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": dimension too large");
+    if (out_dim == 0 || in_dim == 0) return ok();
+    if (!weight || !x || !y) return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": null pointer");
+    if (batch > 1 && (ldx < in_dim || ldy < out_dim))
+        return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": ldx/ldy smaller than the row length");
+    if (reinterpret_cast<uintptr_t>(weight) % 2 || reinterpret_cast<uintptr_t>(x) % 2 ||
+        reinterpret_cast<uintptr_t>(y) % 2)
+        return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": weight, x and y must be 2-byte aligned");
+    const int M = static_cast<int>(out_dim), K = static_cast<int>(in_dim), B = static_cast<int>(batch);
+    const bool vec = K % 8 == 0 && reinterpret_cast<uintptr_t>(weight) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(x) % 16 == 0 && (B == 1 || ldx % 8 == 0);
+    const int waves_needed = M;
+    const int grid = std::min((waves_needed + kF16Waves - 1) / kF16Waves, 8 * cu_count());
+    const auto* w = static_cast<const uint16_t*>(weight);
+    const auto* xp = static_cast<const uint16_t*>(x);
+    auto* yp = static_cast<uint16_t*>(y);
+    if (vec)
+        hipLaunchKernelGGL(gemv_f16<true>, dim3(grid), dim3(kF16Waves * 64), 0, as_stream(stream), w, xp, yp, M, K,
+                           B, ldx, ldy);
+    else
+        hipLaunchKernelGGL(gemv_f16<false>, dim3(grid), dim3(kF16Waves * 64), 0, as_stream(stream), w, xp, yp, M, K,
+                           B, ldx, ldy);
+    if (int rc = check_hip(hipGetLastError(), "gemv_f16 launch")) return rc;
+    return ok();
+}
+
+extern "C" int gdsllm_moe_route_topk(const void* logits, int64_t num_experts, int64_t n_tok, int64_t ld_logits,
+                                     int64_t top_k, int32_t* idx, void* weights, void* stream) {
+    const std::string n = "moe_route_topk";
+    if (num_experts < 1 || num_experts > kMaxExperts)
+        return set_error(GDSLLM_ERR_INVALID_ARGUMENT,
+                         n + ": num_experts must be in [1, 4096], got " + std::to_string(num_experts));
+    if (top_k < 1 || top_k > kMaxTopK || top_k > num_experts)
+        return set_error(GDSLLM_ERR_INVALID_ARGUMENT,
+                         n + ": top_k must be in [1, min(64, num_experts)], got " + std::to_string(top_k));
+    if (n_tok < 0 || n_tok > (int64_t(1) << 31) - 1)
+        return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": bad token count");
+    if (n_tok == 0) return ok();
+    if (ld_logits < num_experts) return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": ld_logits < num_experts");
+    if (!logits || !idx || !weights) return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": null pointer");
+    if (reinterpret_cast<uintptr_t>(logits) % 2 || reinterpret_cast<uintptr_t>(weights) % 2 ||
+        reinterpret_cast<uintptr_t>(idx) % 4)
+        return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": misaligned pointer");
+    hipLaunchKernelGGL(route_topk, dim3(static_cast<unsigned>(n_tok)), dim3(64), 0, as_stream(stream),
+                       static_cast<const uint16_t*>(logits), static_cast<int>(num_experts), ld_logits,
+                       static_cast<int>(top_k), idx, static_cast<uint16_t*>(weights));
+    if (int rc = check_hip(hipGetLastError(), "moe_route_topk launch")) return rc;
+    return ok();
+}
+
+extern "C" int gdsllm_moe_combine(const void* expert_out, const void* shared_out, const void* shared_gate_logit,
+                                  void* y, int64_t hidden, int64_t n_tok, void* stream) {
+    const std::string n = "moe_combine";
+    if (hidden < 0 || n_tok < 0) return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": negative dimension");
+    if (hidden > (int64_t(1) << 24) || n_tok > (int64_t(1) << 24))
+        return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": dimension too large");
+    if (hidden == 0 || n_tok == 0) return ok();
+    if (!expert_out || !shared_out || !shared_gate_logit || !y)
+        return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": null pointer");
+    if ((reinterpret_cast<uintptr_t>(expert_out) | reinterpret_cast<uintptr_t>(shared_out) |
+         reinterpret_cast<uintptr_t>(shared_gate_logit) | reinterpret_cast<uintptr_t>(y)) % 2)
+        return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": pointers must be 2-byte aligned");
+    const int64_t total = hidden * n_tok;
+    hipLaunchKernelGGL(moe_combine, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, as_stream(stream),
+                       static_cast<const uint16_t*>(expert_out), static_cast<const uint16_t*>(shared_out),
+                       static_cast<const uint16_t*>(shared_gate_logit), static_cast<uint16_t*>(y), hidden, total);
+    if (int rc = check_hip(hipGetLastError(), "moe_combine launch")) return rc;
+    return ok();
+}

@@ -50,17 +50,34 @@ def affine_q4_linear(x: torch.Tensor, weights: Dict, name: str, scratch: Optiona
     return F.linear(x, w)
 
 
-def moe_route(
-    x: torch.Tensor, weights: Dict, num_experts_per_token: int, scratch: Optional[torch.Tensor] = None
-) -> Tuple[torch.Tensor, torch.Tensor, list]:
-    """runtime/qwen_moe.py:386-416: router logits -> top-k -> softmax (fp32) -> fp16."""
+def _router_logits(x: torch.Tensor, weights: Dict, scratch: Optional[torch.Tensor]) -> torch.Tensor:
+    """F.linear(x, router) (runtime/qwen_moe.py:405-408) on the device: the fp16
+    router through gemv_f16, an affine-Q4 router through its fused GEMV."""
     router_w = weights["mlp.gate.weight"]
     if isinstance(router_w, dict):
-        router_w = _dequant_affine_q4(router_w, scratch)
-    logits = F.linear(x, router_w)
-    top_logits, top_idx = torch.topk(logits, num_experts_per_token, dim=-1)
-    top_w = F.softmax(top_logits.float(), dim=-1).type_as(x)
-    return top_idx, top_w, top_idx.unique().tolist()
+        return affine_q4_linear(x, weights, "mlp.gate", scratch)
+    return ext().gemv_f16(router_w, x)
+
+
+def moe_route(
+    x: torch.Tensor,
+    weights: Dict,
+    num_experts_per_token: int,
+    scratch: Optional[torch.Tensor] = None,
+    sync_unique: bool = True,
+) -> Tuple[torch.Tensor, torch.Tensor, Optional[list]]:
+    """runtime/qwen_moe.py:386-416: router logits -> top-k -> fp16(softmax_fp32).
+
+    Logits, picks and weights stay on the device (gemv_f16 + moe_route_topk;
+    indices int32, ties to the lower expert index).  The sorted list of unique
+    experts needs the picks on the host: with sync_unique=False it is not built
+    (None) and nothing waits for the device, which is all the resident decode
+    path needs.
+    """
+    logits = _router_logits(x, weights, scratch)
+    top_idx, top_w = ext().moe_route_topk(logits, num_experts_per_token)
+    unique = sorted(set(top_idx.reshape(-1).tolist())) if sync_unique else None
+    return top_idx, top_w, unique
 
 
 _EXPERT_PROJ = ("mlp.switch_mlp.gate_proj", "mlp.switch_mlp.up_proj", "mlp.switch_mlp.down_proj")
@@ -153,6 +170,8 @@ def moe_mlp_selective(
     shared_out = affine_q4_linear(F.silu(shared_gate) * shared_up, weights, "mlp.shared_expert.down_proj", scratch)
     sg = weights["mlp.shared_expert_gate.weight"]
     if isinstance(sg, dict):
-        sg = _dequant_affine_q4(sg, scratch)
-    shared_out = torch.sigmoid(F.linear(x, sg)) * shared_out
-    return (expert_output + shared_out).clamp(min=-65504.0, max=65504.0)
+        gate_logit = affine_q4_linear(x, weights, "mlp.shared_expert_gate", scratch)
+    else:
+        gate_logit = ext().gemv_f16(sg, x)
+    # expert_output + sigmoid(gate) * shared_out, clamped (runtime/qwen_moe.py:508-513), in one kernel
+    return ext().moe_combine(expert_output, shared_out, gate_logit)

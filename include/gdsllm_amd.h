@@ -168,6 +168,39 @@ int gdsllm_moe_gather_affine_q4(const gdsllm_affine_experts* gate,
                                 void* y, void* workspace, size_t workspace_bytes,
                                 void* stream);
 
+/* --------------------------------------- on-device MoE routing, epilogue --
+ * The reference routes on the host side of a sync (F.linear, torch.topk,
+ * softmax, .tolist(); runtime/qwen_moe.py:386-416) and finishes the MoE MLP
+ * with elementwise torch ops (runtime/qwen_moe.py:496-513).  These keep the
+ * whole step on the device, feeding gdsllm_moe_gather_affine_q4 directly.   */
+
+/* y[b][r] = fp16( sum_k w[r][k] * x[b][k] ), fp16 weights row-major
+ * [out_dim][in_dim], fp32 accumulation, batch <= 8.  Replaces F.linear on the
+ * fp16 router (runtime/qwen_moe.py:408) and on the shared-expert gate
+ * (runtime/qwen_moe.py:505-508).                                            */
+int gdsllm_gemv_f16(const void* weight, const void* x, void* y,
+                    int64_t out_dim, int64_t in_dim, int64_t batch,
+                    int64_t ldx, int64_t ldy, void* stream);
+
+/* Per token t < n_tok, from fp16 logits at logits + t*ld_logits: the top_k
+ * largest in descending order into idx[t*top_k ...] (int32) and
+ * fp16(softmax_fp32(picked logits)) into weights[t*top_k ...].  Ties go to
+ * the lower expert index, NaN ranks above every number, -0 equals +0.
+ * num_experts <= 4096, top_k <= min(64, num_experts).  Replaces torch.topk +
+ * F.softmax(.float()).type_as(x) (runtime/qwen_moe.py:410-412).              */
+int gdsllm_moe_route_topk(const void* logits, int64_t num_experts,
+                          int64_t n_tok, int64_t ld_logits, int64_t top_k,
+                          int32_t* idx, void* weights, void* stream);
+
+/* y = clamp(expert_out + fp16(fp16(sigmoid(g_t)) * shared_out), +-65504)
+ * elementwise over n_tok rows of `hidden` fp16 values, g_t = the fp16 shared-
+ * expert gate logit of token t (shared_gate_logit[t]); each op in fp32 rounded
+ * to fp16 as torch does on fp16 tensors, NaN kept.  Replaces
+ * runtime/qwen_moe.py:508-513.                                              */
+int gdsllm_moe_combine(const void* expert_out, const void* shared_out,
+                       const void* shared_gate_logit, void* y,
+                       int64_t hidden, int64_t n_tok, void* stream);
+
 /* ---------------------------------------------------- prefill dequant-GEMM --
  * Y[t][r] = fp16( sum_k X[t][k] * W[r][k] ), t < tokens, on MFMA.  Replaces
  * the prefill branch dequant -> F.linear (runtime/llama.py:160-166).

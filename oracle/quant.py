@@ -162,3 +162,45 @@ def moe_gather(x, gate, up, down, idx, routing_weights):
     if acc is None:
         acc = np.zeros(0)
     return acc, hs
+
+
+def route_topk(logits, k: int):
+    """moe_route (runtime/qwen_moe.py:408-412): torch.topk(logits, k) then
+    F.softmax(top.float(), dim=-1).type_as(x), per row of fp16 logits [n, E].
+
+    Pick order: value descending, ties to the lower expert index, NaN above
+    every number, -0 equal to +0.  Softmax in float32: exp(l - max) / sum,
+    rounded to fp16.  Returns (idx int32 [n, k], weights fp16 [n, k]).
+    """
+    L = np.asarray(logits, dtype=np.float16).astype(np.float32)
+    n, E = L.shape
+    idx = np.empty((n, k), dtype=np.int32)
+    w = np.empty((n, k), dtype=np.float16)
+    for t in range(n):
+        v = L[t]
+        nan = np.isnan(v)
+        order = sorted(range(E), key=lambda e: (0, 0.0, e) if nan[e] else (1, -float(v[e]), e))
+        sel = np.asarray(order[:k], dtype=np.int64)
+        idx[t] = sel
+        top = v[sel]
+        with np.errstate(invalid="ignore", over="ignore"):
+            ex = np.exp((top - top[0]).astype(np.float32)).astype(np.float32)
+            total = np.float32(0.0)
+            for val in ex:
+                total = np.float32(total + val)
+            w[t] = (ex / total).astype(np.float16)
+    return idx, w
+
+
+def moe_combine(expert_out, shared_out, gate_logit):
+    """runtime/qwen_moe.py:508-513 on fp16 tensors [n, hidden] with one gate
+    logit per row: sw = fp16(sigmoid(g)) (fp32 math), s = fp16(sw * shared),
+    r = fp16(expert + s), then clamp to +-65504 (NaN stays NaN)."""
+    eo = np.asarray(expert_out, dtype=np.float16).astype(np.float32)
+    so = np.asarray(shared_out, dtype=np.float16).astype(np.float32)
+    g = np.asarray(gate_logit, dtype=np.float16).astype(np.float32).reshape(-1, 1)
+    with np.errstate(over="ignore", invalid="ignore"):
+        sw = (np.float32(1.0) / (np.float32(1.0) + np.exp(-g))).astype(np.float16).astype(np.float32)
+        s = (sw * so).astype(np.float16).astype(np.float32)
+        r = (eo + s).astype(np.float16)
+    return np.clip(r, np.float16(-65504.0), np.float16(65504.0))

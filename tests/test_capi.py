@@ -212,3 +212,23 @@ def test_extension_rejects_invalid_handle():
         m.fused_affine_q4_gemv(None, x, [4, 64], 0, 0, 0, 64)
     with pytest.raises(RuntimeError, match="invalid buffer handle"):
         m.view_tensor(None, [4], "float16", 0)
+
+
+def test_route_and_combine_validation():
+    lib = capi()
+    assert lib.gdsllm_gemv_f16(16, 16, 16, 4, 8, 9, 8, 4, None) == 1 and "batch" in _err()
+    assert lib.gdsllm_gemv_f16(16, 16, 16, -1, 8, 1, 8, 4, None) == 1
+    assert lib.gdsllm_gemv_f16(None, None, None, 0, 8, 1, 8, 4, None) == 0
+    assert lib.gdsllm_gemv_f16(None, 16, 16, 4, 8, 1, 8, 4, None) == 1 and "null" in _err()
+    assert lib.gdsllm_gemv_f16(16, 16, 16, 4, 8, 2, 4, 4, None) == 1 and "ldx" in _err()
+    idx = 16
+    assert lib.gdsllm_moe_route_topk(16, 512, 1, 512, 65, idx, 16, None) == 1 and "top_k" in _err()
+    assert lib.gdsllm_moe_route_topk(16, 8, 1, 8, 9, idx, 16, None) == 1 and "top_k" in _err()
+    assert lib.gdsllm_moe_route_topk(16, 5000, 1, 5000, 8, idx, 16, None) == 1 and "num_experts" in _err()
+    assert lib.gdsllm_moe_route_topk(16, 512, 1, 100, 8, idx, 16, None) == 1 and "ld_logits" in _err()
+    assert lib.gdsllm_moe_route_topk(16, 512, 0, 512, 8, idx, 16, None) == 0
+    assert lib.gdsllm_moe_route_topk(None, 512, 1, 512, 8, idx, 16, None) == 1 and "null" in _err()
+    assert lib.gdsllm_moe_combine(16, 16, 16, 16, -1, 1, None) == 1
+    assert lib.gdsllm_moe_combine(16, 16, 16, 16, 0, 1, None) == 0
+    assert lib.gdsllm_moe_combine(16, None, 16, 16, 8, 1, None) == 1 and "null" in _err()
+    assert lib.gdsllm_moe_combine(16, 17, 16, 16, 8, 1, None) == 1 and "aligned" in _err()

@@ -331,3 +331,66 @@ def test_affine_double_rounding_follows_reference():
         assert direct != twice
         out = oq.dequant_affine_q4(np.array([nib[i]], np.uint32), s[i:i + 1], b[i:i + 1], 8, 8)
         assert out.view(np.uint16)[0] == to_f16_bits(twice)
+
+
+# ------------------------------------------------------------- MoE routing
+
+
+def _topk_lexsort(v: np.ndarray, k: int) -> np.ndarray:
+    """Independent restatement of the pick order with np.lexsort: NaN first,
+    then value descending (-0 == +0), then index ascending."""
+    x = v.astype(np.float64)
+    nan = np.isnan(x)
+    val = np.where(nan, 0.0, -x) + 0.0  # + 0.0 turns -0 into +0
+    order = np.lexsort((np.arange(v.size), val, ~nan))
+    return order[:k]
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_route_topk_order_matches_lexsort(seed):
+    rng = np.random.default_rng(seed)
+    E = int(rng.integers(8, 300))
+    k = int(rng.integers(1, min(E, 64) + 1))
+    # few distinct values: many ties; plus specials
+    v = rng.integers(-4, 5, size=(3, E)).astype(np.float16) * np.float16(0.5)
+    v[0, rng.integers(0, E, 3)] = np.float16(np.nan)
+    v[1, rng.integers(0, E, 3)] = np.float16(-np.inf)
+    v[2, rng.integers(0, E, 3)] = np.float16(-0.0)
+    idx, w = oq.route_topk(v, k)
+    for t in range(3):
+        assert list(idx[t]) == list(_topk_lexsort(v[t], k))
+
+
+def test_route_topk_softmax_closed_forms():
+    # k = 1: weight exactly 1; two equal logits: 0.5 each; exp(0) / (1 + e^-1)
+    idx, w = oq.route_topk(np.array([[0.25, 3.0, -1.0]], np.float16), 1)
+    assert idx[0, 0] == 1 and w[0, 0] == np.float16(1.0)
+    idx, w = oq.route_topk(np.array([[2.0, -5.0, 2.0]], np.float16), 2)
+    assert list(idx[0]) == [0, 2] and list(w[0]) == [np.float16(0.5)] * 2
+    idx, w = oq.route_topk(np.array([[1.0, 0.0]], np.float16), 2)
+    e = math.exp(-1.0)
+    assert w[0, 0] == np.float16(1.0 / (1.0 + e)) and w[0, 1] == np.float16(e / (1.0 + e))
+    # weights of random rows sum to 1 within k half-ulps of 1 and do not increase
+    rng = np.random.default_rng(7)
+    idx, w = oq.route_topk(rng.standard_normal((4, 512)).astype(np.float16), 10)
+    ws = w.astype(np.float64)
+    assert np.all(np.abs(ws.sum(axis=1) - 1.0) <= 10 * 2.0 ** -11)
+    assert np.all(np.diff(ws, axis=1) <= 0)
+    # a planted mistake (picking the smallest) fails the lexsort check
+    v = rng.standard_normal(50).astype(np.float16)
+    assert list(np.argsort(v)[:5]) != list(_topk_lexsort(v, 5))
+
+
+def test_moe_combine_closed_forms():
+    eo = np.array([[1.0, -2.0, np.inf, np.nan, -60000.0, 3.0]], np.float16)
+    so = np.array([[2.0, 4.0, 1.0, 1.0, -60000.0, -6.0]], np.float16)
+    # g = 0: sigmoid = 0.5 exactly, so s = so / 2 exactly
+    r = oq.moe_combine(eo, so, [0.0])
+    assert list(r[0, :3]) == [np.float16(2.0), np.float16(0.0), np.float16(65504.0)]
+    assert np.isnan(r[0, 3]) and r[0, 4] == np.float16(-65504.0) and r[0, 5] == np.float16(0.0)
+    # g very negative: sigmoid rounds to 0 in fp16 -> r = eo (finite entries)
+    r = oq.moe_combine(np.array([[1.5, -7.0]], np.float16), np.array([[100.0, 100.0]], np.float16), [-30.0])
+    assert list(r[0]) == [np.float16(1.5), np.float16(-7.0)]
+    # g large: sigmoid = 1 -> r = fp16(eo + so)
+    r = oq.moe_combine(np.array([[1.0, 1024.0]], np.float16), np.array([[2.0, 0.5]], np.float16), [20.0])
+    assert list(r[0]) == [np.float16(3.0), np.float16(1024.0)]

@@ -281,9 +281,57 @@ def bench_moe(dev, calls: int = 64, reps: int = 20):
     ms = _replay_ms(run, reps) / calls
     per_expert = 2 * (Fd * H // 2 + 2 * 2 * Fd * H // g) + (H * Fd // 2 + 2 * 2 * H * Fd // g)
     nbytes = k * per_expert + 2 * H + 2 * H
-    return {"us_per_call": round(ms * 1e3, 3), "bytes_per_call": nbytes,
-            "GB_s": round(nbytes / (ms * 1e-3) / 1e9, 1), "pct_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / 80, 1),
-            "launches_per_call": 2, "pool_bytes": sum(t.numel() * t.element_size() for p in pools for t in p)}
+    out = {"us_per_call": round(ms * 1e3, 3), "bytes_per_call": nbytes,
+           "GB_s": round(nbytes / (ms * 1e-3) / 1e9, 1), "pct_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / 80, 1),
+           "launches_per_call": 2, "pool_bytes": sum(t.numel() * t.element_size() for p in pools for t in p)}
+
+    # The whole decode MoE step on the device, no host round trip: fp16 router
+    # GEMV (512 x 4096), top-k + softmax, the top-10 gather, the shared expert
+    # (ffn 1024, as a one-expert gather), the shared-gate GEMV and the combine.
+    # Every call routes its own token and reads its own router and shared
+    # expert (as the layers of a model do), so those come from HBM too.
+    router = (torch.randn(calls, E, H, generator=gen, device=dev) * 0.02).to(torch.float16)
+    sgate = (torch.randn(calls, H, generator=gen, device=dev) * 0.02).to(torch.float16)
+    shared = [syn.affine_q4_weights([calls, Fd, H], g, gen), syn.affine_q4_weights([calls, Fd, H], g, gen),
+              syn.affine_q4_weights([calls, H, Fd], g, gen)]
+    sh_g, sh_u, sh_d = (experts(p) for p in shared)
+    xs = syn.activations(calls, H, gen)
+    logits = torch.empty(calls, E, dtype=torch.float16, device=dev)
+    ridx = torch.empty(calls, k, dtype=torch.int32, device=dev)
+    rw = torch.empty(calls, k, dtype=torch.float16, device=dev)
+    eo, so, yy = (torch.empty(calls, H, dtype=torch.float16, device=dev) for _ in range(3))
+    gl = torch.empty(calls, 1, dtype=torch.float16, device=dev)
+    sidx = torch.arange(calls, dtype=torch.int32, device=dev)
+    sw = torch.ones(calls, dtype=torch.float16, device=dev)
+    ws1_bytes = capi().gdsllm_moe_gather_workspace_size(1, Fd)
+    ws1 = torch.empty(ws1_bytes, dtype=torch.uint8, device=dev)
+
+    def step():
+        s = torch.cuda.current_stream().cuda_stream
+        for i in range(calls):
+            xi = xs[i].data_ptr()
+            check(capi().gdsllm_gemv_f16(router[i].data_ptr(), xi, logits[i].data_ptr(), E, H, 1, H, E, s))
+            check(capi().gdsllm_moe_route_topk(logits[i].data_ptr(), E, 1, E, k, ridx[i].data_ptr(),
+                                               rw[i].data_ptr(), s))
+            check(capi().gdsllm_moe_gather_affine_q4(ctypes.byref(gate), ctypes.byref(up), ctypes.byref(down), xi,
+                                                     ridx[i].data_ptr(), rw[i].data_ptr(), k, eo[i].data_ptr(),
+                                                     ws.data_ptr(), ws_bytes, s))
+            check(capi().gdsllm_moe_gather_affine_q4(ctypes.byref(sh_g), ctypes.byref(sh_u), ctypes.byref(sh_d), xi,
+                                                     sidx[i:].data_ptr(), sw[i:].data_ptr(), 1, so[i].data_ptr(),
+                                                     ws1.data_ptr(), ws1_bytes, s))
+            check(capi().gdsllm_gemv_f16(sgate[i].data_ptr(), xi, gl[i].data_ptr(), 1, H, 1, H, 1, s))
+            check(capi().gdsllm_moe_combine(eo[i].data_ptr(), so[i].data_ptr(), gl[i].data_ptr(), yy[i].data_ptr(), H,
+                                            1, s))
+
+    ms2 = _replay_ms(step, reps) / calls
+    nbytes2 = E * H * 2 + (k + 1) * per_expert + H * 2 + 2 * H * 2
+    out["decode_step"] = {
+        "us_per_token_layer": round(ms2 * 1e3, 3), "bytes_per_token_layer": nbytes2,
+        "GB_s": round(nbytes2 / (ms2 * 1e-3) / 1e9, 1), "pct_of_hbm_peak": round(nbytes2 / (ms2 * 1e-3) / 1e9 / 80, 1),
+        "launches": 8, "host_syncs": 0,
+        "includes": "fp16 router GEMV 512x4096, top-k+softmax, top-10 gather, shared expert (ffn 1024), "
+                    "shared-gate GEMV, combine+clamp"}
+    return out
 
 
 LAYER_70B = [(8192, 8192), (1024, 8192), (1024, 8192), (8192, 8192), (28672, 8192), (28672, 8192), (8192, 28672)]

@@ -24,7 +24,7 @@ namespace {
 
 constexpr int kF16Waves = 4;      // waves per workgroup of the fp16 GEMV
 constexpr int kMaxBatch = 8;
-constexpr int kMaxExperts = 4096;  // logits of one token held in LDS
+constexpr int kMaxExperts = 4096;  // 64 pick words per lane
 constexpr int kMaxTopK = 64;       // one pick per lane
 
 // One wave per row, rows dealt round-robin over the grid's waves.  Vector
@@ -74,56 +74,79 @@ __global__ __launch_bounds__(kF16Waves * 64) void gemv_f16(const uint16_t* __res
     }
 }
 
-// Order key of an fp16 logit: a larger key is picked earlier.  The key is
-// monotone in the value (the fp32 bit pattern with negative numbers inverted
-// and positive ones offset above them), -0 and +0 get the same key (torch.topk
-// sees them as equal), and every NaN ranks above +inf.  The smallest key, -inf,
-// is 0x007FFFFF, so 0 never occurs and marks a logit already taken.
-__device__ __forceinline__ uint32_t logit_key(uint32_t h) {
-    const float v = h2f(h);
-    if (v != v) return 0xFFFFFFFFu;
-    const uint32_t u = v == 0.f ? 0u : __builtin_bit_cast(uint32_t, v);
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+// Pick word of logit e: a 16-bit order key of the fp16 value above a 16-bit
+// inverted index, so the largest word is the largest logit and, among equal
+// logits, the lowest index.  The key is monotone in the value (negative
+// encodings inverted, positive ones offset above them), -0 and +0 share a key
+// (torch.topk sees them as equal) and every NaN ranks above +inf.  The
+// smallest key, -inf's, is 0x03FF, so a word of 0 never occurs: it marks a
+// logit already taken.
+__device__ __forceinline__ uint32_t pick_word(uint32_t h, int e) {
+    const uint32_t mag = h & 0x7FFFu;
+    uint32_t key = (h & 0x8000u) ? (~h & 0xFFFFu) : (h | 0x8000u);
+    key = mag == 0 ? 0x8000u : key;         // +-0
+    key = mag > 0x7C00u ? 0xFFFFu : key;    // NaN
+    return (key << 16) | (0xFFFFu - static_cast<uint32_t>(e));
 }
 
-// One wave per token: k rounds of a wave-wide arg-max over the untaken
-// logits (composite key: logit key, then the lower index), then the softmax
-// of the picks in fp32: exp(l - max) / sum, rounded to fp16.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, false));
+}
+// Maximum over the wave, returned wave-uniform: DPP within each 16-lane row
+// (quad xor 1, quad xor 2, half-row mirror, row mirror), then the four row
+// maxima through readlane.
+__device__ __forceinline__ uint32_t wave_max(uint32_t v) {
+    v = max(v, dpp_u32<0xB1>(v));
+    v = max(v, dpp_u32<0x4E>(v));
+    v = max(v, dpp_u32<0x141>(v));
+    v = max(v, dpp_u32<0x140>(v));
+    const uint32_t r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16);
+    const uint32_t r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
+    return max(max(r0, r1), max(r2, r3));
+}
+
+// One wave per token.  NPL pick words per lane live in registers (logit
+// lane + 64*j), NPL * 64 >= E; k rounds of a wave-wide max take the next pick
+// and its owner clears it.  The softmax of the picks is in fp32, summed in
+// pick order: exp(l - max) / sum, rounded to fp16.
+template <int NPL>
 __global__ __launch_bounds__(64) void route_topk(const uint16_t* __restrict__ logits, int E, int64_t ld, int k,
                                                 int32_t* __restrict__ idx, uint16_t* __restrict__ wts) {
-    __shared__ uint32_t key[kMaxExperts];
     const int lane = threadIdx.x;
     const uint16_t* L = logits + static_cast<int64_t>(blockIdx.x) * ld;
-    for (int e = lane; e < E; e += 64) key[e] = logit_key(L[e]);
-    __syncthreads();
-    int my_idx = 0;
-    float my_val = 0.f;
-    for (int i = 0; i < k; ++i) {
-        uint64_t best = 0;  // (key << 32) | ~index: max = largest key, then lowest index
-        for (int e = lane; e < E; e += 64) {
-            const uint64_t c = (static_cast<uint64_t>(key[e]) << 32) | static_cast<uint32_t>(~e);
-            best = c > best ? c : best;
-        }
+    // all loads first (unconditional, past E re-reading logit 0): a load under
+    // a branch would be waited for before the next one is issued
+    uint32_t h[NPL], word[NPL];
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const uint64_t other = __shfl_xor(best, o, 64);
-            best = other > best ? other : best;
-        }
-        const int e = static_cast<int>(~static_cast<uint32_t>(best));
+    for (int j = 0; j < NPL; ++j) h[j] = L[lane + 64 * j < E ? lane + 64 * j : 0];
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) word[j] = lane + 64 * j < E ? pick_word(h[j], lane + 64 * j) : 0u;
+    // Each round's pick is wave-uniform; its value is decoded from the key
+    // (+-0 -> +0, NaN -> NaN, both softmax-neutral), its exp(l - max) computed
+    // once and summed in pick order, and lane i keeps pick i.
+    int my_idx = 0;
+    float my_ex = 0.f, m = 0.f, sum = 0.f;
+    for (int i = 0; i < k; ++i) {
+        uint32_t best = 0;
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) best = word[j] > best ? word[j] : best;
+        best = wave_max(best);
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) word[j] = word[j] == best ? 0u : word[j];
+        const uint32_t key = best >> 16;
+        const float v = key == 0xFFFFu ? __builtin_nanf("") : h2f((key & 0x8000u) ? (key & 0x7FFFu) : (~key & 0xFFFFu));
+        if (i == 0) m = v;
+        const float ex = expf(fp32_rounded(v - m));
+        sum = fp32_rounded(sum + ex);
         if (lane == i) {
-            my_idx = e;
-            my_val = h2f(L[e]);
+            my_idx = static_cast<int>(0xFFFFu - (best & 0xFFFFu));
+            my_ex = ex;
         }
-        // the winner's slot is marked taken before the next round reads it
-        if (lane == (e & 63)) key[e] = 0u;
-        __syncthreads();
     }
-    const float m = __shfl(my_val, 0, 64);
-    const float ex = lane < k ? expf(fp32_rounded(my_val - m)) : 0.f;
-    const float sum = group_sum<64>(ex);
     if (lane < k) {
         idx[static_cast<int64_t>(blockIdx.x) * k + lane] = my_idx;
-        wts[static_cast<int64_t>(blockIdx.x) * k + lane] = f2h_bits(fp32_rounded(ex / sum));
+        wts[static_cast<int64_t>(blockIdx.x) * k + lane] = f2h_bits(fp32_rounded(my_ex / sum));
     }
 }
 
@@ -197,9 +220,15 @@ extern "C" int gdsllm_moe_route_topk(const void* logits, int64_t num_experts, in
     if (reinterpret_cast<uintptr_t>(logits) % 2 || reinterpret_cast<uintptr_t>(weights) % 2 ||
         reinterpret_cast<uintptr_t>(idx) % 4)
         return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": misaligned pointer");
-    hipLaunchKernelGGL(route_topk, dim3(static_cast<unsigned>(n_tok)), dim3(64), 0, as_stream(stream),
-                       static_cast<const uint16_t*>(logits), static_cast<int>(num_experts), ld_logits,
-                       static_cast<int>(top_k), idx, static_cast<uint16_t*>(weights));
+    const auto* l = static_cast<const uint16_t*>(logits);
+    auto* w = static_cast<uint16_t*>(weights);
+    const int E = static_cast<int>(num_experts), k = static_cast<int>(top_k);
+    const dim3 grid(static_cast<unsigned>(n_tok)), block(64);
+    const hipStream_t s = as_stream(stream);
+    if (E <= 128) hipLaunchKernelGGL(route_topk<2>, grid, block, 0, s, l, E, ld_logits, k, idx, w);
+    else if (E <= 512) hipLaunchKernelGGL(route_topk<8>, grid, block, 0, s, l, E, ld_logits, k, idx, w);
+    else if (E <= 1024) hipLaunchKernelGGL(route_topk<16>, grid, block, 0, s, l, E, ld_logits, k, idx, w);
+    else hipLaunchKernelGGL(route_topk<64>, grid, block, 0, s, l, E, ld_logits, k, idx, w);
     if (int rc = check_hip(hipGetLastError(), "moe_route_topk launch")) return rc;
     return ok();
 }

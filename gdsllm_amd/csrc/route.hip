@@ -30,19 +30,45 @@ constexpr int kMaxTopK = 64;       // one pick per lane
 // One wave per row, rows dealt round-robin over the grid's waves.  Vector
 // path: each lane takes 8 consecutive weights of every 512-column chunk as one
 // 16-byte load (the row length is a multiple of 8 and every row start is
-// 16-byte aligned).  Scalar path: one element per lane per 64 columns.
-template <bool VEC>
+// 16-byte aligned); the NCH loads of a row (NCH = 0: a loop over the row) are
+// all issued before the first dot product, so a wave has its whole row in
+// flight.  Scalar path: one element per lane per 64 columns.
+template <bool VEC, int NCH>
 __global__ __launch_bounds__(kF16Waves * 64) void gemv_f16(const uint16_t* __restrict__ W,
                                                            const uint16_t* __restrict__ X, uint16_t* __restrict__ Y,
                                                            int M, int K, int nb, int64_t ldx, int64_t ldy) {
     const int lane = threadIdx.x & 63;
-    const int nwaves = static_cast<int>(gridDim.x) * kF16Waves;
-    for (int r = static_cast<int>(blockIdx.x) * kF16Waves + (threadIdx.x >> 6); r < M; r += nwaves) {
+    const int wpb = static_cast<int>(blockDim.x) >> 6;
+    const int nwaves = static_cast<int>(gridDim.x) * wpb;
+    for (int r = static_cast<int>(blockIdx.x) * wpb + (threadIdx.x >> 6); r < M; r += nwaves) {
         const uint16_t* wr = W + static_cast<int64_t>(r) * K;
         float acc[kMaxBatch];
 #pragma unroll
         for (int b = 0; b < kMaxBatch; ++b) acc[b] = 0.f;
-        if constexpr (VEC) {
+        if constexpr (VEC && NCH > 0) {
+            uint4 w[NCH];
+#pragma unroll
+            for (int i = 0; i < NCH; ++i) {
+                const int c = 8 * lane + 512 * i;
+                w[i] = c < K ? load_nt16(wr + c) : make_uint4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int b = 0; b < kMaxBatch; ++b) {
+                if (b < nb) {
+#pragma unroll
+                    for (int i = 0; i < NCH; ++i) {
+                        const int c = 8 * lane + 512 * i;
+                        if (c < K) {
+                            const uint4 xv = *reinterpret_cast<const uint4*>(X + b * ldx + c);
+                            acc[b] = dot2(w[i].x, xv.x, acc[b]);
+                            acc[b] = dot2(w[i].y, xv.y, acc[b]);
+                            acc[b] = dot2(w[i].z, xv.z, acc[b]);
+                            acc[b] = dot2(w[i].w, xv.w, acc[b]);
+                        }
+                    }
+                }
+            }
+        } else if constexpr (VEC) {
             for (int c = 8 * lane; c < K; c += 512) {
                 const uint4 w = load_nt16(wr + c);
 #pragma unroll
@@ -188,17 +214,30 @@ extern "C" int gdsllm_gemv_f16(const void* weight, const void* x, void* y, int64
     const int M = static_cast<int>(out_dim), K = static_cast<int>(in_dim), B = static_cast<int>(batch);
     const bool vec = K % 8 == 0 && reinterpret_cast<uintptr_t>(weight) % 16 == 0 &&
                      reinterpret_cast<uintptr_t>(x) % 16 == 0 && (B == 1 || ldx % 8 == 0);
-    const int waves_needed = M;
-    const int grid = std::min((waves_needed + kF16Waves - 1) / kF16Waves, 8 * cu_count());
     const auto* w = static_cast<const uint16_t*>(weight);
     const auto* xp = static_cast<const uint16_t*>(x);
     auto* yp = static_cast<uint16_t*>(y);
-    if (vec)
-        hipLaunchKernelGGL(gemv_f16<true>, dim3(grid), dim3(kF16Waves * 64), 0, as_stream(stream), w, xp, yp, M, K,
-                           B, ldx, ldy);
-    else
-        hipLaunchKernelGGL(gemv_f16<false>, dim3(grid), dim3(kF16Waves * 64), 0, as_stream(stream), w, xp, yp, M, K,
-                           B, ldx, ldy);
+    const hipStream_t st = as_stream(stream);
+    if (vec && K <= 16 * 512) {
+        // one-wave workgroups, so even a few hundred rows reach every CU
+        const int grid = std::min(M, 32 * cu_count());
+        const int nch = (K + 511) / 512;
+        auto launch = [&](auto kern) {
+            hipLaunchKernelGGL(kern, dim3(grid), dim3(64), 0, st, w, xp, yp, M, K, B, ldx, ldy);
+        };
+        if (nch <= 2) launch(gemv_f16<true, 2>);
+        else if (nch <= 4) launch(gemv_f16<true, 4>);
+        else if (nch <= 8) launch(gemv_f16<true, 8>);
+        else launch(gemv_f16<true, 16>);
+    } else {
+        const int grid = std::min((M + kF16Waves - 1) / kF16Waves, 8 * cu_count());
+        if (vec)
+            hipLaunchKernelGGL((gemv_f16<true, 0>), dim3(grid), dim3(kF16Waves * 64), 0, st, w, xp, yp, M, K, B, ldx,
+                               ldy);
+        else
+            hipLaunchKernelGGL((gemv_f16<false, 0>), dim3(grid), dim3(kF16Waves * 64), 0, st, w, xp, yp, M, K, B,
+                               ldx, ldy);
+    }
     if (int rc = check_hip(hipGetLastError(), "gemv_f16 launch")) return rc;
     return ok();
 }

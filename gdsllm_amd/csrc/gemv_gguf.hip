@@ -583,34 +583,34 @@ size_t rows_lds_bytes(int nw, int wpg) {
     return static_cast<size_t>(wpg) * stage_bytes<F>() + static_cast<size_t>(rows_xraw_bytes(NB, nw));
 }
 
-// Rows R0 and R0+1 of a stage in LDS: lane c's blocks 2c, 2c+1 of each row
-// against its x slice, added to acc[b][R0], acc[b][R0+1].  The 2 rows x 2
-// blocks x NB dot-product chains interleave.
-template <Fmt F, int NB, int R0>
+// Rows R0 .. R0+NR-1 of a stage in LDS: lane c's blocks 2c, 2c+1 of each row
+// against its x slice, added to acc[b][R0+r].  The NR rows x 2 blocks x NB
+// dot-product chains interleave.
+template <Fmt F, int NB, int R0, int NR = 2>
 __device__ __forceinline__ void rows_pair(const uint8_t* buf, const XSlice<NB>& xs, float (&acc)[NB][4],
                                           const NibUnpack& nu, int lane) {
     using L = Layout<F>;
     constexpr int kSegBytes = kSbPerWindow * L::kSbBytes;
     constexpr int kSpanDw = L::kBlockBytes / 2;  // dwords of a lane's 2 blocks
     constexpr int kQd = (L::kBlockBytes - 2) / 4;  // qs dwords per block
-    uint32_t D[2][kSpanDw];
+    uint32_t D[NR][kSpanDw];
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
+    for (int r = 0; r < NR; ++r) {
         const uint32_t* src = reinterpret_cast<const uint32_t*>(buf + (R0 + r) * kSegBytes) + kSpanDw * lane;
 #pragma unroll
         for (int i = 0; i < kSpanDw; ++i) D[r][i] = src[i];
     }
     // block 2c: scale = bytes 0-1, qs from byte 2; block 2c+1 starts at byte
     // kBlockBytes (dword-aligned halfway point: scale in the high half)
-    float Sx[NB][2][2];
+    float Sx[NB][NR][2];
 #pragma unroll
     for (int b = 0; b < NB; ++b)
 #pragma unroll
-        for (int r = 0; r < 2; ++r) Sx[b][r][0] = Sx[b][r][1] = 0.f;
+        for (int r = 0; r < NR; ++r) Sx[b][r][0] = Sx[b][r][1] = 0.f;
 #pragma unroll
     for (int dd = 0; dd < kQd; ++dd)
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
+        for (int r = 0; r < NR; ++r) {
             const uint32_t q0 = align2(D[r][dd], D[r][dd + 1]);
             const uint32_t q1 = D[r][kQd + 1 + dd];
 #pragma unroll
@@ -620,7 +620,7 @@ __device__ __forceinline__ void rows_pair(const uint8_t* buf, const XSlice<NB>& 
             }
         }
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
+    for (int r = 0; r < NR; ++r) {
         const float d0 = h2f(D[r][0] & 0xFFFFu), d1 = h2f(D[r][kQd] >> 16);
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
@@ -642,8 +642,10 @@ __global__ __launch_bounds__(kWaves * 64) void gguf_gemv_rows(const RowsTarget t
     using L = Layout<F>;
     constexpr int C = L::kSbChunks;                        // transfers per stage
     constexpr int kSegChunks = kSbPerWindow * L::kSbChunks;
-    constexpr int kHalf = (2 * kSegChunks + 63) / 64;      // transfers that complete rows 0-1
+    // transfers (of 64 16-byte chunks) that complete stage rows 0 .. r
+    constexpr int kRowDone[4] = {(kSegChunks + 63) / 64, (2 * kSegChunks + 63) / 64, (3 * kSegChunks + 63) / 64, C};
     constexpr int kEarly = (2 * kSegChunks) / 64;          // transfers within rows 0-1 only
+    static_assert(C - kRowDone[2] + kEarly < 64, "vmcnt range");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int S = K >> 8;
     const uint32_t row_bytes = static_cast<uint32_t>(S) * L::kSbBytes;
@@ -700,19 +702,26 @@ __global__ __launch_bounds__(kWaves * 64) void gguf_gemv_rows(const RowsTarget t
         }
         // Lanes past the end of a partial window skip; rows past M compute on
         // filler bytes and are never stored.  In flight here: this stage only.
+        // Each row is consumed as soon as the transfers that hold it retire.
         const bool active = lane < st.nsb * 4;
-        wait_vmcnt<C - kHalf>();
-        if (active) rows_pair<F, NB, 0>(buf, xs, acc, nu, lane);
+        wait_vmcnt<C - kRowDone[0]>();
+        if (active) rows_pair<F, NB, 0, 1>(buf, xs, acc, nu, lane);
+        wait_vmcnt<C - kRowDone[1]>();
+        if (active) rows_pair<F, NB, 1, 1>(buf, xs, acc, nu, lane);
         // refill slots of rows 0-1 once their reads have returned
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         const RowsStage nx = stage_at(t + 1);
         if (next) {
             rows_issue<F, 0, kEarly, PAIRED>(buf, nx, X, row_bytes, goff, true, lane);
+            wait_vmcnt<C - kRowDone[2] + kEarly>();
+            if (active) rows_pair<F, NB, 2, 1>(buf, xs, acc, nu, lane);
             wait_vmcnt<kEarly>();
         } else {
+            wait_vmcnt<C - kRowDone[2]>();
+            if (active) rows_pair<F, NB, 2, 1>(buf, xs, acc, nu, lane);
             wait_vmcnt<0>();
         }
-        if (active) rows_pair<F, NB, 2>(buf, xs, acc, nu, lane);
+        if (active) rows_pair<F, NB, 3, 1>(buf, xs, acc, nu, lane);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         if (next) rows_issue<F, kEarly, C, PAIRED>(buf, nx, X, row_bytes, goff, true, lane);
         if (win == NW - 1) {

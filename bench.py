@@ -394,6 +394,64 @@ def bench_prefill(dev, layers, lm_head, tokens: int = 512, reps: int = 3):
             "pct_of_fp16_dense_peak": round(flops / (ms * 1e-3) / 1e12 / 25, 1)}
 
 
+def bench_load(dev, layers: int = 2, reps: int = 3, tokens: int = 512, emb_reps: int = 20):
+    """Converted LLaMA-7B Q4_0 directory (files written first, so they are page-
+    cache resident): one layer file (113 MB) into HBM through
+    ModelWeights.load_layer (pread -> pinned staging -> hipMemcpyAsync), and the
+    embedding lookup of a 512-token chunk from the 32000 x 4096 Q4_0 table:
+    row gather against the reference's whole-table dequant + F.embedding."""
+    import shutil
+    import tempfile
+
+    import torch
+    import torch.nn.functional as F
+
+    from gdsllm_amd.runtime import ext
+    from gdsllm_amd.runtime.scheduler import _embed_tokens
+    from gdsllm_amd.runtime.torch_bridge import ModelWeights
+    from gdsllm_amd.synthetic_model import write_llama
+
+    d = tempfile.mkdtemp(prefix="gdsllm_load_", dir="/dev/shm" if os.path.isdir("/dev/shm") else None)
+    try:
+        write_llama(d, "q4_0", layers=layers, hidden=4096, ffn=11008, vocab=32000, seed=1006)
+        mw = ModelWeights(d)
+        mw.init_gds()
+        times = []
+        for _ in range(reps):
+            for i in range(layers):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                tensors, handle = mw.load_layer(i)
+                torch.cuda.synchronize()
+                times.append(time.perf_counter() - t0)
+                del tensors, handle
+        times.sort()
+        size = mw.layers[0].size_bytes
+        emb, emb_handle = mw.load_special("embed_tokens")
+        w = emb["model.embed_tokens.weight"]
+        ids = torch.randint(0, 32000, (1, tokens), device=dev, generator=torch.Generator(device=dev).manual_seed(7))
+
+        def timed(fn):
+            fn()
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(emb_reps):
+                fn()
+            b.record()
+            torch.cuda.synchronize()
+            return a.elapsed_time(b) * 1e3 / emb_reps
+
+        gather_us = timed(lambda: _embed_tokens(ids, emb))
+        full_us = timed(lambda: F.embedding(ids, ext().dequant_gguf(w["buffer"], w["shape"], "q4_0", w["offset"])))
+        return {"layer_file_bytes": size, "load_ms_median": round(times[len(times) // 2] * 1e3, 3),
+                "load_GB_s": round(size / times[len(times) // 2] / 1e9, 2),
+                "embed_512_gather_us": round(gather_us, 2), "embed_512_full_table_dequant_us": round(full_us, 2),
+                "source": "page-cache resident files (tmpfs when /dev/shm exists)"}
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+
+
 def cpu_baseline(weights_dev, x_dev, y_gpu, seconds: float):
     """Oracle-side torch restatement of dequant -> F.linear (fp32) on the host
     cores, timed over a bounded number of calls; also checks the GPU result."""
@@ -440,9 +498,10 @@ def main() -> int:
     ap.add_argument("--chunk", type=int, default=64, help="launches per captured graph")
     ap.add_argument("--sweep-tokens", type=int, default=100, help="timed 7B decode-sweep tokens (0 = skip)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget (0 = skip)")
-    ap.add_argument("--configs", default="q8,moe,70b,prefill",
+    ap.add_argument("--configs", default="q8,moe,70b,prefill,load",
                     help="comma list of extra workloads to measure: q8 (Q8_0 7B layer), moe (top-10 expert "
-                         "gather), 70b (Q4_0 70B layer, B=1..8), prefill (512-token MFMA GEMM); '' = none")
+                         "gather), 70b (Q4_0 70B layer, B=1..8), prefill (512-token MFMA GEMM), load (7B layer "
+                         "file -> HBM, embedding row gather); '' = none")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -482,7 +541,7 @@ def main() -> int:
               f"(unfused 225 launches: {sweep['unfused']['tok_s']} tok/s)", file=sys.stderr, flush=True)
 
     wanted = {c.strip() for c in args.configs.split(",") if c.strip()}
-    unknown = wanted - {"q8", "moe", "70b", "prefill"}
+    unknown = wanted - {"q8", "moe", "70b", "prefill", "load"}
     if unknown:
         print(f"bench.py: unknown --configs entries {sorted(unknown)}", file=sys.stderr)
         return 2
@@ -491,7 +550,8 @@ def main() -> int:
             ("moe", "moe_affine_q4_top10", lambda: bench_moe(dev)),
             ("70b", "q4_0_layer_70b", lambda: bench_70b_layer(dev)),
             ("prefill", "prefill_7b_512",
-             lambda: bench_prefill(dev, *sweep_weights) if sweep_weights is not None else None)]
+             lambda: bench_prefill(dev, *sweep_weights) if sweep_weights is not None else None),
+            ("load", "load_7b_q4_0", lambda: bench_load(dev))]
     for key, name, fn in runs:
         if key in wanted:
             res = fn()

@@ -40,6 +40,8 @@ SIGNATURES = {
     "gdsllm_buffer_read_file": (ctypes.c_int, [_c_vp, ctypes.c_size_t, ctypes.c_char_p, ctypes.c_size_t, _c_i64, _c_i64, ctypes.c_int, ctypes.POINTER(_c_i64)]),
     "gdsllm_dequant_q4_0": (ctypes.c_int, [_c_vp, _c_vp, _c_i64, _c_vp]),
     "gdsllm_dequant_q8_0": (ctypes.c_int, [_c_vp, _c_vp, _c_i64, _c_vp]),
+    "gdsllm_embed_q4_0": (ctypes.c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp]),
+    "gdsllm_embed_q8_0": (ctypes.c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp]),
     "gdsllm_dequant_affine_q4": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp]),
     "gdsllm_fused_q4_0_gemv": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp]),
     "gdsllm_fused_q8_0_gemv": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp]),

@@ -136,6 +136,55 @@ __global__ __launch_bounds__(kThreads) void dequant_q8_0_bytes(const uint8_t* __
     for (int j = 0; j < 32; ++j) o[j] = f2h_bits(fp32_rounded(d * static_cast<float>(static_cast<int8_t>(s[2 + j]))));
 }
 
+// ---- token-row gather (embedding lookup) ----------------------------------------
+// Row ids[t] of a [vocab][hidden] GGUF table, dequantized into out[t][hidden]
+// with the same per-element rounding as above: F.embedding over the dequantized
+// table (runtime/scheduler.py:22-35) without dequantizing the other rows.
+// grid.y = token, grid.x covers the row's block pairs (hidden % 64 == 0, the
+// table 4-byte aligned); ids outside [0, vocab) give a zero row.
+template <bool Q8>
+__global__ __launch_bounds__(kThreads) void embed_rows_pairs(const uint8_t* __restrict__ table,
+                                                              const int64_t* __restrict__ ids, int64_t vocab,
+                                                              int64_t hidden, uint4* __restrict__ out) {
+    const int64_t t = blockIdx.y;
+    const int64_t pairs = hidden / 64;
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (p >= pairs) return;
+    const int64_t id = ids[t];
+    uint4* o = out + (t * hidden + 64 * p) / 8;
+    if (id < 0 || id >= vocab) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = make_uint4(0, 0, 0, 0);
+        return;
+    }
+    constexpr int kPairDw = Q8 ? 17 : 9;
+    const uint32_t* s =
+        reinterpret_cast<const uint32_t*>(table + id * (hidden / 32) * (Q8 ? 34 : 18)) + p * kPairDw;
+    uint32_t v[kPairDw];
+#pragma unroll
+    for (int i = 0; i < kPairDw; ++i) v[i] = s[i];
+    if constexpr (Q8) {
+        uint32_t q0[8], q1[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            q0[i] = align2(v[i], v[i + 1]);
+            q1[i] = v[9 + i];
+        }
+        q8_block_to_fp16(v[0] & 0xFFFFu, q0, o);
+        q8_block_to_fp16(v[8] >> 16, q1, o + 4);
+    } else {
+        uint32_t q0[4] = {align2(v[0], v[1]), align2(v[1], v[2]), align2(v[2], v[3]), align2(v[3], v[4])};
+        uint32_t q1[4] = {v[5], v[6], v[7], v[8]};
+        uint32_t w[16];
+        q4_block_to_fp16(v[0] & 0xFFFFu, q0, w);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
+        q4_block_to_fp16(v[4] >> 16, q1, w);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[4 + i] = make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
+    }
+}
+
 // ---- affine Q4 --------------------------------------------------------------
 // Word w holds elements 8w..8w+7, nibble n = (word >> 4n) & 15 (LSB first);
 // group = element / group_size over the flat index; value = nib*s + b in fp32,
@@ -266,4 +315,40 @@ extern "C" int gdsllm_dequant_affine_q4(const void* weight, const void* scales, 
     }
     if (int rc = check_hip(hipGetLastError(), "dequant_affine_q4 launch")) return rc;
     return ok();
+}
+
+namespace {
+int embed_rows(bool q8, const void* table, const int64_t* ids, int64_t n_tokens, int64_t vocab, int64_t hidden,
+               void* out, void* stream) {
+    const std::string n = q8 ? "embed_q8_0" : "embed_q4_0";
+    if (n_tokens < 0 || vocab < 0 || hidden < 0) return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": negative size");
+    if (n_tokens == 0 || hidden == 0) return ok();
+    if (!table || !ids || !out) return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": null pointer");
+    if (hidden % 64 != 0)
+        return set_error(GDSLLM_ERR_UNSUPPORTED, n + ": hidden must be a multiple of 64, got " + std::to_string(hidden));
+    if (n_tokens > 65535 || hidden > (int64_t(1) << 24))
+        return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": too many tokens (max 65535 per call) or hidden too large");
+    if (reinterpret_cast<uintptr_t>(table) % 4 || reinterpret_cast<uintptr_t>(out) % 16 ||
+        reinterpret_cast<uintptr_t>(ids) % 8)
+        return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": table must be 4-byte, out 16-byte, ids 8-byte aligned");
+    const dim3 grid(static_cast<unsigned>((hidden / 64 + kThreads - 1) / kThreads), static_cast<unsigned>(n_tokens));
+    if (q8)
+        hipLaunchKernelGGL(embed_rows_pairs<true>, grid, dim3(kThreads), 0, as_stream(stream),
+                           static_cast<const uint8_t*>(table), ids, vocab, hidden, static_cast<uint4*>(out));
+    else
+        hipLaunchKernelGGL(embed_rows_pairs<false>, grid, dim3(kThreads), 0, as_stream(stream),
+                           static_cast<const uint8_t*>(table), ids, vocab, hidden, static_cast<uint4*>(out));
+    if (int rc = check_hip(hipGetLastError(), (n + " launch").c_str())) return rc;
+    return ok();
+}
+}  // namespace
+
+extern "C" int gdsllm_embed_q4_0(const void* table, const int64_t* token_ids, int64_t n_tokens, int64_t vocab,
+                                 int64_t hidden, void* out, void* stream) {
+    return embed_rows(false, table, token_ids, n_tokens, vocab, hidden, out, stream);
+}
+
+extern "C" int gdsllm_embed_q8_0(const void* table, const int64_t* token_ids, int64_t n_tokens, int64_t vocab,
+                                 int64_t hidden, void* out, void* stream) {
+    return embed_rows(true, table, token_ids, n_tokens, vocab, hidden, out, stream);
 }

@@ -233,6 +233,38 @@ torch::Tensor dequant_gguf(const Handle& h, std::vector<int64_t> shape, const st
     return out;
 }
 
+// Embedding rows of a GGUF table [vocab, hidden] for token_ids (any shape,
+// int64/int32, on the buffer's device): output token_ids.shape + [hidden]
+// fp16, the rows F.embedding would take from the dequantized table
+// (runtime/scheduler.py:22-35) without dequantizing the rest of it.
+torch::Tensor embed_gguf(const Handle& h, torch::Tensor token_ids, std::vector<int64_t> shape,
+                         const std::string& gguf_type, int64_t offset) {
+    const char* where = "embed_gguf";
+    check_handle(h, where);
+    if (shape.size() != 2) throw std::runtime_error("embed_gguf: shape must be [vocab, hidden]");
+    const int64_t vocab = shape[0], hidden = shape[1];
+    const int64_t bb = gguf_block_bytes(gguf_type, where);
+    if (hidden % 32 != 0) throw std::runtime_error("embed_gguf: hidden must be a multiple of 32");
+    check_range(h, offset, vocab * (hidden / 32) * bb, where);
+    if (!token_ids.is_cuda() || token_ids.get_device() != h->device_id())
+        throw std::runtime_error("embed_gguf: token_ids must be on the weight buffer's device");
+    auto ids = token_ids.to(torch::kInt64).contiguous().view(-1);
+    std::vector<int64_t> out_shape(token_ids.sizes().begin(), token_ids.sizes().end());
+    out_shape.push_back(hidden);
+    auto out = torch::empty(out_shape, fp16_on(h->device_id()));
+    void* s = stream_of(h->device_id());
+    const int64_t n = ids.numel();
+    for (int64_t t = 0; t < n; t += 65535) {
+        const int64_t c = std::min<int64_t>(65535, n - t);
+        const auto* ip = ids.data_ptr<int64_t>() + t;
+        auto* op = static_cast<uint16_t*>(out.data_ptr()) + t * hidden;
+        const int rc = gguf_type == "q4_0" ? gdsllm_embed_q4_0(at_offset(h, offset), ip, c, vocab, hidden, op, s)
+                                           : gdsllm_embed_q8_0(at_offset(h, offset), ip, c, vocab, hidden, op, s);
+        check(rc, where);
+    }
+    return out;
+}
+
 // x: [in_dim] / [1, in_dim] (the reference's contract) or [B, in_dim], B <= 8.
 // Returns [B, out_dim]; B = 1 reproduces the reference's [1, out_dim].
 torch::Tensor fused_dequant_gemv(const Handle& h, torch::Tensor x, std::vector<int64_t> weight_shape,
@@ -513,6 +545,8 @@ PYBIND11_MODULE(gds_io_ext, m) {
     m.def("dequant_gguf", &dequant_gguf, "Dequantize GGUF Q4_0/Q8_0 blocks from a buffer to fp16.",
           py::arg("handle"), py::arg("shape"), py::arg("gguf_type"), py::arg("offset"),
           py::arg("output") = py::none());
+    m.def("embed_gguf", &embed_gguf, "Embedding rows of a GGUF Q4_0/Q8_0 table, dequantized on the fly.",
+          py::arg("handle"), py::arg("token_ids"), py::arg("shape"), py::arg("gguf_type"), py::arg("offset") = 0);
     m.def("fused_dequant_gemv", &fused_dequant_gemv, "Fused dequant + GEMV for Q4_0/Q8_0 (decode).",
           py::arg("handle"), py::arg("x"), py::arg("weight_shape"), py::arg("gguf_type"), py::arg("offset"));
     m.def("dequant_affine_q4", &dequant_affine_q4, "Dequantize affine Q4 (uint32 + scales + biases) to fp16.",

@@ -69,6 +69,16 @@ int gdsllm_dequant_q4_0(const void* src, void* dst, int64_t num_blocks, void* st
 /* Replaces launch_dequant_q8_0 (runtime/gguf_dequant.h:19-20,
  * runtime/gguf_dequant.cu:60-68).  dst: fp16[num_blocks*32].              */
 int gdsllm_dequant_q8_0(const void* src, void* dst, int64_t num_blocks, void* stream);
+/* Embedding lookup over a GGUF table [vocab][hidden]: out[t] = the fp16
+ * dequantized row token_ids[t] (bit-exact as above), zeros for an id outside
+ * [0, vocab).  Replaces the reference's dequantize-the-whole-table-then-
+ * F.embedding (runtime/scheduler.py:22-35) by a gather of the needed rows.
+ * hidden % 64 == 0; token_ids: int64 on device; out: fp16[n_tokens][hidden].
+ * At most 65535 tokens per call.                                             */
+int gdsllm_embed_q4_0(const void* table, const int64_t* token_ids, int64_t n_tokens,
+                      int64_t vocab, int64_t hidden, void* out, void* stream);
+int gdsllm_embed_q8_0(const void* table, const int64_t* token_ids, int64_t n_tokens,
+                      int64_t vocab, int64_t hidden, void* out, void* stream);
 /* Replaces launch_dequant_affine_q4 (runtime/affine_q4_dequant.h:29-32,
  * runtime/affine_q4_dequant.cu:61-73).  Elements are grouped by flat index
  * (group = i / group_size) exactly as the reference does; `in_dim` is checked

@@ -54,7 +54,10 @@ int gdsllm_buffer_alloc(size_t size, int device_id, void** dev_ptr, size_t* roun
 int gdsllm_buffer_free(void* dev_ptr, int device_id);
 /* Read `size` bytes of `path` starting at `file_offset` into dev_ptr+buf_offset.
  * `buf_size` is the buffer's size, checked like gds_read (runtime/gds_io.cu:140-142).
- * *bytes_read receives the count copied (short only at end of file).        */
+ * *bytes_read receives the count copied (short only at end of file).
+ * Blocking: returns once the bytes are in HBM.  Four reader threads share the
+ * work in 8 MiB chunks through a per-device pinned staging pool (64 MiB, kept
+ * until the process ends); reads on one device run one at a time.         */
 int gdsllm_buffer_read_file(void* dev_ptr, size_t buf_size, const char* path,
                             size_t size, int64_t file_offset, int64_t buf_offset,
                             int device_id, int64_t* bytes_read);

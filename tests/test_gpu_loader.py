@@ -127,3 +127,21 @@ def test_region_loads_round_to_4k(gpu, tmp_path):
         want = np.frombuffer(f.read(5000), dtype=np.uint8)
     got = to_np(ext().view_tensor(h, [5000], "uint8", 0))
     assert np.array_equal(got, want)
+
+
+def test_multi_chunk_reads_and_short_read(gpu, tmp_path):
+    """Reads spanning many 8 MiB staging chunks (split over the reader
+    threads) at an unaligned offset, and the end-of-file count."""
+    path = str(tmp_path / "big.bin")
+    n = 5 * (8 << 20) + 12345
+    data = np.random.default_rng(18).integers(0, 256, n + 5000, dtype=np.uint8)
+    data.tofile(path)
+    h = ext().load_file_region(path, n, 4103)
+    assert np.array_equal(to_np(ext().view_tensor(h, [n], "uint8", 0)), data[4103:4103 + n])
+    whole = ext().load_file(path, n + 5000)
+    assert np.array_equal(to_np(ext().view_tensor(whole, [n + 5000], "uint8", 0)), data)
+    with pytest.raises(RuntimeError, match=f"expected {n + 5001} bytes, got {n + 5000}"):
+        ext().load_file(path, n + 5001)
+    t = ext().load_tensor(path, [3, 1000], "float16", (8 << 20) * 3 - 10)
+    want = data[(8 << 20) * 3 - 10:][:6000].view(np.float16).reshape(3, 1000)
+    assert np.array_equal(to_np(t).view(np.uint16), want.view(np.uint16))

@@ -153,6 +153,19 @@ def test_moe_gather_validation():
                                            None) == 1
 
 
+@pytest.mark.parametrize("name", ["gdsllm_embed_q4_0", "gdsllm_embed_q8_0"])
+def test_embed_validation(name):
+    fn = getattr(capi(), name)
+    assert fn(None, None, 0, 10, 64, None, None) == 0  # no tokens: nothing to do
+    assert fn(16, 16, -1, 10, 64, 16, None) == 1 and "negative" in _err()
+    assert fn(None, 16, 4, 10, 64, 16, None) == 1 and "null" in _err()
+    assert fn(16, 16, 4, 10, 96, 16, None) == 2 and "multiple of 64" in _err()
+    assert fn(16, 16, 65536, 10, 64, 16, None) == 1 and "65535" in _err()
+    assert fn(18, 16, 4, 10, 64, 16, None) == 1 and "aligned" in _err()
+    assert fn(16, 16, 4, 10, 64, 24, None) == 1 and "aligned" in _err()
+    assert fn(16, 12, 4, 10, 64, 16, None) == 1 and "aligned" in _err()
+
+
 def test_buffer_validation():
     lib = capi()
     assert lib.gdsllm_buffer_alloc(4096, 0, None, None) == 1

@@ -103,3 +103,24 @@ def test_affine_dequant_rounds_through_fp32(gpu):
     torch.cuda.synchronize()
     ref = oq.dequant_affine_q4(nib, scales, biases, 8 * n, 8)
     assert np.array_equal(_bits(to_np(out)), _bits(ref))
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("vocab,hidden,n", [(300, 64, 37), (97, 192, 5), (1000, 4096, 129), (3, 64, 1)])
+def test_embed_rows_bit_exact(gpu, fmt, vocab, hidden, n):
+    """Row gather of a GGUF table through the C ABI: each row is bit-identical
+    to that row of the whole-table dequant; ids outside [0, vocab) give zeros."""
+    make = syn.q4_0_weights if fmt == "q4_0" else syn.q8_0_weights
+    raw = make(vocab, hidden, gen(300 + vocab + hidden))
+    table = (oq.dequant_q4_0 if fmt == "q4_0" else oq.dequant_q8_0)(to_np(raw)).reshape(vocab, hidden)
+    ids = torch.randint(-2, vocab + 2, (n,), generator=gen(301 + n), dtype=torch.int64)
+    ids[0] = vocab - 1
+    src, ids_dev = on_gpu(raw, gpu), ids.to(gpu)
+    out = torch.full((n, hidden), float("nan"), dtype=torch.float16, device=gpu)
+    fn = capi().gdsllm_embed_q4_0 if fmt == "q4_0" else capi().gdsllm_embed_q8_0
+    check(fn(ptr(src), ptr(ids_dev), n, vocab, hidden, ptr(out), stream()))
+    torch.cuda.synchronize()
+    got = _bits(to_np(out))
+    for r, t in enumerate(ids.tolist()):
+        want = _bits(table[t]) if 0 <= t < vocab else np.zeros(hidden, np.uint16)
+        assert np.array_equal(got[r], want), f"{fmt} row {r} (token {t})"

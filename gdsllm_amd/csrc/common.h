@@ -110,6 +110,13 @@ struct NibUnpack {
         asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "s"(mask_hi), "v"(bits_hi));
         return r;
     }
+    // The same conversions written in C on the opaque registers (the compiler
+    // still forms one v_and_or_b32 each).  Required where the result feeds an
+    // MFMA directly: the compiler inserts the VALU-write -> MFMA-read wait
+    // states only after instructions it can see, so an MFMA operand written by
+    // the asm forms above may be read before the write has landed.
+    __device__ __forceinline__ uint32_t lo_c(uint32_t v) const { return (v & mask_lo) | bits_lo; }
+    __device__ __forceinline__ uint32_t hi_c(uint32_t v) const { return (v & mask_hi) | bits_hi; }
 };
 
 // v read from another lane of the same 16-lane DPP row (VALU data movement).
@@ -187,6 +194,27 @@ __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
     asm volatile("" ::: "memory");
+}
+
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// One LDS-DMA transfer of 16 (4) bytes per lane from base + voff[lane] to
+// lds + 16l (4l); base and lds are wave-uniform (lds goes to M0).  Written as
+// inline asm, the transfers are invisible to the compiler's counters: it
+// neither waits for them before its own LDS accesses nor counts them, so a
+// kernel using them waits with wait_vmcnt_asm and keeps every other vector
+// memory operation out of the windows it counts.
+__device__ __forceinline__ void dma16_asm(uint32_t voff, const void* base, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds) : "m0");
+}
+__device__ __forceinline__ void dma4_asm(uint32_t voff, const void* base, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "s"(lds) : "m0");
+}
+#pragma clang diagnostic pop
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_asm() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
 // LDS accesses written as instructions the compiler does not analyse.  The

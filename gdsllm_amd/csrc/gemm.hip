@@ -264,24 +264,6 @@ static_assert(kWSlot / 1024 == 3 * (kWaves - 2), "waves 0-5 move a super-block i
 
 typedef float float16_t __attribute__((ext_vector_type(16)));
 
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-// One LDS-DMA transfer of 16 (4) bytes per lane from base + voff[lane] to
-// lds + 16l (4l); base and lds are wave-uniform.  Invisible to the compiler's
-// counters.
-__device__ __forceinline__ void dma16_asm(uint32_t voff, const void* base, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds) : "m0");
-}
-__device__ __forceinline__ void dma4_asm(uint32_t voff, const void* base, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "s"(lds) : "m0");
-}
-#pragma clang diagnostic pop
-template <int N>
-__device__ __forceinline__ void wait_vmcnt_asm() {
-    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
 __global__ __launch_bounds__(sk::kWaves * 64) void dequant_gemm_q4_0_sk(const uint8_t* __restrict__ W,
                                                                       const uint16_t* __restrict__ X,
                                                                       uint16_t* __restrict__ Y, int M, int K, int T,
@@ -392,8 +374,8 @@ __global__ __launch_bounds__(sk::kWaves * 64) void dequant_gemm_q4_0_sk(const ui
             u32x4_t lo, hi;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                lo[e] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(half2_t, nib.lo(t[e])) + off_lo) * dd);
-                hi[e] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(half2_t, nib.hi(t[e])) + off_hi) * dd);
+                lo[e] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(half2_t, nib.lo_c(t[e])) + off_lo) * dd);
+                hi[e] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(half2_t, nib.hi_c(t[e])) + off_hi) * dd);
             }
             o.wb[0][fr] = __builtin_bit_cast(half8_t, lo);
             o.wb[1][fr] = __builtin_bit_cast(half8_t, hi);

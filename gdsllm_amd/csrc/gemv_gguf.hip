@@ -872,10 +872,10 @@ __device__ __forceinline__ half8_t weight_a_operand(const PairWords<F>& p, const
         const half2_t lo_off = {static_cast<half_t>(-1032.0f), static_cast<half_t>(-1032.0f)};
         const half2_t hi_off = {static_cast<half_t>(-72.0f), static_cast<half_t>(-72.0f)};
         const uint32_t qs = q >> 8;
-        h[0] = __builtin_bit_cast(half2_t, nu.lo(q)) + lo_off;
-        h[1] = __builtin_bit_cast(half2_t, nu.hi(q)) + hi_off;
-        h[2] = __builtin_bit_cast(half2_t, nu.lo(qs)) + lo_off;
-        h[3] = __builtin_bit_cast(half2_t, nu.hi(qs)) + hi_off;
+        h[0] = __builtin_bit_cast(half2_t, nu.lo_c(q)) + lo_off;
+        h[1] = __builtin_bit_cast(half2_t, nu.hi_c(q)) + hi_off;
+        h[2] = __builtin_bit_cast(half2_t, nu.lo_c(qs)) + lo_off;
+        h[3] = __builtin_bit_cast(half2_t, nu.hi_c(qs)) + hi_off;
     } else {
         uint32_t q0, q1;
         if constexpr (ODD == 0) {
@@ -1083,6 +1083,246 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void gguf_gemv_mfma(const uint8_t*
         if (q + 2 < Q) compute(I2{});
 }
 
+// ---- Q4_0 batched GEMV, batch 3..8: raw codes on the matrix cores ------------
+// The weights enter v_mfma_f32_16x16x32_f16 as their exponent-trick codes, not
+// dequantized: 1024 + q for low nibbles, 64 + q for high nibbles, one
+// v_and_or_b32 per pair of weights.  Per block b and batch row t the MFMA then
+// yields S = sum_k x_k * code_k, and
+//     sum_k x_k * (q_k - 8) = S - c,   c = 1032 * sum_lo x + 72 * sum_hi x,
+// exactly as in the batch-1 path; the block's scale multiplies (S - c) in
+// fp32 afterwards (v_fma_mix, one per output).  c itself comes from one more
+// MFMA per block pair, x times a constant operand (-1032 / -72), and enters
+// the weight MFMAs as their C input, so no VALU work computes it.
+//
+// Operands: A = x, 16 slots = batch rows 0-7 of block 2p (slots 0-7) and of
+// block 2p+1 (slots 8-15); B = weights, 16 columns = rows 0-7 of a row group
+// with block 2p (columns 0-7) and block 2p+1 (columns 8-15).  Lane group g
+// (lanes 16g..16g+15) holds k-group g of every operand: elements 4g..4g+3
+// (low nibbles of qs dword g) and 16+4g..19+4g (its high nibbles), so x is read
+// from LDS in its natural order (two 8-byte reads) and only the outputs whose
+// slot and column take the same block are valid: lanes 0-7 and 16-23 (block
+// 2p, batch rows 4g+v) and lanes 40-47 and 56-63 (block 2p+1).  Each lane
+// holds one column, i.e. one (row, block), so it applies a single scale.
+//
+// Work split: a workgroup of 8 waves owns a tile of RT rows (32 or 16) at a
+// time; wave w takes super-blocks w, w+8, ... of K.  A stage is the tile's rows
+// x one super-block (RT*144 bytes of weights) plus x of its 256 columns for 8
+// batch rows (4 KiB), moved by LDS DMA; every wave keeps two stages in flight.
+// At the end of a tile the waves' partial sums meet in LDS and are added in
+// wave order, so results do not depend on timing.
+namespace bq {
+constexpr int kWaves = 8;
+constexpr int kXStride = 1088;                  // LDS bytes per x transfer (2 batch rows + bank padding)
+constexpr int kXBytes = 4 * kXStride;
+template <int RT>
+constexpr int w_dma() { return (RT * 9 + 63) / 64; }  // weight transfers per stage: 5 (RT 32), 3 (RT 16)
+template <int RT>
+constexpr int w_last_lanes() { return RT * 9 - 64 * (w_dma<RT>() - 1); }
+template <int RT>
+constexpr int slot_bytes() { return RT * 144 + kXBytes; }
+template <int RT>
+constexpr int red_bytes() { return kWaves * 8 * RT * 4; }
+template <int RT>
+constexpr int lds_bytes() { return kWaves * 2 * slot_bytes<RT>() + 2 * red_bytes<RT>(); }
+}  // namespace bq
+
+template <int RT>
+__global__ __launch_bounds__(bq::kWaves * 64) void gguf_gemv_q4_codes(const uint8_t* __restrict__ W,
+                                                                     const uint16_t* __restrict__ X,
+                                                                     uint16_t* __restrict__ Y, int M, int K, int nb,
+                                                                     int64_t ldx, int64_t ldy) {
+    constexpr int NRG = RT / 8;        // row groups of 8 per stage
+    constexpr int NWD = bq::w_dma<RT>();
+    constexpr int kOps = NWD + 4;      // transfers per stage
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int S = K >> 8;
+    const uint32_t row_bytes = static_cast<uint32_t>(S) * 144u;
+    const int ntiles = (M + RT - 1) / RT;
+    const int T = (ntiles - static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) - 1) / static_cast<int>(gridDim.x);
+    const int nst = S > wave ? (S - 1 - wave) / bq::kWaves + 1 : 0;  // stages of this wave per tile
+    const int Q = T * nst;
+    const uint32_t lds0 = lds_addr(lds);
+    const uint32_t slot0 = lds0 + wave * 2 * bq::slot_bytes<RT>();
+    float* red0 = reinterpret_cast<float*>(lds + bq::kWaves * 2 * bq::slot_bytes<RT>());
+
+    // transfer offsets.  x transfer j: batch rows 2j + (lane >> 5) (rows past
+    // nb read row nb - 1), 16-byte chunk lane & 31 of the stage's 256 columns.
+    uint32_t xoff[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int t = min(2 * j + (lane >> 5), nb - 1);
+        xoff[j] = static_cast<uint32_t>(2 * (t * ldx + 8 * (lane & 31)));
+    }
+    // weight transfer j: chunk c = 64j + lane = row c / 9, chunk c % 9 of the
+    // row's super-block (rows past the tile's last valid row read that row)
+    auto w_offsets = [&](int nrows, uint32_t (&off)[NWD]) {
+#pragma unroll
+        for (int j = 0; j < NWD; ++j) {
+            const int c = min(64 * j + lane, RT * 9 - 1);
+            const int r = c / 9;
+            off[j] = static_cast<uint32_t>(min(r, nrows - 1)) * row_bytes + 16u * static_cast<uint32_t>(c - 9 * r);
+        }
+    };
+    uint32_t woff_full[NWD];
+    w_offsets(RT, woff_full);
+
+    // next stage to issue: tile ii of this workgroup, step ss of this wave
+    int ii = 0, ss = 0;
+    auto issue = [&](int q) {
+        const uint32_t slot = slot0 + (q & 1) * bq::slot_bytes<RT>();
+        const int sb = wave + bq::kWaves * ss;
+        const int row0 = RT * (static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) * ii);
+        const uint16_t* xb = X + 256 * sb;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dma16_asm(xoff[j], xb, slot + RT * 144 + bq::kXStride * j);
+        const uint8_t* wb = W + static_cast<int64_t>(row0) * row_bytes + 144 * sb;
+        uint32_t woff[NWD];
+        const int nrows = min(RT, M - row0);
+        if (nrows == RT) {
+#pragma unroll
+            for (int j = 0; j < NWD; ++j) woff[j] = woff_full[j];
+        } else {
+            w_offsets(nrows, woff);
+        }
+#pragma unroll
+        for (int j = 0; j < NWD - 1; ++j) dma16_asm(woff[j], wb, slot + 1024 * j);
+        if (lane < bq::w_last_lanes<RT>()) dma16_asm(woff[NWD - 1], wb, slot + 1024 * (NWD - 1));
+        if (++ss == nst) {
+            ss = 0;
+            ++ii;
+        }
+    };
+
+    // per-lane operand geometry
+    const int g = lane >> 4, j = lane & 15, par = j >> 3;
+    // x: batch row j & 7 of block 2p + par, elements 4g.. and 16+4g.. (bytes +32)
+    const uint32_t xrd = (j & 7) / 2 * bq::kXStride + (j & 1) * 512 + 64 * par + 8 * g;
+    // weights: row 8rg + (j & 7), block 2p + par; qs dword g starts at byte
+    // 144r + 18(2p + par) + 2 + 4g, which is 2 mod 4 for the even block
+    const uint32_t wrd = 144 * (j & 7) + (par ? 20 : 0) + 4 * g;
+    const uint32_t drd = 144 * (j & 7) + 18 * par;
+    const uint32_t sel01 = par ? 0x0C010C00u : 0x0C030C02u;
+    const uint32_t sel23 = par ? 0x0C030C02u : 0x0C050C04u;
+    const NibUnpack nu;
+    const half8_t kneg = {static_cast<half_t>(-1032.0f), static_cast<half_t>(-1032.0f), static_cast<half_t>(-1032.0f),
+                          static_cast<half_t>(-1032.0f), static_cast<half_t>(-72.0f),   static_cast<half_t>(-72.0f),
+                          static_cast<half_t>(-72.0f),   static_cast<half_t>(-72.0f)};
+
+    float4_t acc[NRG];
+#pragma unroll
+    for (int r = 0; r < NRG; ++r) acc[r] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](int q) {
+        const uint8_t* slot = lds + (slot0 - lds0) + (q & 1) * bq::slot_bytes<RT>();
+        const uint8_t* xs = slot + RT * 144 + xrd;
+        half8_t xa[4];
+        float4_t dc[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const uint2 lo = *reinterpret_cast<const uint2*>(xs + 128 * p);
+            const uint2 hi = *reinterpret_cast<const uint2*>(xs + 128 * p + 32);
+            xa[p] = __builtin_bit_cast(half8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+            dc[p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[p], kneg, float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        }
+#pragma unroll
+        for (int rg = 0; rg < NRG; ++rg)
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const uint8_t* wr = slot + 1152 * rg + 36 * p;
+                const uint32_t d0 = *reinterpret_cast<const uint32_t*>(wr + wrd);
+                const uint32_t d1 = *reinterpret_cast<const uint32_t*>(wr + wrd + 4);
+                const half_t dv = __builtin_bit_cast(half_t, *reinterpret_cast<const uint16_t*>(wr + drd));
+                const uint32_t p01 = __builtin_amdgcn_perm(d1, d0, sel01);
+                const uint32_t p23 = __builtin_amdgcn_perm(d1, d0, sel23);
+                const half8_t wb =
+                    __builtin_bit_cast(half8_t, make_uint4(nu.lo_c(p01), nu.lo_c(p23), nu.hi_c(p01), nu.hi_c(p23)));
+                const float4_t D = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[p], wb, dc[p], 0, 0, 0);
+                const float dsc = static_cast<float>(dv);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[rg][v] = __builtin_fmaf(dsc, D[v], acc[rg][v]);
+            }
+    };
+
+    // End of tile ck: lanes 0-7 / 16-23 add the block-2p+1 partials of lanes
+    // +40, write batch rows 4g+v of row 8rg + j to LDS; after the barrier each
+    // of the first 8*RT threads sums one (batch row, row) over the waves.
+    int ck = 0;
+    auto finish_tile = [&]() {
+        float* red = red0 + (ck & 1) * (bq::red_bytes<RT>() / 4);
+        const int src = lane + 40 < 64 ? lane + 40 : lane;
+#pragma unroll
+        for (int rg = 0; rg < NRG; ++rg) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float o = __shfl(acc[rg][v], src, 64);
+                if (g < 2 && j < 8) red[(wave * 8 + 4 * g + v) * RT + 8 * rg + j] = acc[rg][v] + o;
+            }
+            acc[rg] = float4_t{0.f, 0.f, 0.f, 0.f};
+        }
+        lds_barrier();
+        const int i = threadIdx.x;
+        const int row0 = RT * (static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) * ck);
+        if (i < 8 * RT) {
+            const int t = i / RT, r = i - t * RT;
+            float sum = 0.f;
+#pragma unroll
+            for (int w = 0; w < bq::kWaves; ++w) sum += red[(w * 8 + t) * RT + r];
+            if (t < nb && row0 + r < M) Y[t * ldy + row0 + r] = f2h_bits(sum);
+        }
+        ++ck;
+    };
+
+    if (nst == 0) {
+        // K has fewer super-blocks than the workgroup has waves: this wave
+        // adds zero partials to every tile's sum
+        for (int k = 0; k < T; ++k) finish_tile();
+        return;
+    }
+    issue(0);
+    if (Q > 1) issue(1);
+    int cs = 0;  // step of the stage being computed within its tile
+    for (int q = 0; q < Q; ++q) {
+        if (q + 1 < Q)
+            wait_vmcnt_asm<kOps>();  // stage q has landed (stage q+1 may be in flight)
+        else
+            wait_vmcnt_asm<0>();
+        compute(q);
+        // every LDS read of this slot has returned before the DMA refills it
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (q + 2 < Q) issue(q + 2);
+        if (++cs == nst) {
+            cs = 0;
+            finish_tile();
+        }
+    }
+}
+
+template <int RT>
+int launch_q4_codes(const void* w, const uint16_t* x, uint16_t* y, int M, int K, int64_t batch, int64_t ldx,
+                    int64_t ldy, hipStream_t stream) {
+    constexpr size_t lds = bq::lds_bytes<RT>();
+    const void* fn = reinterpret_cast<const void*>(&gguf_gemv_q4_codes<RT>);
+    if (int rc = prepare_lds(fn, lds)) return rc;
+    const int tiles = (M + RT - 1) / RT;
+    const int resident = blocks_per_cu(fn, lds, bq::kWaves * 64) * cu_count();
+    const int grid = std::min(tiles, resident);
+    hipLaunchKernelGGL((gguf_gemv_q4_codes<RT>), dim3(grid), dim3(bq::kWaves * 64), lds, stream,
+                       static_cast<const uint8_t*>(w), x, y, M, K, static_cast<int>(batch), ldx, ldy);
+    return check_hip(hipGetLastError(), "gguf_gemv_q4_codes launch");
+}
+
+// Row-tile height for the code kernel: the one whose slowest workgroup has
+// the fewest rows to stream (ties go to 32-row tiles, which move less x per
+// weight byte).
+inline int q4_codes_rows(int M) {
+    const int cus = cu_count();
+    const int r32 = (M + 31) / 32, r16 = (M + 15) / 16;
+    const int64_t cost32 = static_cast<int64_t>((r32 + cus - 1) / cus) * 32;
+    const int64_t cost16 = static_cast<int64_t>((r16 + cus - 1) / cus) * 16;
+    return cost16 < cost32 ? 16 : 32;
+}
+
 // Any in_dim % 32 == 0 and any alignment: one wave per row, one lane per block,
 // byte loads, the reference's per-element order of operations.
 template <Fmt F>
@@ -1266,6 +1506,11 @@ int gemv(const char* name, const void* w, const void* x, void* y, int64_t out_di
     if (rc != -1) return rc == GDSLLM_OK ? ok() : rc;
     rc = GDSLLM_OK;
     const bool x_al16 = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (ldx % 8 == 0);
+    if (F == Fmt::Q4_0 && fast && batch >= 3 && K <= (1 << 20) && x_al16) {
+        const int rc2 = q4_codes_rows(M) == 32 ? launch_q4_codes<32>(w, xp, yp, M, K, batch, ldx, ldy, s)
+                                               : launch_q4_codes<16>(w, xp, yp, M, K, batch, ldx, ldy, s);
+        return rc2 == GDSLLM_OK ? ok() : rc2;
+    }
     if (fast && batch >= 3 && K <= (1 << 20) && x_al16) {
         // Q4_0: two row tiles per workgroup while that still gives every CU
         // one; Q8_0 stages are twice as large and take one tile

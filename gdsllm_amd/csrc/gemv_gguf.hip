@@ -1312,16 +1312,13 @@ int launch_q4_codes(const void* w, const uint16_t* x, uint16_t* y, int M, int K,
     return check_hip(hipGetLastError(), "gguf_gemv_q4_codes launch");
 }
 
-// Row-tile height for the code kernel: the one whose slowest workgroup has
-// the fewest rows to stream (ties go to 32-row tiles, which move less x per
-// weight byte).
-inline int q4_codes_rows(int M) {
-    const int cus = cu_count();
-    const int r32 = (M + 31) / 32, r16 = (M + 15) / 16;
-    const int64_t cost32 = static_cast<int64_t>((r32 + cus - 1) / cus) * 32;
-    const int64_t cost16 = static_cast<int64_t>((r16 + cus - 1) / cus) * 16;
-    return cost16 < cost32 ? 16 : 32;
-}
+// Row-tile height for the code kernel.  A 16-row stage moves 1.8 bytes of x
+// per weight byte (a 32-row one 0.9), which costs more than the uneven last
+// round of 32-row tiles (measured on MI355X: 28672x8192 at batch 8 40.8 us
+// with 32-row tiles, 47.1 us with 16; 8192x8192 13.3 vs 15.8 us), so 16-row
+// tiles serve only matrices too short to give half the CUs a 32-row tile
+// (1024x8192: 8.7 us against 11.6).
+inline int q4_codes_rows(int M) { return (M + 31) / 32 >= cu_count() / 2 ? 32 : 16; }
 
 // Any in_dim % 32 == 0 and any alignment: one wave per row, one lane per block,
 // byte loads, the reference's per-element order of operations.

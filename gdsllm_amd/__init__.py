@@ -42,6 +42,8 @@ SIGNATURES = {
     "gdsllm_dequant_q8_0": (ctypes.c_int, [_c_vp, _c_vp, _c_i64, _c_vp]),
     "gdsllm_embed_q4_0": (ctypes.c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp]),
     "gdsllm_embed_q8_0": (ctypes.c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp]),
+    "gdsllm_dequant_int8": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
+    "gdsllm_fused_int8_gemv": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp]),
     "gdsllm_dequant_affine_q4": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp]),
     "gdsllm_fused_q4_0_gemv": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp]),
     "gdsllm_fused_q8_0_gemv": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp]),

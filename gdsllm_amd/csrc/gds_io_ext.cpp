@@ -480,6 +480,65 @@ torch::Tensor gemv_f16(torch::Tensor weight, torch::Tensor x) {
     return out;
 }
 
+// ---- per-column int8 weights (runtime/llama.py:162-165) -------------------------
+
+void check_int8_weights(const torch::Tensor& w, const torch::Tensor& scale, const char* where) {
+    if (!w.is_cuda() || w.scalar_type() != torch::kInt8 || w.dim() != 2)
+        throw std::runtime_error(std::string(where) + ": weight must be a 2-D int8 CUDA tensor");
+    check_fp16_cuda(scale, "scale", where);
+    if (scale.numel() != w.size(1))
+        throw std::runtime_error(std::string(where) + ": scale must hold one value per input column (" +
+                                 std::to_string(w.size(1)) + ")");
+    if (scale.get_device() != w.get_device())
+        throw std::runtime_error(std::string(where) + ": weight and scale must be on the same device");
+}
+
+// (w.float() * scale).half(), bit-exact, into `output` when given.
+torch::Tensor dequant_int8(torch::Tensor weight, torch::Tensor scale, c10::optional<torch::Tensor> output) {
+    const char* where = "dequant_int8";
+    check_int8_weights(weight, scale, where);
+    torch::Tensor w = weight.contiguous(), s = scale.contiguous();
+    torch::Tensor out;
+    if (output.has_value() && output->defined()) {
+        out = *output;
+        check_fp16_cuda(out, "output", where);
+        if (out.numel() < w.numel() || !out.is_contiguous())
+            throw std::runtime_error(std::string(where) + ": output must be a contiguous fp16 tensor of " +
+                                     std::to_string(w.numel()) + " elements");
+        out = out.view(-1).narrow(0, 0, w.numel()).view(w.sizes());
+    } else {
+        out = torch::empty(w.sizes(), s.options());
+    }
+    check(gdsllm_dequant_int8(w.data_ptr(), s.data_ptr(), out.data_ptr(), w.size(0), w.size(1),
+                              stream_of(w.get_device())),
+          where);
+    return out;
+}
+
+// F.linear(x, (w.float() * scale).half()) for x [..., in_dim] fp16: the fused
+// GEMV for up to 8 rows of x, else the bit-exact dequant and one GEMM.
+torch::Tensor int8_linear(torch::Tensor weight, torch::Tensor scale, torch::Tensor x) {
+    const char* where = "int8_linear";
+    check_int8_weights(weight, scale, where);
+    check_fp16_cuda(x, "x", where);
+    if (x.get_device() != weight.get_device())
+        throw std::runtime_error(std::string(where) + ": x must be on the weight's device");
+    torch::Tensor w = weight.contiguous(), s = scale.contiguous(), xf = x.contiguous();
+    const int64_t out_dim = w.size(0), in_dim = w.size(1);
+    if (xf.size(-1) != in_dim)
+        throw std::runtime_error(std::string(where) + ": last dim of x must equal in_dim " + std::to_string(in_dim));
+    const int64_t rows = in_dim ? xf.numel() / in_dim : 0;
+    auto out_shape = xf.sizes().vec();
+    out_shape.back() = out_dim;
+    if (rows > 8) return at::linear(xf, dequant_int8(w, s, c10::nullopt)).view(out_shape);
+    torch::Tensor out = torch::empty(out_shape, xf.options());
+    if (rows == 0) return out;
+    check(gdsllm_fused_int8_gemv(w.data_ptr(), s.data_ptr(), xf.data_ptr(), out.data_ptr(), out_dim, in_dim, rows,
+                                 in_dim, out_dim, stream_of(w.get_device())),
+          where);
+    return out;
+}
+
 py::tuple moe_route_topk(torch::Tensor logits, int64_t top_k) {
     const char* where = "moe_route_topk";
     check_fp16_cuda(logits, "logits", where);
@@ -568,6 +627,10 @@ PYBIND11_MODULE(gds_io_ext, m) {
           py::arg("handle"), py::arg("x"), py::arg("weight_shape"), py::arg("gguf_type"), py::arg("offset"));
     m.def("gemv_f16", &gemv_f16, "fp16-weight GEMV (router, shared-expert gate): x [..., K] -> [..., M].",
           py::arg("weight"), py::arg("x"));
+    m.def("dequant_int8", &dequant_int8, "(w.float() * scale).half() of per-column int8 weights, bit-exact.",
+          py::arg("weight"), py::arg("scale"), py::arg("output") = py::none());
+    m.def("int8_linear", &int8_linear, "F.linear(x, (w.float() * scale).half()) without the fp32 round trip.",
+          py::arg("weight"), py::arg("scale"), py::arg("x"));
     m.def("moe_route_topk", &moe_route_topk, "Top-k experts and fp16(softmax_fp32) weights from fp16 logits.",
           py::arg("logits"), py::arg("top_k"));
     m.def("moe_combine", &moe_combine, "clamp(expert_out + sigmoid(gate) * shared_out) with torch fp16 semantics.",

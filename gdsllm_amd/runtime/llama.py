@@ -7,7 +7,10 @@ arguments and weight-metadata dicts ({"buffer", "shape", "gguf_type",
 the same contract:
   * decode with batch > 1 (x [B, 1, K], B <= 8) runs one batched fused GEMV
     instead of failing the reference's x.view(-1) size check;
-  * Q4_0 prefill runs the fused MFMA dequant-GEMM instead of dequant + GEMM.
+  * Q4_0 prefill runs the fused MFMA dequant-GEMM instead of dequant + GEMM;
+  * per-column int8 weights (runtime/llama.py:162-165) go through
+    gds_io_ext.int8_linear: a fused GEMV at decode, a bit-exact dequant and one
+    GEMM at prefill, instead of an fp32 copy of the whole matrix per call.
 Q8_0 prefill keeps the reference's dequant -> F.linear route.
 """
 
@@ -55,6 +58,7 @@ def dequant_linear(
             return _fused_dequant_gemm(x, w)
         w = _dequant_gguf(w, scratch)
     elif w.dtype == torch.int8:
-        scale = weights[f"{name}.scale"]
-        w = (w.float() * scale).half()
+        # per-column int8: fused GEMV for up to 8 rows of x, else the bit-exact
+        # dequant and one GEMM (no fp32 copy of the matrix)
+        return ext().int8_linear(w, weights[f"{name}.scale"], x)
     return F.linear(x, w)

@@ -9,7 +9,8 @@ changes, both on the fast side of the same contract:
     would give (gds_io_ext.embed_gguf);
   * a GGUF lm_head goes through dequant_linear, i.e. the fused dequant+GEMV
     at decode and the MFMA dequant-GEMM for Q4_0 prefill, instead of dequant
-    into a temporary plus F.linear.
+    into a temporary plus F.linear; an int8 lm_head goes through
+    gds_io_ext.int8_linear instead of an fp32 copy of the matrix.
 """
 
 from __future__ import annotations
@@ -42,10 +43,5 @@ def _lm_head_proj(h: torch.Tensor, tensors: dict, key: str = "lm_head.weight",
     if isinstance(w, dict) and "gguf_type" in w:
         return dequant_linear(h, {key: w}, key[: -len(".weight")], scratch)
     if w.dtype == torch.int8:
-        scale = tensors[key[: -len(".weight")] + ".scale"]
-        if w.shape[0] * w.shape[1] * 4 > 512 * 1024 * 1024:  # bounded fp32 temporaries
-            step = 16384
-            return torch.cat([F.linear(h, (w[i:i + step].float() * scale).half()) for i in range(0, w.shape[0], step)],
-                             dim=-1)
-        w = (w.float() * scale).half()
+        return ext().int8_linear(w, tensors[key[: -len(".weight")] + ".scale"], h)
     return F.linear(h, w)

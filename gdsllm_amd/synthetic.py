@@ -7,7 +7,8 @@ torch.Generator, on whatever device the generator lives on, so a CPU copy and
 a GPU copy made from equal seeds hold identical bytes.
 
 Distributions follow the benchmark configurations: Q4_0 d ~ U(0.005, 0.02) and
-uniform nibbles; Q8_0 d ~ U(0.001, 0.004) and q ~ U[-127, 127]; affine
+uniform nibbles; Q8_0 d ~ U(0.001, 0.004) and q ~ U[-127, 127]; per-column
+int8 scale ~ U(0.001, 0.004) and q ~ U[-128, 127]; affine
 scale ~ U(0.005, 0.02), bias ~ N(0, 0.05), uniform nibbles; x ~ N(0, 1) fp16.
 """
 
@@ -48,6 +49,13 @@ def q8_0_weights(rows: int, cols: int, gen: torch.Generator, d_range=(0.001, 0.0
     out[:, :2] = d.view(torch.uint8).view(nblk, 2)
     out[:, 2:] = qs.view(torch.uint8)
     return out.view(rows, cols // 32 * 34)
+
+
+def int8_weights(rows: int, cols: int, gen: torch.Generator, s_range=(0.001, 0.004)):
+    """(q int8 [rows, cols], scale fp16 [1, cols]): the per-column int8 format
+    of tools/convert_weights.py:55-83 with q ~ U[-128, 127] and scale ~ U(s_range)."""
+    q = torch.randint(-128, 128, (rows, cols), dtype=torch.int8, device=_dev(gen), generator=gen)
+    return q, _fp16_uniform(cols, *s_range, gen).view(1, cols)
 
 
 def affine_q4_weights(shape, group_size: int, gen: torch.Generator):

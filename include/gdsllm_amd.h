@@ -105,6 +105,24 @@ int gdsllm_fused_q4_0_gemv(const void* weight, const void* x, void* y,
 int gdsllm_fused_q8_0_gemv(const void* weight, const void* x, void* y,
                            int64_t out_dim, int64_t in_dim, int64_t batch,
                            int64_t ldx, int64_t ldy, void* stream);
+/* ------------------------------------------------- per-column int8 weights --
+ * The converter's "int8" format (tools/convert_weights.py:55-83): W int8
+ * [out_dim][in_dim] row-major, scale fp16 [in_dim] (one per input column).
+ * Replace the projection runtime/llama.py:162-165 computes from it,
+ * w = (w.float() * scale).half(); F.linear(x, w), which dequantizes the whole
+ * matrix through fp32 on every call.                                         */
+
+/* dst fp16[rows][cols] = RN16(w * scale[col]): bit-exact with the reference's
+ * (w.float() * scale).half().                                                */
+int gdsllm_dequant_int8(const void* weight, const void* scale, void* dst, int64_t rows, int64_t cols,
+                        void* stream);
+/* y[b][r] = sum_k RN16(w[r][k] * scale[k]) * x[b][k] with fp32 accumulation,
+ * batch 1..8, x rows ldx apart, y rows ldy apart.  The fast path needs
+ * in_dim % 16 == 0, 16-byte aligned weight, scale and x (ldx % 8 == 0 when
+ * batch > 1); other shapes run a slower kernel with the same results.        */
+int gdsllm_fused_int8_gemv(const void* weight, const void* scale, const void* x, void* y, int64_t out_dim,
+                           int64_t in_dim, int64_t batch, int64_t ldx, int64_t ldy, void* stream);
+
 /* ----------------------------------------------------- decode-step fusions --
  * No counterpart in the reference, which issues one dequant_linear per
  * projection: q/k/v of one layer read the same x (runtime/llama.py:212-214),

@@ -58,6 +58,26 @@ def dequant_q8_0(raw) -> np.ndarray:
     return (d * qs).astype(np.float16).reshape(-1)
 
 
+def dequant_int8(w_int8, scale_fp16) -> np.ndarray:
+    """Per-column int8 weights as runtime/llama.py:162-165 dequantizes them:
+    (w.float() * scale).half(), scale [1, in_dim] broadcast over the rows
+    (layout from tools/convert_weights.py:55-83).  An int8 times an fp16 value
+    is exact in fp32, so this is one RNE rounding of q * s."""
+    q = np.asarray(w_int8, dtype=np.int8).astype(np.float32)
+    s = np.asarray(scale_fp16, dtype=np.float16).reshape(1, -1).astype(np.float32)
+    return (q * s).astype(np.float16)
+
+
+def quantize_int8(w_fp16) -> tuple[np.ndarray, np.ndarray]:
+    """quantize_tensor_int8 of tools/convert_weights.py:55-83 for a 2-D tensor:
+    scale = max_r |W[r, c]| / 127 per column (at least 1e-10),
+    q = clip(round(W / scale), -128, 127); returns (q int8, scale fp16 [1, cols])."""
+    w = np.asarray(w_fp16, dtype=np.float16).astype(np.float32)
+    scale = np.maximum(np.abs(w).max(axis=0, keepdims=True) / 127.0, 1e-10)
+    q = np.clip(np.round(w / scale), -128, 127).astype(np.int8)
+    return q, scale.astype(np.float16)
+
+
 def unpack_affine_nibbles(words: np.ndarray) -> np.ndarray:
     """uint32 words -> nibbles, element 8w+n = (word >> 4n) & 15 (LSB first;
     runtime/affine_q4_dequant.cu:50-58, tools/convert_qwen_moe.py:170-179)."""

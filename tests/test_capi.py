@@ -166,6 +166,23 @@ def test_embed_validation(name):
     assert fn(16, 12, 4, 10, 64, 16, None) == 1 and "aligned" in _err()
 
 
+def test_int8_validation():
+    lib = capi()
+    g = lib.gdsllm_fused_int8_gemv
+    assert g(16, 16, 16, 16, 4, 64, 0, 64, 4, None) == 1 and "batch" in _err()
+    assert g(16, 16, 16, 16, 4, 64, 9, 64, 4, None) == 1
+    assert g(16, 16, 16, 16, -1, 64, 1, 64, 4, None) == 1 and "negative" in _err()
+    assert g(None, 16, 16, 16, 4, 64, 1, 64, 4, None) == 1 and "null" in _err()
+    assert g(16, 16, 16, 16, 4, 64, 2, 32, 4, None) == 1 and "ldx" in _err()
+    assert g(16, 16, 17, 16, 4, 64, 1, 64, 4, None) == 1 and "aligned" in _err()
+    assert g(None, None, None, None, 0, 64, 1, 64, 0, None) == 0  # empty problems are no-ops
+    d = lib.gdsllm_dequant_int8
+    assert d(16, 16, 16, -1, 4, None) == 1 and "negative" in _err()
+    assert d(None, 16, 16, 2, 4, None) == 1 and "null" in _err()
+    assert d(16, 17, 16, 2, 4, None) == 1 and "aligned" in _err()
+    assert d(None, None, None, 0, 4, None) == 0
+
+
 def test_buffer_validation():
     lib = capi()
     assert lib.gdsllm_buffer_alloc(4096, 0, None, None) == 1
@@ -199,6 +216,10 @@ def test_extension_module_surface():
                               "output"],
         "fused_affine_q4_gemv": ["handle", "x", "weight_shape", "weight_offset", "scale_offset", "bias_offset",
                                  "group_size"],
+        # extensions of this build
+        "embed_gguf": ["handle", "token_ids", "shape", "gguf_type", "offset"],
+        "dequant_int8": ["weight", "scale", "output"],
+        "int8_linear": ["weight", "scale", "x"],
     }
     for name, args in expected.items():
         fn = getattr(m, name)

@@ -88,7 +88,8 @@ def test_gguf_gemv_strided_batch(gpu, B):
     xw[:, :K] = x
     xd = xw.to(gpu)
     y = torch.full((B, M + 10), 7.0, dtype=torch.float16, device=gpu)
-    check(capi().gdsllm_fused_q4_0_gemv(ptr(w.to(gpu)), ptr(xd), ptr(y), M, K, B, K + 64, M + 10, stream()))
+    wd = w.to(gpu)  # held across the call: a freed copy could be reused before the kernel reads it
+    check(capi().gdsllm_fused_q4_0_gemv(ptr(wd), ptr(xd), ptr(y), M, K, B, K + 64, M + 10, stream()))
     torch.cuda.synchronize()
     yn = to_np(y)
     assert np.all(yn[:, M:] == 7.0), "wrote outside the output rows"

@@ -142,7 +142,8 @@ def test_dequant_gemm_q4_0(gpu, T, M, K):
     deq = oq.dequant_q4_0(to_np(w)).reshape(M, K)
     xd = x.to(gpu)
     y = torch.empty(T, M, dtype=torch.float16, device=gpu)
-    check(capi().gdsllm_dequant_gemm_q4_0(ptr(w.to(gpu)), ptr(xd), ptr(y), M, K, T, K, M, stream()))
+    wd = w.to(gpu)  # held across the call: a freed copy could be reused before the kernel reads it
+    check(capi().gdsllm_dequant_gemm_q4_0(ptr(wd), ptr(xd), ptr(y), M, K, T, K, M, stream()))
     torch.cuda.synchronize()
     assert_gemv_close(to_np(y), deq, to_np(x), f"gemm T{T} {M}x{K}")
 
@@ -156,7 +157,8 @@ def test_dequant_gemm_strided(gpu):
     deq = oq.dequant_q4_0(to_np(w)).reshape(M, K)
     xd = xfull.to(gpu)
     y = torch.full((T, ldy), 7.0, dtype=torch.float16, device=gpu)
-    check(capi().gdsllm_dequant_gemm_q4_0(ptr(w.to(gpu)), ptr(xd), ptr(y), M, K, T, ldx, ldy, stream()))
+    wd = w.to(gpu)  # held across the call: a freed copy could be reused before the kernel reads it
+    check(capi().gdsllm_dequant_gemm_q4_0(ptr(wd), ptr(xd), ptr(y), M, K, T, ldx, ldy, stream()))
     torch.cuda.synchronize()
     yh = to_np(y)
     assert_gemv_close(yh[:, :M].copy(), deq, to_np(x).copy(), "gemm strided")

@@ -394,3 +394,66 @@ def test_moe_combine_closed_forms():
     # g large: sigmoid = 1 -> r = fp16(eo + so)
     r = oq.moe_combine(np.array([[1.0, 1024.0]], np.float16), np.array([[2.0, 0.5]], np.float16), [20.0])
     assert list(r[0]) == [np.float16(3.0), np.float16(1024.0)]
+
+
+# ------------------------------------------------------- per-column int8 weights
+
+
+def test_int8_matches_exact_rounding():
+    """Every q in [-128, 127] against special and random column scales, each
+    product rounded once with exact arithmetic; the sign of zero follows
+    IEEE (0 * negative scale = -0)."""
+    rng = np.random.default_rng(3)
+    scales = np.concatenate([np.array(SPECIAL_D, np.float16), rng.uniform(-0.01, 0.01, 24).astype(np.float16)])
+    q = np.arange(-128, 128, dtype=np.int16).astype(np.int8)[:, None].repeat(scales.size, axis=1)
+    got = oq.dequant_int8(q, scales.reshape(1, -1)).view(np.uint16)
+    for c, s in enumerate(scales):
+        sv = Fraction(float(s)) if np.isfinite(s) else None
+        s_neg = bool(np.array([s], np.float16).view(np.uint16)[0] & 0x8000)
+        for r in range(256):
+            qv = int(q[r, c])
+            g = int(got[r, c])
+            if sv is None:
+                continue
+            v = round_rne(sv * qv, 11, -14, 15)
+            if v == 0:
+                assert _sign_bit(g) == (s_neg != (qv < 0)) and g & 0x7FFF == 0, (qv, s)
+            else:
+                assert g == to_f16_bits(v), (qv, s)
+
+
+def test_int8_scale_is_per_column():
+    """q = 1 everywhere returns each column's scale in every row: a scale
+    broadcast along rows instead of columns fails."""
+    scale = np.arange(1, 9, dtype=np.float16).reshape(1, 8) * np.float16(0.125)
+    out = oq.dequant_int8(np.ones((3, 8), np.int8), scale)
+    assert np.array_equal(out, np.repeat(scale, 3, axis=0))
+
+
+def test_int8_quantizer_round_trip():
+    """The restated converter quantizer (tools/convert_weights.py:55-83) and the
+    dequant invert each other to within half a column scale; the extreme of
+    each column maps to +-127."""
+    rng = np.random.default_rng(4)
+    w = (rng.standard_normal((64, 96)) * rng.uniform(0.01, 1.0, 96)).astype(np.float16)
+    q, s = oq.quantize_int8(w)
+    assert q.dtype == np.int8 and s.shape == (1, 96)
+    back = oq.dequant_int8(q, s).astype(np.float64)
+    err = np.abs(back - w.astype(np.float64))
+    # rounding to q (half the exact scale), the fp16 rounding of the stored
+    # scale (times |q|), and the fp16 rounding of the dequantized product
+    s_exact = np.abs(w.astype(np.float64)).max(axis=0, keepdims=True) / 127.0
+    bound = 0.5 * s_exact + np.abs(q) * np.abs(s.astype(np.float64) - s_exact) + np.abs(back) * 2.0 ** -11 + 1e-12
+    assert np.all(err <= bound * (1 + 1e-6))
+    assert np.all(np.abs(q).max(axis=0) == 127)
+
+
+def test_int8_gemv_brute_force():
+    """oq.gemv over the int8 dequant equals a plain loop over exact products."""
+    rng = np.random.default_rng(5)
+    q = rng.integers(-128, 128, (5, 48)).astype(np.int8)
+    s = rng.uniform(0.001, 0.004, (1, 48)).astype(np.float16)
+    x = rng.standard_normal((2, 48)).astype(np.float16)
+    w = oq.dequant_int8(q, s)
+    want = [[sum(float(w[r, k]) * float(x[b, k]) for k in range(48)) for r in range(5)] for b in range(2)]
+    assert np.allclose(oq.gemv(w, x), np.array(want), rtol=1e-12, atol=1e-12)

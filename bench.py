@@ -239,6 +239,49 @@ def bench_q8_layer(dev, layers_rotated: int = 3, reps: int = 50):
             "layers_rotated": layers_rotated}
 
 
+def bench_int8_layer(dev, layers_rotated: int = 2, reps: int = 50, ref_reps: int = 5):
+    """Per-column int8 LLaMA-7B decoder layer at batch 1 (the converter's int8
+    format): 7 fused GEMVs per layer over `layers_rotated` distinct layers
+    (2 x 202 MB > the 256 MB Infinity Cache).  Beside it, the reference's
+    expression for the same layer on the same GPU,
+    F.linear(x, (w.float() * scale).half()) per projection (runtime/llama.py:162-165)."""
+    import torch
+    import torch.nn.functional as F
+
+    from gdsllm_amd import capi, check
+    from gdsllm_amd import synthetic as syn
+
+    gen = torch.Generator(device=dev).manual_seed(1007)
+    layers = [[syn.int8_weights(m, k, gen) for m, k in LAYER_SHAPES] for _ in range(layers_rotated)]
+    xs = {k: syn.activations(1, k, gen) for k in (4096, 11008)}
+    ys = {m: torch.empty(1, m, dtype=torch.float16, device=dev) for m in (4096, 11008)}
+    lib = capi()
+
+    def run():
+        st = torch.cuda.current_stream().cuda_stream
+        for lw in layers:
+            for (q, sc), (m, k) in zip(lw, LAYER_SHAPES):
+                check(lib.gdsllm_fused_int8_gemv(q.data_ptr(), sc.data_ptr(), xs[k].data_ptr(), ys[m].data_ptr(),
+                                                 m, k, 1, k, m, st))
+
+    def run_ref():
+        for (q, sc), (m, k) in zip(layers[0], LAYER_SHAPES):
+            F.linear(xs[k], (q.float() * sc).half())
+
+    ms = _replay_ms(run, reps) / layers_rotated
+    run_ref()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(ref_reps):
+        run_ref()
+    torch.cuda.synchronize()
+    ref_ms = (time.perf_counter() - t0) * 1e3 / ref_reps
+    nbytes = sum(m * k + 2 * k + 2 * k + 2 * m for m, k in LAYER_SHAPES)
+    return {"us_per_layer": round(ms * 1e3, 3), "bytes_per_layer": nbytes,
+            "GB_s": round(nbytes / (ms * 1e-3) / 1e9, 1), "pct_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / 80, 1),
+            "layers_rotated": layers_rotated, "reference_expression_us_per_layer": round(ref_ms * 1e3, 1)}
+
+
 def bench_moe(dev, calls: int = 64, reps: int = 20):
     """Affine-Q4 top-10 expert-gather MLP, 512 experts, hidden 4096, ffn 1024,
     group 64, batch 1; every call in the graph uses its own fresh random
@@ -498,10 +541,10 @@ def main() -> int:
     ap.add_argument("--chunk", type=int, default=64, help="launches per captured graph")
     ap.add_argument("--sweep-tokens", type=int, default=100, help="timed 7B decode-sweep tokens (0 = skip)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget (0 = skip)")
-    ap.add_argument("--configs", default="q8,moe,70b,prefill,load",
+    ap.add_argument("--configs", default="q8,moe,70b,prefill,load,int8",
                     help="comma list of extra workloads to measure: q8 (Q8_0 7B layer), moe (top-10 expert "
                          "gather), 70b (Q4_0 70B layer, B=1..8), prefill (512-token MFMA GEMM), load (7B layer "
-                         "file -> HBM, embedding row gather); '' = none")
+                         "file -> HBM, embedding row gather), int8 (per-column int8 7B layer); '' = none")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -541,7 +584,7 @@ def main() -> int:
               f"(unfused 225 launches: {sweep['unfused']['tok_s']} tok/s)", file=sys.stderr, flush=True)
 
     wanted = {c.strip() for c in args.configs.split(",") if c.strip()}
-    unknown = wanted - {"q8", "moe", "70b", "prefill", "load"}
+    unknown = wanted - {"q8", "moe", "70b", "prefill", "load", "int8"}
     if unknown:
         print(f"bench.py: unknown --configs entries {sorted(unknown)}", file=sys.stderr)
         return 2
@@ -551,7 +594,8 @@ def main() -> int:
             ("70b", "q4_0_layer_70b", lambda: bench_70b_layer(dev)),
             ("prefill", "prefill_7b_512",
              lambda: bench_prefill(dev, *sweep_weights) if sweep_weights is not None else None),
-            ("load", "load_7b_q4_0", lambda: bench_load(dev))]
+            ("load", "load_7b_q4_0", lambda: bench_load(dev)),
+            ("int8", "int8_layer_7b_b1", lambda: bench_int8_layer(dev))]
     for key, name, fn in runs:
         if key in wanted:
             res = fn()

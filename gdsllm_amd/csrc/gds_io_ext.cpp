@@ -530,7 +530,16 @@ torch::Tensor int8_linear(torch::Tensor weight, torch::Tensor scale, torch::Tens
     const int64_t rows = in_dim ? xf.numel() / in_dim : 0;
     auto out_shape = xf.sizes().vec();
     out_shape.back() = out_dim;
-    if (rows > 8) return at::linear(xf, dequant_int8(w, s, c10::nullopt)).view(out_shape);
+    if (rows > 8) {
+        // bounded fp16 temporaries, as the reference bounds its fp32 ones
+        // (runtime/scheduler.py:59-67): row chunks of at most 512 MiB
+        const int64_t step = std::max<int64_t>(1, (int64_t(512) << 20) / std::max<int64_t>(1, 2 * in_dim));
+        if (out_dim <= step) return at::linear(xf, dequant_int8(w, s, c10::nullopt)).view(out_shape);
+        std::vector<torch::Tensor> parts;
+        for (int64_t r = 0; r < out_dim; r += step)
+            parts.push_back(at::linear(xf, dequant_int8(w.narrow(0, r, std::min(step, out_dim - r)), s, c10::nullopt)));
+        return at::cat(parts, -1).view(out_shape);
+    }
     torch::Tensor out = torch::empty(out_shape, xf.options());
     if (rows == 0) return out;
     check(gdsllm_fused_int8_gemv(w.data_ptr(), s.data_ptr(), xf.data_ptr(), out.data_ptr(), out_dim, in_dim, rows,

@@ -98,3 +98,20 @@ def test_int8_linear_op_and_dispatch(gpu, rows):
     assert_gemv_close(to_np(y2), w, to_np(x), f"int8_linear rows={rows}")
     full = ext().dequant_int8(qd, sd)
     assert np.array_equal(to_np(full).view(np.uint16), w.view(np.uint16))
+
+
+def test_int8_linear_prefill_row_chunks(gpu):
+    """Above 512 MiB of fp16 weights, prefill dequantizes in row chunks: rows on
+    both sides of every chunk boundary agree with the oracle."""
+    M, K, rows = 40000, 8192, 9
+    g = torch.Generator().manual_seed(51)
+    q = torch.randint(-128, 128, (M, K), dtype=torch.int8, generator=g)
+    s = torch.empty(1, K).uniform_(0.001, 0.004, generator=g).to(torch.float16)
+    x = syn.activations(rows, K, gen(52))
+    qd, sd, xd = q.to(gpu), s.to(gpu), x.to(gpu)
+    y = to_np(ext().int8_linear(qd, sd, xd))
+    assert y.shape == (rows, M)
+    step = (512 << 20) // (2 * K)
+    check_rows = sorted({0, step - 1, step, M - 1})
+    w = oq.dequant_int8(to_np(q[check_rows]), to_np(s))
+    assert_gemv_close(y[:, check_rows], w, to_np(x), "int8 prefill chunk boundaries")

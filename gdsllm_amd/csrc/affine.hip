@@ -514,8 +514,16 @@ struct GateUpPairs {
     uint16_t* h;
     int F;
     int M;
-    // Lane l holds idx[l] (the slot count is at most 64), read once per wave.
-    __device__ int lane_index(int lane) const { return lane < M / (2 * F) ? idx[lane] : -1; }
+    // Optional shared expert (one-expert descriptors) in slot shared_slot,
+    // after the routed slots; -1 when absent.
+    gdsllm_affine_experts sgate, sup;
+    int shared_slot = -1;
+    // Lane l holds idx[l] (the slot count is at most 64), read once per wave;
+    // the shared slot reads expert 0 of its own descriptors.
+    __device__ int lane_index(int lane) const {
+        if (lane == shared_slot) return 0;
+        return lane < M / (2 * F) ? idx[lane] : -1;
+    }
     // v is the same for the whole wave (one row per load group), so the
     // expert index is a lane read, not a dependent global load.
     __device__ bool locate(int v, const uint32_t*& w, const uint16_t*& s, const uint16_t*& b, int K, int gpr,
@@ -523,7 +531,8 @@ struct GateUpPairs {
         const int k = v / (2 * F);
         const int rem = v - k * 2 * F;
         const int n = rem >> 1;
-        const gdsllm_affine_experts& p = (rem & 1) ? up : gate;
+        const bool sh = k == shared_slot;
+        const gdsllm_affine_experts& p = (rem & 1) ? (sh ? sup : up) : (sh ? sgate : gate);
         const int e = __builtin_amdgcn_readlane(lane_idx, k);
         if (e < 0 || e >= p.num_experts) return false;
         w = reinterpret_cast<const uint32_t*>(static_cast<const char*>(p.weight) + e * p.weight_stride) +
@@ -662,11 +671,18 @@ __global__ __launch_bounds__(kThreads) void affine_rows(Rows rows, const uint16_
 // row.  h of all selected experts is prepared once per workgroup in LDS
 // (records as in affine_gemv).  A stage is R output rows: R*SLOTS chunk loads
 // per lane, issued before h is prepared for the first stage.
+//
+// With a shared expert (nsh = 1: sdown, one expert, in slot top_k of h and of
+// the lane slots, gl its fp16 gate logit) the lanes of that slot accumulate
+// the shared down row separately, and the row's writer applies
+// y = clamp(fp16(routed) + fp16(fp16(sigmoid(g)) * fp16(shared))) with the
+// rounding of moe_combine (torch's fp16 elementwise ops, qwen_moe.py:508-513).
 template <int LR, int SLOTS, int NT>
 __global__ __launch_bounds__(NT) void moe_down_rows(gdsllm_affine_experts down, const int32_t* __restrict__ idx,
                                                           const uint16_t* __restrict__ rw,
                                                           const uint16_t* __restrict__ hbuf, int top_k,
-                                                          uint16_t* __restrict__ Y) {
+                                                          uint16_t* __restrict__ Y, gdsllm_affine_experts sdown,
+                                                          const uint16_t* __restrict__ gl, int nsh) {
     constexpr int EPI = 64 / LR;
     constexpr int R = SLOTS <= 4 ? 2 : 1;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -691,11 +707,12 @@ __global__ __launch_bounds__(NT) void moe_down_rows(gdsllm_affine_experts down, 
 #pragma unroll
     for (int i = 0; i < SLOTS; ++i) {
         const int k = i * EPI + sub;
-        eraw[i] = k < top_k ? idx[k] : -1;
+        eraw[i] = k < top_k ? idx[k] : (k == top_k && nsh ? 0 : -1);
         wraw[i] = k < top_k ? rw[k] : 0u;
     }
+    const uint32_t graw = nsh ? gl[0] : 0u;
     constexpr int kEarly = 2;
-    const int items = top_k * CPR * 4;
+    const int items = (top_k + nsh) * CPR * 4;
     uint4 hraw[kEarly];
 #pragma unroll
     for (int u = 0; u < kEarly; ++u) {
@@ -709,6 +726,7 @@ __global__ __launch_bounds__(NT) void moe_down_rows(gdsllm_affine_experts down, 
     // expert slot of each lane: k, routing weight, this lane's chunk of row 0
     int kk[SLOTS];
     float wk[SLOTS];
+    bool shs[SLOTS];  // this lane's slot i holds the shared expert
     const uint8_t* wrow[SLOTS];
     const uint16_t *srow[SLOTS], *brow[SLOTS];
     const int gi = (32 * li) / gsize;
@@ -716,13 +734,15 @@ __global__ __launch_bounds__(NT) void moe_down_rows(gdsllm_affine_experts down, 
     for (int i = 0; i < SLOTS; ++i) {
         const int k = i * EPI + sub;
         const int e = eraw[i];
-        const bool valid = e >= 0 && e < down.num_experts;
+        shs[i] = nsh && k == top_k;
+        const gdsllm_affine_experts& p = shs[i] ? sdown : down;
+        const bool valid = e >= 0 && e < p.num_experts;
         kk[i] = valid ? k : -1;
-        wk[i] = valid ? h2f(wraw[i]) : 0.f;
+        wk[i] = valid ? (shs[i] ? 1.0f : h2f(wraw[i])) : 0.f;
         const int64_t ee = valid ? e : 0;
-        wrow[i] = static_cast<const uint8_t*>(down.weight) + ee * down.weight_stride + 16 * li;
-        srow[i] = reinterpret_cast<const uint16_t*>(static_cast<const char*>(down.scales) + ee * down.scale_stride) + gi;
-        brow[i] = reinterpret_cast<const uint16_t*>(static_cast<const char*>(down.biases) + ee * down.bias_stride) + gi;
+        wrow[i] = static_cast<const uint8_t*>(p.weight) + ee * p.weight_stride + 16 * li;
+        srow[i] = reinterpret_cast<const uint16_t*>(static_cast<const char*>(p.scales) + ee * p.scale_stride) + gi;
+        brow[i] = reinterpret_cast<const uint16_t*>(static_cast<const char*>(p.biases) + ee * p.bias_stride) + gi;
     }
     uint4 wv[R][SLOTS];
     uint32_t sv[R][SLOTS], bv[R][SLOTS];  // raw bits: see affine_rows
@@ -787,9 +807,9 @@ __global__ __launch_bounds__(NT) void moe_down_rows(gdsllm_affine_experts down, 
                 cb[r][i] = bv[r][i];
             }
         if (t + 1 < T) issue(st + TW);
-        float acc[R];
+        float acc[R], accs[R];
 #pragma unroll
-        for (int r = 0; r < R; ++r) acc[r] = 0.f;
+        for (int r = 0; r < R; ++r) acc[r] = accs[r] = 0.f;
 #pragma unroll
         for (int i = 0; i < SLOTS; ++i)
             if (kk[i] >= 0) {
@@ -805,22 +825,43 @@ __global__ __launch_bounds__(NT) void moe_down_rows(gdsllm_affine_experts down, 
                 }
                 const float2 cs2 = *reinterpret_cast<const float2*>(rec + 64);
 #pragma unroll
-                for (int r = 0; r < R; ++r)
-                    acc[r] = __builtin_fmaf(wk[i], chunk_dot_p(cw[r][i], p, cs2.x, cs2.y, h2f(cs[r][i]), h2f(cb[r][i]), nu),
-                                            acc[r]);
+                for (int r = 0; r < R; ++r) {
+                    const float d = chunk_dot_p(cw[r][i], p, cs2.x, cs2.y, h2f(cs[r][i]), h2f(cb[r][i]), nu);
+                    if (shs[i])
+                        accs[r] += d;
+                    else
+                        acc[r] = __builtin_fmaf(wk[i], d, acc[r]);
+                }
             }
         // sum over all 64 lanes (every expert slot and chunk); R = 2: lanes < 32 row 0
-        float v;
-        if constexpr (R == 2) {
-            const bool h32 = lane & 32;
-            v = (h32 ? acc[1] : acc[0]) + __shfl_xor(h32 ? acc[0] : acc[1], 32);
-        } else {
-            v = acc[0] + __shfl_xor(acc[0], 32);
-        }
-        v += __shfl_xor(v, 16);
-        v = lanes_sum<16>(v);
+        auto lanes64 = [&](const float (&a)[R]) {
+            float v;
+            if constexpr (R == 2) {
+                const bool h32 = lane & 32;
+                v = (h32 ? a[1] : a[0]) + __shfl_xor(h32 ? a[0] : a[1], 32);
+            } else {
+                v = a[0] + __shfl_xor(a[0], 32);
+            }
+            v += __shfl_xor(v, 16);
+            return lanes_sum<16>(v);
+        };
+        const float v = lanes64(acc);
         const int o = st * R + (R == 2 ? (lane >> 5) : 0);
-        if ((lane & 31) == 0 && (R == 2 || lane == 0) && o < H) Y[o] = f2h_bits(v);
+        const bool writer = (lane & 31) == 0 && (R == 2 || lane == 0) && o < H;
+        if (nsh) {
+            const float vs = lanes64(accs);
+            if (writer) {
+                const float g = h2f(graw);
+                const float sw = h2f(f2h_bits(fp32_rounded(1.0f / fp32_rounded(1.0f + expf(-g)))));
+                const float sc = h2f(f2h_bits(fp32_rounded(sw * h2f(f2h_bits(vs)))));
+                float r = h2f(f2h_bits(fp32_rounded(h2f(f2h_bits(v)) + sc)));
+                if (r > 65504.0f) r = 65504.0f;  // NaN compares false both ways and stays NaN
+                if (r < -65504.0f) r = -65504.0f;
+                Y[o] = f2h_bits(r);
+            }
+        } else if (writer) {
+            Y[o] = f2h_bits(v);
+        }
     }
 }
 
@@ -871,32 +912,36 @@ int dispatch_rows(const Rows& rows, const uint16_t* x, int K, int gsize, int64_t
 // fewer times.
 template <int LR, int SLOTS>
 int launch_moe_down(const gdsllm_affine_experts& down, const int32_t* idx, const uint16_t* rw, const uint16_t* h,
-                    int top_k, uint16_t* y, hipStream_t stream) {
+                    int top_k, uint16_t* y, hipStream_t stream, const gdsllm_affine_experts* sdown = nullptr,
+                    const uint16_t* gl = nullptr) {
     constexpr int NT = (SLOTS <= 3 || SLOTS == 5) ? 1024 : 512;
     const void* fn = reinterpret_cast<const void*>(&moe_down_rows<LR, SLOTS, NT>);
-    const size_t lds = static_cast<size_t>(top_k) * (down.in_dim / 32) * kRec;
+    const int nsh = sdown ? 1 : 0;
+    const size_t lds = static_cast<size_t>(top_k + nsh) * (down.in_dim / 32) * kRec;
     if (int rc = prepare_lds(fn, lds)) return rc;
     constexpr int R = SLOTS <= 4 ? 2 : 1;
     const int stages = static_cast<int>((down.out_dim + R - 1) / R);
     const int need = (stages + NT / 64 - 1) / (NT / 64);
     const int cap = blocks_per_cu(fn, lds, NT) * cu_count();
     const int grid = need < cap ? need : cap;
-    hipLaunchKernelGGL((moe_down_rows<LR, SLOTS, NT>), dim3(grid), dim3(NT), lds, stream, down, idx, rw, h, top_k, y);
+    hipLaunchKernelGGL((moe_down_rows<LR, SLOTS, NT>), dim3(grid), dim3(NT), lds, stream, down, idx, rw, h, top_k, y,
+                       sdown ? *sdown : down, gl, nsh);
     return check_hip(hipGetLastError(), "moe_down_rows launch");
 }
 
 template <int LR>
 int dispatch_moe_down_slots(int slots, const gdsllm_affine_experts& down, const int32_t* idx, const uint16_t* rw,
-                            const uint16_t* h, int top_k, uint16_t* y, hipStream_t stream) {
+                            const uint16_t* h, int top_k, uint16_t* y, hipStream_t stream,
+                            const gdsllm_affine_experts* sdown = nullptr, const uint16_t* gl = nullptr) {
     switch (slots) {
-        case 1: return launch_moe_down<LR, 1>(down, idx, rw, h, top_k, y, stream);
-        case 2: return launch_moe_down<LR, 2>(down, idx, rw, h, top_k, y, stream);
-        case 3: return launch_moe_down<LR, 3>(down, idx, rw, h, top_k, y, stream);
-        case 4: return launch_moe_down<LR, 4>(down, idx, rw, h, top_k, y, stream);
-        case 5: return launch_moe_down<LR, 5>(down, idx, rw, h, top_k, y, stream);
-        case 6: return launch_moe_down<LR, 6>(down, idx, rw, h, top_k, y, stream);
-        case 7: return launch_moe_down<LR, 7>(down, idx, rw, h, top_k, y, stream);
-        case 8: return launch_moe_down<LR, 8>(down, idx, rw, h, top_k, y, stream);
+        case 1: return launch_moe_down<LR, 1>(down, idx, rw, h, top_k, y, stream, sdown, gl);
+        case 2: return launch_moe_down<LR, 2>(down, idx, rw, h, top_k, y, stream, sdown, gl);
+        case 3: return launch_moe_down<LR, 3>(down, idx, rw, h, top_k, y, stream, sdown, gl);
+        case 4: return launch_moe_down<LR, 4>(down, idx, rw, h, top_k, y, stream, sdown, gl);
+        case 5: return launch_moe_down<LR, 5>(down, idx, rw, h, top_k, y, stream, sdown, gl);
+        case 6: return launch_moe_down<LR, 6>(down, idx, rw, h, top_k, y, stream, sdown, gl);
+        case 7: return launch_moe_down<LR, 7>(down, idx, rw, h, top_k, y, stream, sdown, gl);
+        case 8: return launch_moe_down<LR, 8>(down, idx, rw, h, top_k, y, stream, sdown, gl);
         default: return set_error(GDSLLM_ERR_UNSUPPORTED, "moe_down_rows: too many expert slots");
     }
 }
@@ -1092,4 +1137,79 @@ extern "C" int gdsllm_moe_gather_affine_q4(const gdsllm_affine_experts* gate, co
     }
     if (int rc = check_hip(hipGetLastError(), "moe_down launch")) return rc;
     return ok();
+}
+
+extern "C" int gdsllm_moe_step_affine_q4(const gdsllm_affine_experts* gate, const gdsllm_affine_experts* up,
+                                         const gdsllm_affine_experts* down, const gdsllm_affine_experts* shared_gate,
+                                         const gdsllm_affine_experts* shared_up,
+                                         const gdsllm_affine_experts* shared_down, const void* x, const int32_t* idx,
+                                         const void* routing_weights, int64_t top_k, const void* shared_gate_logit,
+                                         void* y, void* workspace, size_t workspace_bytes, void* stream) {
+    const std::string n = "moe_step_affine_q4";
+    std::string err;
+    if (check_experts(gate, "gate", err) || check_experts(up, "up", err) || check_experts(down, "down", err) ||
+        check_experts(shared_gate, "shared_gate", err) || check_experts(shared_up, "shared_up", err) ||
+        check_experts(shared_down, "shared_down", err))
+        return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": " + err);
+    if (top_k < 1 || top_k > 63)
+        return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": top_k must be in [1, 63], got " + std::to_string(top_k));
+    const int64_t H = gate->in_dim, F = gate->out_dim;
+    if (up->in_dim != H || up->out_dim != F || down->in_dim != F || down->out_dim != H ||
+        gate->group_size != up->group_size || up->num_experts != gate->num_experts ||
+        down->num_experts != gate->num_experts)
+        return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": gate/up [E,F,H] and down [E,H,F] shapes disagree");
+    if (shared_gate->in_dim != H || shared_up->in_dim != H || shared_down->out_dim != H ||
+        shared_gate->out_dim != shared_up->out_dim || shared_down->in_dim != shared_gate->out_dim)
+        return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": shared expert shapes disagree with hidden size");
+    if (!x || !idx || !routing_weights || !shared_gate_logit || !y || !workspace)
+        return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": null pointer");
+    if (reinterpret_cast<uintptr_t>(x) % 2 || reinterpret_cast<uintptr_t>(y) % 2 ||
+        reinterpret_cast<uintptr_t>(routing_weights) % 2 || reinterpret_cast<uintptr_t>(shared_gate_logit) % 2 ||
+        reinterpret_cast<uintptr_t>(idx) % 4 || reinterpret_cast<uintptr_t>(workspace) % 16)
+        return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": misaligned pointer");
+    if (workspace_bytes < gdsllm_moe_gather_workspace_size(top_k + 1, F))
+        return set_error(GDSLLM_ERR_INVALID_ARGUMENT,
+                         n + ": workspace too small (" + std::to_string(workspace_bytes) + " < " +
+                             std::to_string(gdsllm_moe_gather_workspace_size(top_k + 1, F)) + ")");
+    // The fused step serves the row-span shapes with a shared expert of the
+    // routed experts' width and grouping; anything else is the caller's
+    // separate gather + shared expert + combine.
+    const int cpr_h = static_cast<int>(H / 32), cpr_f = static_cast<int>(F / 32);
+    const int nslot = static_cast<int>(top_k) + 1;
+    const int slots = (cpr_f >= 16 && cpr_f <= 64) ? (nslot + 64 / cpr_f - 1) / (64 / cpr_f) : 0;
+    const bool rows_path = H % 2048 == 0 && H <= 8192 && (cpr_f == 16 || cpr_f == 32 || cpr_f == 64) && slots >= 1 &&
+                           slots <= 8 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
+    if (!rows_path || shared_gate->out_dim != F || shared_gate->group_size != gate->group_size ||
+        shared_up->group_size != gate->group_size || shared_down->group_size != down->group_size)
+        return set_error(GDSLLM_ERR_UNSUPPORTED, n + ": shape outside the fused step (use the separate launches)");
+    const size_t budget = static_cast<size_t>(max_lds_bytes());
+    if (static_cast<size_t>(nslot) * cpr_f * kRec > budget || static_cast<size_t>(cpr_h) * kRec > budget)
+        return set_error(GDSLLM_ERR_UNSUPPORTED, n + ": hidden or (top_k+1)*ffn too large for LDS staging");
+    hipStream_t s = as_stream(stream);
+    auto* gu = static_cast<uint16_t*>(workspace);
+    uint16_t* h = gu + static_cast<int64_t>(nslot) * 2 * F;  // after the gate/up outputs of every slot
+    GateUpPairs pairs{*gate, *up, idx, gu, h, static_cast<int>(F), static_cast<int>(2 * nslot * F)};
+    pairs.sgate = *shared_gate;
+    pairs.sup = *shared_up;
+    pairs.shared_slot = static_cast<int>(top_k);
+    const auto* xp = static_cast<const uint16_t*>(x);
+    const int gs = static_cast<int>(gate->group_size);
+    int rc;
+    switch (cpr_h / 64) {
+        case 1: rc = launch_affine_rows<64, 1, 1>(pairs, xp, static_cast<int>(H), gs, H, s); break;
+        case 2: rc = launch_affine_rows<64, 2, 1>(pairs, xp, static_cast<int>(H), gs, H, s); break;
+        case 3: rc = launch_affine_rows<64, 3, 1>(pairs, xp, static_cast<int>(H), gs, H, s); break;
+        default: rc = launch_affine_rows<64, 4, 1>(pairs, xp, static_cast<int>(H), gs, H, s); break;
+    }
+    if (rc) return rc;
+    const auto* wp = static_cast<const uint16_t*>(routing_weights);
+    const auto* gl = static_cast<const uint16_t*>(shared_gate_logit);
+    auto* yp = static_cast<uint16_t*>(y);
+    const int tk = static_cast<int>(top_k);
+    switch (cpr_f) {
+        case 16: rc = dispatch_moe_down_slots<16>(slots, *down, idx, wp, h, tk, yp, s, shared_down, gl); break;
+        case 32: rc = dispatch_moe_down_slots<32>(slots, *down, idx, wp, h, tk, yp, s, shared_down, gl); break;
+        default: rc = dispatch_moe_down_slots<64>(slots, *down, idx, wp, h, tk, yp, s, shared_down, gl); break;
+    }
+    return rc ? rc : ok();
 }

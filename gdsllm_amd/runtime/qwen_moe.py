@@ -100,6 +100,34 @@ def moe_gather(x: torch.Tensor, weights: Dict, top_k_indices: torch.Tensor, top_
     return out.view(1, 1, -1)
 
 
+_SHARED_PROJ = ("mlp.shared_expert.gate_proj", "mlp.shared_expert.up_proj", "mlp.shared_expert.down_proj")
+
+
+def _entry(m: dict) -> tuple:
+    return (m["buffer"], list(m["shape"]), m["weight_offset"], m["scale_offset"], m["bias_offset"], m["group_size"])
+
+
+def moe_step(x: torch.Tensor, weights: Dict, top_k_indices: torch.Tensor, top_k_weights: torch.Tensor):
+    """The decode MoE MLP of runtime/qwen_moe.py:455-513 for one token in three
+    launches: the fp16 shared-expert-gate GEMV, then one launch for the gate/up
+    rows of the top-k experts and the shared expert, and one for their down
+    rows with the sigmoid-gated combine and clamp.  Returns (1, 1, hidden), or
+    None when the layer has no affine_q4 shared expert with an fp16 gate or its
+    shapes are outside the fused kernels (the caller then runs the separate
+    launches)."""
+    shared = [weights.get(f"{p}.weight") for p in _SHARED_PROJ]
+    sg = weights.get("mlp.shared_expert_gate.weight")
+    if any(not isinstance(m, dict) for m in shared) or not isinstance(sg, torch.Tensor):
+        return None
+    routed = [weights[f"{p}.weight"] for p in _EXPERT_PROJ]
+    gate_logit = ext().gemv_f16(sg, x)
+    out = ext().moe_step_affine_q4(
+        x.reshape(-1), [_entry(m) for m in routed + shared],
+        top_k_indices.reshape(-1), top_k_weights.reshape(-1), gate_logit.reshape(-1),
+    )
+    return None if out is None else out.view(1, 1, -1)
+
+
 def _expert_meta(stacked: dict, e: int) -> dict:
     """One expert's slice of a stacked [E, N, K] affine_q4 entry (runtime/torch_bridge.py:326-337)."""
     E, N, K = stacked["shape"]
@@ -130,6 +158,10 @@ def moe_mlp_selective(
     x_flat = x.view(-1, hidden)
     n_tok = x_flat.shape[0]
     resident = expert_tensors is None
+    if resident and n_tok == 1:
+        fused = moe_step(x, weights, top_k_indices, top_k_weights)
+        if fused is not None:
+            return fused
     if resident and n_tok == 1:
         expert_output = moe_gather(x, weights, top_k_indices, top_k_weights).view(1, hidden)
     else:

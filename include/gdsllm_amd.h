@@ -198,6 +198,24 @@ int gdsllm_moe_gather_affine_q4(const gdsllm_affine_experts* gate,
                                 const void* routing_weights, int64_t top_k,
                                 void* y, void* workspace, size_t workspace_bytes,
                                 void* stream);
+/* The whole decode MoE MLP of qwen_moe.py:455-513 after routing, in two
+ * launches: the top_k routed experts and the shared expert (one-expert
+ * descriptors shared_gate/shared_up [1][F][H], shared_down [1][H][F]) share
+ * the gate/up launch, and the down launch also applies the shared expert and
+ * the combine: y = clamp(fp16(sum_k w_k * down_k(h_k)) +
+ * fp16(fp16(sigmoid(g)) * fp16(shared_down(h_s))), +-65504) with g the fp16
+ * shared-gate logit (from gdsllm_gemv_f16), the rounding of
+ * gdsllm_moe_combine.  No counterpart in the reference, which issues ~40
+ * launches for it.  Needs the row-span shapes of gdsllm_moe_gather_affine_q4
+ * with top_k + 1 slots and a shared expert of the routed width and grouping
+ * (else GDSLLM_ERR_UNSUPPORTED); workspace_bytes >=
+ * gdsllm_moe_gather_workspace_size(top_k + 1, F).                            */
+int gdsllm_moe_step_affine_q4(const gdsllm_affine_experts* gate, const gdsllm_affine_experts* up,
+                              const gdsllm_affine_experts* down, const gdsllm_affine_experts* shared_gate,
+                              const gdsllm_affine_experts* shared_up, const gdsllm_affine_experts* shared_down,
+                              const void* x, const int32_t* idx, const void* routing_weights, int64_t top_k,
+                              const void* shared_gate_logit, void* y, void* workspace, size_t workspace_bytes,
+                              void* stream);
 
 /* --------------------------------------- on-device MoE routing, epilogue --
  * The reference routes on the host side of a sync (F.linear, torch.topk,

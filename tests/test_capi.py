@@ -27,7 +27,7 @@ def declared_functions() -> dict:
 def test_header_declares_the_entry_points():
     names = set(declared_functions())
     assert {"gdsllm_fused_q4_0_gemv", "gdsllm_fused_q8_0_gemv", "gdsllm_fused_affine_q4_gemv", "gdsllm_dequant_q4_0",
-            "gdsllm_dequant_q8_0", "gdsllm_dequant_affine_q4", "gdsllm_moe_gather_affine_q4",
+            "gdsllm_dequant_q8_0", "gdsllm_dequant_affine_q4", "gdsllm_moe_gather_affine_q4", "gdsllm_moe_step_affine_q4",
             "gdsllm_dequant_gemm_q4_0"} <= names
 
 
@@ -153,6 +153,35 @@ def test_moe_gather_validation():
                                            None) == 1
 
 
+def test_moe_step_validation():
+    """The fused decode step checks its arguments, and answers UNSUPPORTED (2)
+    for shapes outside its kernels before touching the device."""
+    lib = capi()
+    H, F = 2048, 512
+    gate, up, down = _experts(N=F, K=H), _experts(N=F, K=H), _experts(N=H, K=F)
+    sg, su, sd = _experts(E=1, N=F, K=H), _experts(E=1, N=F, K=H), _experts(E=1, N=H, K=F)
+    ws = lib.gdsllm_moe_gather_workspace_size(5, F)
+
+    def call(g=gate, u=up, d=down, a=sg, b=su, c=sd, k=4, wsb=ws, gl=16, x=16):
+        return lib.gdsllm_moe_step_affine_q4(*(ctypes.byref(e) for e in (g, u, d, a, b, c)), x, 16, 16, k, gl, 16,
+                                             16, wsb, None)
+
+    assert call(k=0) == 1 and "top_k" in _err()
+    assert call(k=64) == 1
+    assert call(wsb=lib.gdsllm_moe_gather_workspace_size(4, F)) == 1 and "workspace" in _err()
+    assert call(d=_experts(N=F, K=H)) == 1 and "disagree" in _err()
+    assert call(c=_experts(E=1, N=1024, K=F)) == 1 and "shared" in _err()
+    assert call(gl=None) == 1 and "null" in _err()
+    assert call(gl=17) == 1 and "misaligned" in _err()
+    assert call(x=8) == 2  # x off the 16-byte grid: separate launches
+    small = dict(g=_experts(N=F, K=1024), u=_experts(N=F, K=1024), d=_experts(N=1024, K=F),
+                 a=_experts(E=1, N=F, K=1024), b=_experts(E=1, N=F, K=1024), c=_experts(E=1, N=1024, K=F))
+    assert call(**small) == 2 and "separate" in _err()  # hidden not a multiple of 2048
+    wide = dict(a=_experts(E=1, N=1024, K=H), b=_experts(E=1, N=1024, K=H), c=_experts(E=1, N=H, K=1024))
+    assert call(**wide) == 2  # shared width differs from the routed width
+    assert call(k=32, wsb=lib.gdsllm_moe_gather_workspace_size(33, F)) == 2  # 33 slots, 4 per lane group: > 8
+
+
 @pytest.mark.parametrize("name", ["gdsllm_embed_q4_0", "gdsllm_embed_q8_0"])
 def test_embed_validation(name):
     fn = getattr(capi(), name)
@@ -220,6 +249,7 @@ def test_extension_module_surface():
         "embed_gguf": ["handle", "token_ids", "shape", "gguf_type", "offset"],
         "dequant_int8": ["weight", "scale", "output"],
         "int8_linear": ["weight", "scale", "x"],
+        "moe_step_affine_q4": ["x", "entries", "top_k_indices", "top_k_weights", "shared_gate_logit"],
     }
     for name, args in expected.items():
         fn = getattr(m, name)

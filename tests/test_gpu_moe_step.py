@@ -1,0 +1,135 @@
+"""The fused decode MoE step (gdsllm_moe_step_affine_q4): routed top-k experts
+and the shared expert in one gate/up launch, their down rows with the
+sigmoid-gated combine in one more (runtime/qwen_moe.py:455-513 after routing).
+
+Its output is bit-identical to the separate launches it replaces (the top-k
+gather, a one-expert gather of the shared expert, the fp16 gate GEMV and the
+combine): the shared expert occupies its own lane slot, so every sum is formed
+in the same order.  The oracle composition bounds both under a relative-L2
+tolerance."""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from gdsllm_amd import capi, check
+from helpers import affine_dequant_np, experts_struct, gen, moe_gather, oq, ptr, stream, syn, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(parts, gpu):
+    return tuple(t.to(gpu) for t in parts)
+
+
+def _shared_stacked(parts):
+    return tuple(t.unsqueeze(0) for t in parts)
+
+
+def _step(routed, shared, x, idx, w, gl, g, top_k, gpu):
+    structs = [experts_struct(*p, g) for p in routed + shared]
+    F = structs[0].out_dim
+    ws_bytes = capi().gdsllm_moe_gather_workspace_size(top_k + 1, F)
+    ws = torch.full((ws_bytes,), 0xFF, dtype=torch.uint8, device=gpu)  # NaN-filled: every read slot must be written
+    y = torch.empty(structs[2].out_dim, dtype=torch.float16, device=gpu)
+    check(capi().gdsllm_moe_step_affine_q4(*(ctypes.byref(s) for s in structs), ptr(x), ptr(idx), ptr(w), top_k,
+                                           ptr(gl), ptr(y), ptr(ws), ws_bytes, stream()))
+    torch.cuda.synchronize()
+    return y
+
+
+def _separate(routed, shared, x, idx, w, gl, g, gpu):
+    eo = moe_gather(*routed, x, idx, w, g)
+    one = torch.zeros(1, dtype=torch.int32, device=gpu)
+    unit = torch.ones(1, dtype=torch.float16, device=gpu)
+    so = moe_gather(*shared, x, one, unit, g)
+    y = torch.empty_like(eo)
+    check(capi().gdsllm_moe_combine(ptr(eo), ptr(so), ptr(gl), ptr(y), eo.numel(), 1, stream()))  # hidden, n_tok
+    torch.cuda.synchronize()
+    return y
+
+
+# (E, H, F, top_k): one to eight lane slots, 4 / 2 / 1 experts per lane group
+CASES = [(8, 2048, 512, 1), (16, 2048, 512, 3), (64, 2048, 512, 4), (128, 2048, 512, 8), (64, 4096, 512, 10),
+         (32, 2048, 1024, 2), (32, 4096, 1024, 5), (16, 6144, 1024, 3), (16, 2048, 2048, 1), (16, 8192, 2048, 7),
+         (512, 2048, 512, 31)]
+
+
+@pytest.mark.parametrize("E,H,F,k", CASES)
+def test_moe_step_matches_separate_launches(gpu, E, H, F, k):
+    g = 64
+    gg = gen(9100 + E + H + F + k)
+    routed_cpu = [syn.affine_q4_weights(s, g, gg) for s in ([E, F, H], [E, F, H], [E, H, F])]
+    shared_cpu = [_shared_stacked(syn.affine_q4_weights(s, g, gg)) for s in ([F, H], [F, H], [H, F])]
+    routed = [_dev(p, gpu) for p in routed_cpu]
+    shared = [_dev(p, gpu) for p in shared_cpu]
+    x = syn.activations(1, H, gen(9200 + k)).to(gpu)
+    picks = torch.randperm(E, generator=gen(9300 + k))[:k].to(torch.int32)
+    rw = torch.softmax(torch.randn(k, generator=gen(9400 + k)), 0).to(torch.float16)
+    gl_cpu = torch.tensor([0.75 - 0.1 * k], dtype=torch.float16)
+    idx, w, gl = picks.to(gpu), rw.to(gpu), gl_cpu.to(gpu)
+
+    y = _step(routed, shared, x, idx, w, gl, g, k, gpu)
+    want = _separate(routed, shared, x, idx, w, gl, g, gpu)
+    np.testing.assert_array_equal(to_np(y).view(np.uint16), to_np(want).view(np.uint16))
+
+    def dq(p, e):
+        return affine_dequant_np(*(t[e] for t in p), g).reshape(p[0].shape[1], -1)
+
+    xn = to_np(x).reshape(-1)
+    eo, _ = oq.moe_gather(xn, lambda e: dq(routed_cpu[0], e), lambda e: dq(routed_cpu[1], e),
+                          lambda e: dq(routed_cpu[2], e), to_np(picks), to_np(rw))
+    so, _ = oq.moe_gather(xn, lambda e: dq(shared_cpu[0], e), lambda e: dq(shared_cpu[1], e),
+                          lambda e: dq(shared_cpu[2], e), np.zeros(1, np.int32), np.ones(1, np.float16))
+    ref = oq.moe_combine(eo.astype(np.float16)[None], so.astype(np.float16)[None], to_np(gl_cpu)).astype(np.float64)
+    got = to_np(y).astype(np.float64)
+    rel = float(np.linalg.norm(got - ref.reshape(-1)) / np.linalg.norm(ref))
+    assert np.all(np.isfinite(got)) and rel <= 5e-3, f"rel L2 {rel:.3e}"
+
+
+def test_moe_step_invalid_indices_and_clamp(gpu):
+    """Out-of-range expert indices contribute nothing (as in the gather), and a
+    large shared gate drives outputs past fp16 range into the +-65504 clamp."""
+    E, H, F, k, g = 16, 2048, 512, 6, 64
+    gg = gen(9500)
+    routed = [_dev(syn.affine_q4_weights(s, g, gg), gpu) for s in ([E, F, H], [E, F, H], [E, H, F])]
+    # shared down rows scaled up so fp16(sigmoid(g) * shared) overflows for some rows
+    sgw, suw, sdw = (_shared_stacked(syn.affine_q4_weights(s, g, gg)) for s in ([F, H], [F, H], [H, F]))
+    sdw = (sdw[0], (sdw[1].float() * 2000).to(torch.float16), (sdw[2].float() * 2000).to(torch.float16))
+    shared = [_dev(p, gpu) for p in (sgw, suw, sdw)]
+    x = syn.activations(1, H, gen(9501)).to(gpu)
+    idx = torch.tensor([3, -1, 15, 16, 7, 1 << 20], dtype=torch.int32, device=gpu)
+    w = torch.full((k,), 1.0 / k, dtype=torch.float16, device=gpu)
+    gl = torch.tensor([4.0], dtype=torch.float16, device=gpu)
+    y = _step(routed, shared, x, idx, w, gl, g, k, gpu)
+    want = _separate(routed, shared, x, idx, w, gl, g, gpu)
+    yn = to_np(y)
+    np.testing.assert_array_equal(yn.view(np.uint16), to_np(want).view(np.uint16))
+    assert np.any(np.abs(yn) == 65504.0) and np.all(np.isfinite(yn))
+
+
+def test_moe_step_two_calls_share_nothing(gpu):
+    """A second call with fewer experts on the same workspace gives the result
+    a fresh workspace gives (no state carried from the first)."""
+    E, H, F, g = 32, 2048, 1024, 64
+    gg = gen(9600)
+    routed = [_dev(syn.affine_q4_weights(s, g, gg), gpu) for s in ([E, F, H], [E, F, H], [E, H, F])]
+    shared = [_dev(_shared_stacked(syn.affine_q4_weights(s, g, gg)), gpu) for s in ([F, H], [F, H], [H, F])]
+    x = syn.activations(1, H, gen(9601)).to(gpu)
+    gl = torch.tensor([-0.5], dtype=torch.float16, device=gpu)
+    structs = [experts_struct(*p, g) for p in routed + shared]
+    ws_bytes = capi().gdsllm_moe_gather_workspace_size(9, F)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=gpu)
+    outs = []
+    for k in (8, 3):
+        idx = torch.arange(k, dtype=torch.int32, device=gpu) * 3
+        w = torch.full((k,), 1.0 / k, dtype=torch.float16, device=gpu)
+        y = torch.empty(H, dtype=torch.float16, device=gpu)
+        check(capi().gdsllm_moe_step_affine_q4(*(ctypes.byref(s) for s in structs), ptr(x), ptr(idx), ptr(w), k,
+                                               ptr(gl), ptr(y), ptr(ws), ws_bytes, stream()))
+        torch.cuda.synchronize()
+        outs.append((y, _separate(routed, shared, x, idx, w, gl, g, gpu)))
+    for y, want in outs:
+        np.testing.assert_array_equal(to_np(y).view(np.uint16), to_np(want).view(np.uint16))

@@ -1312,6 +1312,252 @@ int launch_q4_codes(const void* w, const uint16_t* x, uint16_t* y, int M, int K,
     return check_hip(hipGetLastError(), "gguf_gemv_q4_codes launch");
 }
 
+// ---- Q4_0 codes on MFMA with x held in registers (in_dim <= 8192) ----------
+//
+// Same operands and arithmetic as gguf_gemv_q4_codes, different data
+// movement.  Wave w of a workgroup always takes super-blocks w, w+8, ... of K
+// (at most 4 at in_dim 8192), for every 16-row tile the workgroup owns, so its
+// slice of x (up to 4 super-blocks x 8 batch rows, 16 KiB) is loaded once and
+// its offset corrections computed once.  LDS then holds weights only: 8 stage
+// slots per wave, so a wave keeps up to 8 stages in flight against 2 when
+// every stage carried its own x, and x is read once per wave instead of once
+// per row tile.  The x slice comes in by LDS DMA (2 batch rows x 512 bytes per
+// transfer) into the wave's slots and is read into registers before the
+// first weights are issued; register loads straight from HBM gathered 8
+// batch rows per instruction and took ~4 us longer per launch.
+namespace bx {
+constexpr int kWaves = 8;
+constexpr int kNSB = 4;  // super-blocks of K per wave at most
+constexpr int kRT = 16;  // rows per tile
+constexpr int kNWD = (kRT * 9 + 63) / 64;                  // weight transfers per stage (3)
+constexpr int kLastLanes = kRT * 9 - 64 * (kNWD - 1);      // lanes of the last one (16)
+constexpr int kNS = 8;                                     // stage slots per wave
+constexpr int kSlotBytes = kRT * 144;                      // one super-block of the tile's rows
+constexpr int kRedBytes = kWaves * 8 * kRT * 4;            // one tile's partial sums
+constexpr int kLdsBytes = kWaves * kNS * kSlotBytes + 2 * kRedBytes;
+static_assert(kNS * kSlotBytes >= kNSB * 4096, "the x slice is staged in the wave's slots");
+}  // namespace bx
+
+__global__ __launch_bounds__(bx::kWaves * 64) void gguf_gemv_q4_xreg(const uint8_t* __restrict__ W,
+                                                                    const uint16_t* __restrict__ X,
+                                                                    uint16_t* __restrict__ Y, int M, int K, int nb,
+                                                                    int64_t ldx, int64_t ldy) {
+    constexpr int RT = bx::kRT, NRG = RT / 8, NWD = bx::kNWD, NS = bx::kNS;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int S = K >> 8;
+    const uint32_t row_bytes = static_cast<uint32_t>(S) * 144u;
+    const int ntiles = (M + RT - 1) / RT;
+    const int T = (ntiles - static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) - 1) / static_cast<int>(gridDim.x);
+    const int nst = S > wave ? (S - 1 - wave) / bx::kWaves + 1 : 0;  // super-blocks of this wave (<= 4)
+    const int Q = T * nst;
+    const uint32_t lds0 = lds_addr(lds);
+    const uint32_t slot0 = lds0 + wave * NS * bx::kSlotBytes;
+    float* red0 = reinterpret_cast<float*>(lds + bx::kWaves * NS * bx::kSlotBytes);
+
+    // weight transfer j: chunk c = 64j + lane = row c / 9, chunk c % 9 of the
+    // row's super-block (rows past the tile's last valid row read that row)
+    auto w_offsets = [&](int nrows, uint32_t (&off)[NWD]) {
+#pragma unroll
+        for (int j = 0; j < NWD; ++j) {
+            const int c = min(64 * j + lane, RT * 9 - 1);
+            const int r = c / 9;
+            off[j] = static_cast<uint32_t>(min(r, nrows - 1)) * row_bytes + 16u * static_cast<uint32_t>(c - 9 * r);
+        }
+    };
+    uint32_t woff_full[NWD];
+    w_offsets(RT, woff_full);
+
+    int ii = 0, ss = 0, qs = 0;  // next stage to issue: tile ii, super-block step ss, slot qs
+    auto issue = [&]() {
+        const uint32_t slot = slot0 + qs * bx::kSlotBytes;
+        const int sb = wave + bx::kWaves * ss;
+        const int row0 = RT * (static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) * ii);
+        const uint8_t* wb = W + static_cast<int64_t>(row0) * row_bytes + 144 * sb;
+        uint32_t woff[NWD];
+        const int nrows = min(RT, M - row0);
+        if (nrows == RT) {
+#pragma unroll
+            for (int j = 0; j < NWD; ++j) woff[j] = woff_full[j];
+        } else {
+            w_offsets(nrows, woff);
+        }
+#pragma unroll
+        for (int j = 0; j < NWD - 1; ++j) dma16_asm(woff[j], wb, slot + 1024 * j);
+        if (lane < bx::kLastLanes) dma16_asm(woff[NWD - 1], wb, slot + 1024 * (NWD - 1));
+        if (++ss == nst) {
+            ss = 0;
+            ++ii;
+        }
+        if (++qs == NS) qs = 0;
+    };
+
+    // per-lane operand geometry, as in gguf_gemv_q4_codes
+    const int g = lane >> 4, j = lane & 15, par = j >> 3;
+    const uint32_t wrd = 144 * (j & 7) + (par ? 20 : 0) + 4 * g;
+    const uint32_t drd = 144 * (j & 7) + 18 * par;
+    const uint32_t sel01 = par ? 0x0C010C00u : 0x0C030C02u;
+    const uint32_t sel23 = par ? 0x0C030C02u : 0x0C050C04u;
+    const NibUnpack nu;
+
+    int ck = 0;
+    float4_t acc[NRG];
+#pragma unroll
+    for (int r = 0; r < NRG; ++r) acc[r] = float4_t{0.f, 0.f, 0.f, 0.f};
+    auto finish_tile = [&]() {
+        float* red = red0 + (ck & 1) * (bx::kRedBytes / 4);
+        const int src = lane + 40 < 64 ? lane + 40 : lane;
+#pragma unroll
+        for (int rg = 0; rg < NRG; ++rg) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float o = __shfl(acc[rg][v], src, 64);
+                if (g < 2 && j < 8) red[(wave * 8 + 4 * g + v) * RT + 8 * rg + j] = acc[rg][v] + o;
+            }
+            acc[rg] = float4_t{0.f, 0.f, 0.f, 0.f};
+        }
+        lds_barrier();
+        const int i = threadIdx.x;
+        const int row0 = RT * (static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) * ck);
+        if (i < 8 * RT) {
+            const int t = i / RT, r = i - t * RT;
+            float sum = 0.f;
+#pragma unroll
+            for (int w = 0; w < bx::kWaves; ++w) sum += red[(w * 8 + t) * RT + r];
+            if (t < nb && row0 + r < M) Y[t * ldy + row0 + r] = f2h_bits(sum);
+        }
+        ++ck;
+    };
+
+    if (nst == 0) {
+        // K has fewer super-blocks than the workgroup has waves: this wave
+        // adds zero partials to every tile's sum
+        for (int k = 0; k < T; ++k) finish_tile();
+        return;
+    }
+
+    // x slice: 4 transfers per super-block into the wave's slots (transfer jj
+    // holds batch rows 2jj, 2jj+1, rows past nb repeat row nb - 1; the
+    // super-blocks past this wave's last repeat it), then into registers.
+    half8_t xa[bx::kNSB][4];
+    {
+#pragma unroll
+        for (int s2 = 0; s2 < bx::kNSB; ++s2) {
+            const int sb = wave + bx::kWaves * min(s2, nst - 1);
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                const int tr = min(2 * jj + (lane >> 5), nb - 1);
+                dma16_asm(static_cast<uint32_t>(2 * (tr * ldx + 8 * (lane & 31))), X + 256 * sb,
+                          slot0 + 4096 * s2 + 1024 * jj);
+            }
+        }
+        wait_vmcnt_asm<0>();
+        // lane (g, j): batch row j & 7 of block 2p + par, elements 4g.. and 16+4g..
+        const int t = min(j & 7, nb - 1);
+        const uint8_t* xl = lds + (slot0 - lds0) + (t >> 1) * 1024 + (t & 1) * 512 + 2 * (32 * par + 4 * g);
+#pragma unroll
+        for (int s2 = 0; s2 < bx::kNSB; ++s2)
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const uint2 lo = *reinterpret_cast<const uint2*>(xl + 4096 * s2 + 128 * p);
+                const uint2 hi = *reinterpret_cast<const uint2*>(xl + 4096 * s2 + 128 * p + 32);
+                xa[s2][p] = __builtin_bit_cast(half8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+            }
+        // the reads have returned before transfers overwrite the slots
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+    int issued = min(Q, NS);  // stages of weights issued
+    for (int q = 0; q < issued; ++q) issue();
+
+    // offset corrections of every block of the slice, once
+    const half8_t kneg = {static_cast<half_t>(-1032.0f), static_cast<half_t>(-1032.0f), static_cast<half_t>(-1032.0f),
+                          static_cast<half_t>(-1032.0f), static_cast<half_t>(-72.0f),   static_cast<half_t>(-72.0f),
+                          static_cast<half_t>(-72.0f),   static_cast<half_t>(-72.0f)};
+    float4_t dc[bx::kNSB][4];
+#pragma unroll
+    for (int s2 = 0; s2 < bx::kNSB; ++s2)
+#pragma unroll
+        for (int p = 0; p < 4; ++p)
+            dc[s2][p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[s2][p], kneg, float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+
+    int q = 0, cslot = 0;
+    for (int t = 0; t < T; ++t) {
+#pragma unroll
+        for (int s2 = 0; s2 < bx::kNSB; ++s2) {
+            if (s2 < nst) {
+                // stages of weights issued after stage q
+                switch (issued - 1 - q) {
+                    case 0: wait_vmcnt_asm<0>(); break;
+                    case 1: wait_vmcnt_asm<1 * NWD>(); break;
+                    case 2: wait_vmcnt_asm<2 * NWD>(); break;
+                    case 3: wait_vmcnt_asm<3 * NWD>(); break;
+                    case 4: wait_vmcnt_asm<4 * NWD>(); break;
+                    case 5: wait_vmcnt_asm<5 * NWD>(); break;
+                    case 6: wait_vmcnt_asm<6 * NWD>(); break;
+                    default: wait_vmcnt_asm<(NS - 1) * NWD>(); break;
+                }
+                const uint8_t* sl = lds + (slot0 - lds0) + cslot * bx::kSlotBytes;
+#pragma unroll
+                for (int rg = 0; rg < NRG; ++rg)
+#pragma unroll
+                    for (int p = 0; p < 4; ++p) {
+                        const uint8_t* wr = sl + 1152 * rg + 36 * p;
+                        const uint32_t d0 = *reinterpret_cast<const uint32_t*>(wr + wrd);
+                        const uint32_t d1 = *reinterpret_cast<const uint32_t*>(wr + wrd + 4);
+                        const half_t dv = __builtin_bit_cast(half_t, *reinterpret_cast<const uint16_t*>(wr + drd));
+                        const uint32_t p01 = __builtin_amdgcn_perm(d1, d0, sel01);
+                        const uint32_t p23 = __builtin_amdgcn_perm(d1, d0, sel23);
+                        const half8_t wbv = __builtin_bit_cast(
+                            half8_t, make_uint4(nu.lo_c(p01), nu.lo_c(p23), nu.hi_c(p01), nu.hi_c(p23)));
+                        const float4_t D = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[s2][p], wbv, dc[s2][p], 0, 0, 0);
+                        const float dsc = static_cast<float>(dv);
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) acc[rg][v] = __builtin_fmaf(dsc, D[v], acc[rg][v]);
+                    }
+                // every LDS read of this slot has returned before the DMA refills it
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                if (q + NS < Q) {
+                    issue();
+                    ++issued;
+                }
+                ++q;
+                if (++cslot == NS) cslot = 0;
+            }
+        }
+        finish_tile();
+    }
+}
+
+int launch_q4_xreg(const void* w, const uint16_t* x, uint16_t* y, int M, int K, int64_t batch, int64_t ldx,
+                   int64_t ldy, hipStream_t stream) {
+    constexpr size_t lds = bx::kLdsBytes;
+    const void* fn = reinterpret_cast<const void*>(&gguf_gemv_q4_xreg);
+    if (int rc = prepare_lds(fn, lds)) return rc;
+    const int tiles = (M + bx::kRT - 1) / bx::kRT;
+    const int resident = blocks_per_cu(fn, lds, bx::kWaves * 64) * cu_count();
+    if (resident < 1) return set_error(GDSLLM_ERR_UNSUPPORTED, "gguf_gemv_q4_xreg: no workgroup fits a compute unit");
+    const int grid = std::min(tiles, resident);
+    hipLaunchKernelGGL(gguf_gemv_q4_xreg, dim3(grid), dim3(bx::kWaves * 64), lds, stream,
+                       static_cast<const uint8_t*>(w), x, y, M, K, static_cast<int>(batch), ldx, ldy);
+    return check_hip(hipGetLastError(), "gguf_gemv_q4_xreg launch");
+}
+
+// Choice between the two batched Q4_0 kernels (measured on MI355X at batch 8,
+// us):              codes (32-row tiles)   x in registers (16-row tiles)
+//   28672 x 8192          40.4                    32.7
+//   11008 x 4096          13.9                    12.5
+//   16384 x 8192          22.3                    22.8
+//    8192 x 8192          13.6                    15.2
+//    4096 x 4096           7.5                     7.9
+//    1024 x 8192           8.5                     8.7
+// The x-in-registers kernel pays ~1.5 us for x before its first weights; it
+// wins where the code kernel's 32-row tiles split unevenly over the compute
+// units (896 and 344 tiles on 256) and re-read x for every extra tile.
+inline bool use_q4_xreg(int M, int K) {
+    const int t32 = (M + 31) / 32, cu = cu_count();
+    return K <= 8192 && t32 > cu && t32 % cu != 0;
+}
+
 // Row-tile height for the code kernel.  A 16-row stage moves 1.8 bytes of x
 // per weight byte (a 32-row one 0.9), which costs more than the uneven last
 // round of 32-row tiles (measured on MI355X: 28672x8192 at batch 8 40.8 us
@@ -1503,6 +1749,11 @@ int gemv(const char* name, const void* w, const void* x, void* y, int64_t out_di
     if (rc != -1) return rc == GDSLLM_OK ? ok() : rc;
     rc = GDSLLM_OK;
     const bool x_al16 = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (ldx % 8 == 0);
+    if (F == Fmt::Q4_0 && fast && batch >= 3 && x_al16 && use_q4_xreg(M, K) &&
+        2 * (7 * ldx + K) < (int64_t{1} << 31)) {
+        const int rc2 = launch_q4_xreg(w, xp, yp, M, K, batch, ldx, ldy, s);
+        return rc2 == GDSLLM_OK ? ok() : rc2;
+    }
     if (F == Fmt::Q4_0 && fast && batch >= 3 && K <= (1 << 20) && x_al16) {
         const int rc2 = q4_codes_rows(M) == 32 ? launch_q4_codes<32>(w, xp, yp, M, K, batch, ldx, ldy, s)
                                                : launch_q4_codes<16>(w, xp, yp, M, K, batch, ldx, ldy, s);

@@ -38,8 +38,14 @@ def test_gguf_gemv_b1(gpu, fmt, M, K):
 
 # K = 256 (one super-block: most waves of a batched workgroup have no stage),
 # ragged row tiles at both tile heights (8200 rows: 32-row tiles with a part
-# tile), in_dim % 256 != 0 (generic kernel)
-BATCHED_SHAPES = [(70, 4096), (33, 11008), (20, 96), (24, 8192), (9, 28672), (13003, 1024), (40, 256), (8200, 512)]
+# tile), in_dim % 256 != 0 (generic kernel); super-blocks per row not a
+# multiple of the 8 waves (5120: waves with 3 and 2, 2816: 2 and 1) and more
+# tiles than workgroups (4100 x 6144).  Rows 8200, 9000, 8300, 8500 and 13003
+# split unevenly into 32-row tiles over 256 compute units, so batch 3-8 Q4_0
+# takes the x-in-registers kernel there (with part tiles, 1 super-block per
+# row, and 20 / 11 super-blocks over 8 waves)
+BATCHED_SHAPES = [(70, 4096), (33, 11008), (20, 96), (24, 8192), (9, 28672), (13003, 1024), (40, 256), (8200, 512),
+                  (50, 5120), (1000, 2816), (4100, 6144), (9000, 5120), (8300, 256), (8500, 2816)]
 
 
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])

@@ -23,6 +23,8 @@
 // selected expert into LDS and computes each output row as the weighted sum
 // over experts of the down-projection rows.
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace gdsllm {
@@ -507,32 +509,47 @@ __device__ __forceinline__ int reduce4_index(int lane) {
 // the same FFN row adjacent: virtual row v -> slot k = v / (2F), FFN row
 // n = (v % 2F) / 2, projection v & 1 (0 = gate, 1 = up).  Outputs: g/u fp16
 // [top_k][2][F], and h = fp16(fp16(silu(g)) * u) fp16 [top_k][F].
-struct GateUpPairs {
+// The shared expert of the fused decode step (one-expert descriptors) fills
+// slot shared_slot, after the routed slots.
+struct SharedSlot {
+    gdsllm_affine_experts sgate, sup;
+    int shared_slot;
+};
+struct NoSharedSlot {};
+
+template <bool SH>
+struct GateUpPairsT : std::conditional_t<SH, SharedSlot, NoSharedSlot> {
     gdsllm_affine_experts gate, up;
     const int32_t* idx;
     uint16_t* gu;
     uint16_t* h;
     int F;
     int M;
-    // Optional shared expert (one-expert descriptors) in slot shared_slot,
-    // after the routed slots; -1 when absent.
-    gdsllm_affine_experts sgate, sup;
-    int shared_slot = -1;
     // Lane l holds idx[l] (the slot count is at most 64), read once per wave;
     // the shared slot reads expert 0 of its own descriptors.
     __device__ int lane_index(int lane) const {
-        if (lane == shared_slot) return 0;
+        if constexpr (SH)
+            if (lane == this->shared_slot) return 0;
         return lane < M / (2 * F) ? idx[lane] : -1;
+    }
+    __device__ const gdsllm_affine_experts& proj(int k, bool is_up) const {
+        if constexpr (SH)
+            if (k == this->shared_slot) return is_up ? this->sup : this->sgate;
+        return is_up ? up : gate;
     }
     // v is the same for the whole wave (one row per load group), so the
     // expert index is a lane read, not a dependent global load.
     __device__ bool locate(int v, const uint32_t*& w, const uint16_t*& s, const uint16_t*& b, int K, int gpr,
                            int lane_idx) const {
-        const int k = v / (2 * F);
-        const int rem = v - k * 2 * F;
+        // v, and so the slot and projection, are wave-uniform: said outright,
+        // the descriptor is chosen in scalar registers (computed per lane, the
+        // shared variant read it with a vector load whose wait drained every
+        // weight load in flight)
+        const int vu = __builtin_amdgcn_readfirstlane(v);
+        const int k = vu / (2 * F);
+        const int rem = vu - k * 2 * F;
         const int n = rem >> 1;
-        const bool sh = k == shared_slot;
-        const gdsllm_affine_experts& p = (rem & 1) ? (sh ? sup : up) : (sh ? sgate : gate);
+        const gdsllm_affine_experts& p = proj(k, rem & 1);
         const int e = __builtin_amdgcn_readlane(lane_idx, k);
         if (e < 0 || e >= p.num_experts) return false;
         w = reinterpret_cast<const uint32_t*>(static_cast<const char*>(p.weight) + e * p.weight_stride) +
@@ -549,9 +566,11 @@ struct GateUpPairs {
         gu[(2 * k + (rem & 1)) * F + (rem >> 1)] = f2h_bits(val);
     }
 };
+using GateUpPairs = GateUpPairsT<false>;
+using GateUpPairsShared = GateUpPairsT<true>;
 
 template <class Rows> struct IsGateUp { static constexpr bool value = false; };
-template <> struct IsGateUp<GateUpPairs> { static constexpr bool value = true; };
+template <bool SH> struct IsGateUp<GateUpPairsT<SH>> { static constexpr bool value = true; };
 
 template <int LR, int CPL, int NB, class Rows>
 __global__ __launch_bounds__(kThreads) void affine_rows(Rows rows, const uint16_t* __restrict__ X, int K, int gsize,
@@ -677,12 +696,15 @@ __global__ __launch_bounds__(kThreads) void affine_rows(Rows rows, const uint16_
 // the shared down row separately, and the row's writer applies
 // y = clamp(fp16(routed) + fp16(fp16(sigmoid(g)) * fp16(shared))) with the
 // rounding of moe_combine (torch's fp16 elementwise ops, qwen_moe.py:508-513).
-template <int LR, int SLOTS, int NT>
+template <int LR, int SLOTS, int NT, bool SH>
 __global__ __launch_bounds__(NT) void moe_down_rows(gdsllm_affine_experts down, const int32_t* __restrict__ idx,
                                                           const uint16_t* __restrict__ rw,
                                                           const uint16_t* __restrict__ hbuf, int top_k,
                                                           uint16_t* __restrict__ Y, gdsllm_affine_experts sdown,
-                                                          const uint16_t* __restrict__ gl, int nsh) {
+                                                          const uint16_t* __restrict__ gl) {
+    // SH: a separate instantiation, so the gather without a shared expert
+    // keeps its registers (the extra accumulator made it spill)
+    constexpr int nsh = SH ? 1 : 0;
     constexpr int EPI = 64 / LR;
     constexpr int R = SLOTS <= 4 ? 2 : 1;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -734,7 +756,7 @@ __global__ __launch_bounds__(NT) void moe_down_rows(gdsllm_affine_experts down, 
     for (int i = 0; i < SLOTS; ++i) {
         const int k = i * EPI + sub;
         const int e = eraw[i];
-        shs[i] = nsh && k == top_k;
+        shs[i] = SH && k == top_k;
         const gdsllm_affine_experts& p = shs[i] ? sdown : down;
         const bool valid = e >= 0 && e < p.num_experts;
         kk[i] = valid ? k : -1;
@@ -827,7 +849,7 @@ __global__ __launch_bounds__(NT) void moe_down_rows(gdsllm_affine_experts down, 
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
                     const float d = chunk_dot_p(cw[r][i], p, cs2.x, cs2.y, h2f(cs[r][i]), h2f(cb[r][i]), nu);
-                    if (shs[i])
+                    if (SH && shs[i])
                         accs[r] += d;
                     else
                         acc[r] = __builtin_fmaf(wk[i], d, acc[r]);
@@ -848,7 +870,7 @@ __global__ __launch_bounds__(NT) void moe_down_rows(gdsllm_affine_experts down, 
         const float v = lanes64(acc);
         const int o = st * R + (R == 2 ? (lane >> 5) : 0);
         const bool writer = (lane & 31) == 0 && (R == 2 || lane == 0) && o < H;
-        if (nsh) {
+        if constexpr (SH) {
             const float vs = lanes64(accs);
             if (writer) {
                 const float g = h2f(graw);
@@ -914,18 +936,27 @@ template <int LR, int SLOTS>
 int launch_moe_down(const gdsllm_affine_experts& down, const int32_t* idx, const uint16_t* rw, const uint16_t* h,
                     int top_k, uint16_t* y, hipStream_t stream, const gdsllm_affine_experts* sdown = nullptr,
                     const uint16_t* gl = nullptr) {
+    // 5 slots fit 1024 threads (128 registers) only without the shared
+    // expert's accumulator
     constexpr int NT = (SLOTS <= 3 || SLOTS == 5) ? 1024 : 512;
-    const void* fn = reinterpret_cast<const void*>(&moe_down_rows<LR, SLOTS, NT>);
+    constexpr int NTS = SLOTS <= 3 ? 1024 : 512;
+    const void* fn = sdown ? reinterpret_cast<const void*>(&moe_down_rows<LR, SLOTS, NTS, true>)
+                           : reinterpret_cast<const void*>(&moe_down_rows<LR, SLOTS, NT, false>);
     const int nsh = sdown ? 1 : 0;
+    const int nt = sdown ? NTS : NT;
     const size_t lds = static_cast<size_t>(top_k + nsh) * (down.in_dim / 32) * kRec;
     if (int rc = prepare_lds(fn, lds)) return rc;
     constexpr int R = SLOTS <= 4 ? 2 : 1;
     const int stages = static_cast<int>((down.out_dim + R - 1) / R);
-    const int need = (stages + NT / 64 - 1) / (NT / 64);
-    const int cap = blocks_per_cu(fn, lds, NT) * cu_count();
+    const int need = (stages + nt / 64 - 1) / (nt / 64);
+    const int cap = blocks_per_cu(fn, lds, nt) * cu_count();
     const int grid = need < cap ? need : cap;
-    hipLaunchKernelGGL((moe_down_rows<LR, SLOTS, NT>), dim3(grid), dim3(NT), lds, stream, down, idx, rw, h, top_k, y,
-                       sdown ? *sdown : down, gl, nsh);
+    if (sdown)
+        hipLaunchKernelGGL((moe_down_rows<LR, SLOTS, NTS, true>), dim3(grid), dim3(NTS), lds, stream, down, idx, rw,
+                           h, top_k, y, *sdown, gl);
+    else
+        hipLaunchKernelGGL((moe_down_rows<LR, SLOTS, NT, false>), dim3(grid), dim3(NT), lds, stream, down, idx, rw, h,
+                           top_k, y, down, gl);
     return check_hip(hipGetLastError(), "moe_down_rows launch");
 }
 
@@ -1090,7 +1121,7 @@ extern "C" int gdsllm_moe_gather_affine_q4(const gdsllm_affine_experts* gate, co
                            slots <= 8 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
     if (rows_path) {
         uint16_t* h = gu + top_k * 2 * F;
-        GateUpPairs pairs{*gate, *up, idx, gu, h, static_cast<int>(F), static_cast<int>(2 * top_k * F)};
+        GateUpPairs pairs{{}, *gate, *up, idx, gu, h, static_cast<int>(F), static_cast<int>(2 * top_k * F)};
         int rc;
         switch (cpr_h / 64) {
             case 1: rc = launch_affine_rows<64, 1, 1>(pairs, xp, static_cast<int>(H), static_cast<int>(gate->group_size), H, s); break;
@@ -1188,7 +1219,14 @@ extern "C" int gdsllm_moe_step_affine_q4(const gdsllm_affine_experts* gate, cons
     hipStream_t s = as_stream(stream);
     auto* gu = static_cast<uint16_t*>(workspace);
     uint16_t* h = gu + static_cast<int64_t>(nslot) * 2 * F;  // after the gate/up outputs of every slot
-    GateUpPairs pairs{*gate, *up, idx, gu, h, static_cast<int>(F), static_cast<int>(2 * nslot * F)};
+    GateUpPairsShared pairs{};
+    pairs.gate = *gate;
+    pairs.up = *up;
+    pairs.idx = idx;
+    pairs.gu = gu;
+    pairs.h = h;
+    pairs.F = static_cast<int>(F);
+    pairs.M = static_cast<int>(2 * nslot * F);
     pairs.sgate = *shared_gate;
     pairs.sup = *shared_up;
     pairs.shared_slot = static_cast<int>(top_k);

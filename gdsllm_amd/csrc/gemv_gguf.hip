@@ -1760,11 +1760,8 @@ int gemv(const char* name, const void* w, const void* x, void* y, int64_t out_di
         return rc2 == GDSLLM_OK ? ok() : rc2;
     }
     if (fast && batch >= 3 && K <= (1 << 20) && x_al16) {
-        // Q4_0: two row tiles per workgroup while that still gives every CU
-        // one; Q8_0 stages are twice as large and take one tile
-        const int rc2 = F == Fmt::Q4_0 && (M + 31) / 32 >= cu_count()
-                            ? launch_mfma<F, 2>(w, xp, yp, M, K, batch, ldx, ldy, s)
-                            : launch_mfma<F, 1>(w, xp, yp, M, K, batch, ldx, ldy, s);
+        // Q8_0 (Q4_0 took the code kernels above)
+        const int rc2 = launch_mfma<F, 1>(w, xp, yp, M, K, batch, ldx, ldy, s);
         return rc2 == GDSLLM_OK ? ok() : rc2;
     }
     if (fast) {

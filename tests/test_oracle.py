@@ -396,6 +396,25 @@ def test_moe_combine_closed_forms():
     assert list(r[0]) == [np.float16(3.0), np.float16(1024.0)]
 
 
+def test_silu_fp16_against_torch_over_every_fp16():
+    """silu_fp16 (the fp16 F.silu step of qwen_moe.py:471) against torch's own
+    CPU F.silu on all 65,536 fp16 inputs: bit-equal except 3 inputs at one ulp
+    (torch's vectorized exp rounds differently there); +-inf and NaN behave
+    alike.  A planted mistake (sigmoid without the factor x) fails."""
+    torch = pytest.importorskip("torch")
+    allh = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16)
+    with np.errstate(all="ignore"):
+        got = oq.silu_fp16(allh)
+        bad = (np.float32(1.0) / (np.float32(1.0) + np.exp(-allh.astype(np.float32)))).astype(np.float16)
+    want = torch.nn.functional.silu(torch.from_numpy(allh.copy())).numpy()
+    same = (got.view(np.uint16) == want.view(np.uint16)) | (np.isnan(got) & np.isnan(want))
+    assert (~same).sum() <= 3
+    diff = np.abs(got[~same].astype(np.float64) - want[~same].astype(np.float64))
+    assert np.all(diff <= oq.fp16_ulp(want[~same].astype(np.float64)))
+    planted = (bad.view(np.uint16) == want.view(np.uint16)) | (np.isnan(bad) & np.isnan(want))
+    assert (~planted).sum() > 10000
+
+
 # ------------------------------------------------------- per-column int8 weights
 
 

@@ -368,8 +368,8 @@ def bench_moe(dev, calls: int = 64, reps: int = 20):
 
     ms2 = _replay_ms(step, reps) / calls
 
-    # The same step with the shared expert and the combine fused into the
-    # gather's two launches (gdsllm_moe_step_affine_q4): 5 launches.
+    # The same step with the shared expert, its gate and the combine fused
+    # into the gather's two launches (gdsllm_moe_step_affine_q4): 4 launches.
     def one_expert(e, i):
         w, sc, bi = (t[i] for t in shared[e])
         n, kw = w.shape
@@ -378,7 +378,7 @@ def bench_moe(dev, calls: int = 64, reps: int = 20):
                              n * (kk // g) * 2, 1, n, kk, g)
 
     sh_one = [[one_expert(e, i) for e in range(3)] for i in range(calls)]
-    wsf_bytes = capi().gdsllm_moe_gather_workspace_size(k + 1, Fd)
+    wsf_bytes = capi().gdsllm_moe_step_workspace_size(k, Fd)
     wsf = torch.empty(wsf_bytes, dtype=torch.uint8, device=dev)
     yf = torch.empty(calls, H, dtype=torch.float16, device=dev)
 
@@ -389,11 +389,10 @@ def bench_moe(dev, calls: int = 64, reps: int = 20):
             check(capi().gdsllm_gemv_f16(router[i].data_ptr(), xi, logits[i].data_ptr(), E, H, 1, H, E, s))
             check(capi().gdsllm_moe_route_topk(logits[i].data_ptr(), E, 1, E, k, ridx[i].data_ptr(),
                                                rw[i].data_ptr(), s))
-            check(capi().gdsllm_gemv_f16(sgate[i].data_ptr(), xi, gl[i].data_ptr(), 1, H, 1, H, 1, s))
             sg_, su_, sd_ = sh_one[i]
             check(capi().gdsllm_moe_step_affine_q4(ctypes.byref(gate), ctypes.byref(up), ctypes.byref(down),
                                                    ctypes.byref(sg_), ctypes.byref(su_), ctypes.byref(sd_), xi,
-                                                   ridx[i].data_ptr(), rw[i].data_ptr(), k, gl[i].data_ptr(),
+                                                   ridx[i].data_ptr(), rw[i].data_ptr(), k, sgate[i].data_ptr(),
                                                    yf[i].data_ptr(), wsf.data_ptr(), wsf_bytes, s))
 
     ms3 = _replay_ms(step_fused, reps) / calls
@@ -404,7 +403,7 @@ def bench_moe(dev, calls: int = 64, reps: int = 20):
     out["decode_step"] = {
         "us_per_token_layer": round(ms3 * 1e3, 3), "bytes_per_token_layer": nbytes2,
         "GB_s": round(nbytes2 / (ms3 * 1e-3) / 1e9, 1), "pct_of_hbm_peak": round(nbytes2 / (ms3 * 1e-3) / 1e9 / 80, 1),
-        "launches": 5, "host_syncs": 0, "includes": includes,
+        "launches": 4, "host_syncs": 0, "includes": includes,
         "separate_launches": {"us_per_token_layer": round(ms2 * 1e3, 3), "launches": 8},
         "bit_identical_to_separate": bool(torch.equal(yf.view(torch.int16), yy.view(torch.int16)))}
     return out

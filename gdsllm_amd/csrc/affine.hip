@@ -514,6 +514,8 @@ __device__ __forceinline__ int reduce4_index(int lane) {
 struct SharedSlot {
     gdsllm_affine_experts sgate, sup;
     int shared_slot;
+    const uint16_t* gate_w;  // fp16 [K] shared-expert gate row
+    uint16_t* logit;         // fp16 out: its logit on x
 };
 struct NoSharedSlot {};
 
@@ -586,6 +588,14 @@ __global__ __launch_bounds__(kThreads) void affine_rows(Rows rows, const uint16_
     const int TW = gridDim.x * kWaves;
     const int gw = blockIdx.x * kWaves + (threadIdx.x >> 6);
     const int T = gw < stages ? (stages - 1 - gw) / TW + 1 : 0;
+    if constexpr (std::is_same_v<Rows, GateUpPairsT<true>>) {
+        // the shared-expert gate logit, by the grid's last wave (it has the
+        // fewest stages), as gdsllm_gemv_f16 would compute it
+        if (gw == TW - 1) {
+            const float g = f16_row_dot(rows.gate_w, X, K, lane);
+            if (lane == 0) *rows.logit = f2h_bits(g);
+        }
+    }
     if (T == 0) return;
     const NibUnpack nu;
 
@@ -1053,6 +1063,10 @@ extern "C" size_t gdsllm_moe_gather_workspace_size(int64_t top_k, int64_t ffn_di
     return (bytes + 255) / 256 * 256;
 }
 
+extern "C" size_t gdsllm_moe_step_workspace_size(int64_t top_k, int64_t ffn_dim) {
+    return gdsllm_moe_gather_workspace_size(top_k + 1, ffn_dim) + 256;  // + the shared-gate logit
+}
+
 static int check_experts(const gdsllm_affine_experts* p, const char* what, std::string& err) {
     if (!p) { err = std::string(what) + " is null"; return 1; }
     if (!p->weight || !p->scales || !p->biases) { err = std::string(what) + ": null pointer"; return 1; }
@@ -1174,7 +1188,7 @@ extern "C" int gdsllm_moe_step_affine_q4(const gdsllm_affine_experts* gate, cons
                                          const gdsllm_affine_experts* down, const gdsllm_affine_experts* shared_gate,
                                          const gdsllm_affine_experts* shared_up,
                                          const gdsllm_affine_experts* shared_down, const void* x, const int32_t* idx,
-                                         const void* routing_weights, int64_t top_k, const void* shared_gate_logit,
+                                         const void* routing_weights, int64_t top_k, const void* shared_gate_weight,
                                          void* y, void* workspace, size_t workspace_bytes, void* stream) {
     const std::string n = "moe_step_affine_q4";
     std::string err;
@@ -1192,16 +1206,16 @@ extern "C" int gdsllm_moe_step_affine_q4(const gdsllm_affine_experts* gate, cons
     if (shared_gate->in_dim != H || shared_up->in_dim != H || shared_down->out_dim != H ||
         shared_gate->out_dim != shared_up->out_dim || shared_down->in_dim != shared_gate->out_dim)
         return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": shared expert shapes disagree with hidden size");
-    if (!x || !idx || !routing_weights || !shared_gate_logit || !y || !workspace)
+    if (!x || !idx || !routing_weights || !shared_gate_weight || !y || !workspace)
         return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": null pointer");
     if (reinterpret_cast<uintptr_t>(x) % 2 || reinterpret_cast<uintptr_t>(y) % 2 ||
-        reinterpret_cast<uintptr_t>(routing_weights) % 2 || reinterpret_cast<uintptr_t>(shared_gate_logit) % 2 ||
+        reinterpret_cast<uintptr_t>(routing_weights) % 2 || reinterpret_cast<uintptr_t>(shared_gate_weight) % 2 ||
         reinterpret_cast<uintptr_t>(idx) % 4 || reinterpret_cast<uintptr_t>(workspace) % 16)
         return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": misaligned pointer");
-    if (workspace_bytes < gdsllm_moe_gather_workspace_size(top_k + 1, F))
+    if (workspace_bytes < gdsllm_moe_step_workspace_size(top_k, F))
         return set_error(GDSLLM_ERR_INVALID_ARGUMENT,
                          n + ": workspace too small (" + std::to_string(workspace_bytes) + " < " +
-                             std::to_string(gdsllm_moe_gather_workspace_size(top_k + 1, F)) + ")");
+                             std::to_string(gdsllm_moe_step_workspace_size(top_k, F)) + ")");
     // The fused step serves the row-span shapes with a shared expert of the
     // routed experts' width and grouping; anything else is the caller's
     // separate gather + shared expert + combine.
@@ -1209,7 +1223,8 @@ extern "C" int gdsllm_moe_step_affine_q4(const gdsllm_affine_experts* gate, cons
     const int nslot = static_cast<int>(top_k) + 1;
     const int slots = (cpr_f >= 16 && cpr_f <= 64) ? (nslot + 64 / cpr_f - 1) / (64 / cpr_f) : 0;
     const bool rows_path = H % 2048 == 0 && H <= 8192 && (cpr_f == 16 || cpr_f == 32 || cpr_f == 64) && slots >= 1 &&
-                           slots <= 8 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
+                           slots <= 8 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                           reinterpret_cast<uintptr_t>(shared_gate_weight) % 16 == 0;
     if (!rows_path || shared_gate->out_dim != F || shared_gate->group_size != gate->group_size ||
         shared_up->group_size != gate->group_size || shared_down->group_size != down->group_size)
         return set_error(GDSLLM_ERR_UNSUPPORTED, n + ": shape outside the fused step (use the separate launches)");
@@ -1230,6 +1245,11 @@ extern "C" int gdsllm_moe_step_affine_q4(const gdsllm_affine_experts* gate, cons
     pairs.sgate = *shared_gate;
     pairs.sup = *shared_up;
     pairs.shared_slot = static_cast<int>(top_k);
+    // the logit sits after the gather's workspace
+    auto* glw = reinterpret_cast<uint16_t*>(static_cast<uint8_t*>(workspace) +
+                                            gdsllm_moe_gather_workspace_size(top_k + 1, F));
+    pairs.gate_w = static_cast<const uint16_t*>(shared_gate_weight);
+    pairs.logit = glw;
     const auto* xp = static_cast<const uint16_t*>(x);
     const int gs = static_cast<int>(gate->group_size);
     int rc;
@@ -1241,7 +1261,7 @@ extern "C" int gdsllm_moe_step_affine_q4(const gdsllm_affine_experts* gate, cons
     }
     if (rc) return rc;
     const auto* wp = static_cast<const uint16_t*>(routing_weights);
-    const auto* gl = static_cast<const uint16_t*>(shared_gate_logit);
+    const uint16_t* gl = glw;
     auto* yp = static_cast<uint16_t*>(y);
     const int tk = static_cast<int>(top_k);
     switch (cpr_f) {

@@ -171,6 +171,24 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// One fp16 row dot x (both 16-byte aligned, K % 8 == 0) by one wave, summed
+// in the order of gemv_f16's vector path: lane l takes 8 weights of every
+// 512-column chunk, chunks in order, v_dot2 into fp32, then a wave sum.  The
+// same inputs give the same bits as gdsllm_gemv_f16.
+__device__ __forceinline__ float f16_row_dot(const uint16_t* __restrict__ w, const uint16_t* __restrict__ x, int K,
+                                             int lane) {
+    float acc = 0.f;
+    for (int c = 8 * lane; c < K; c += 512) {
+        const uint4 wv = *reinterpret_cast<const uint4*>(w + c);
+        const uint4 xv = *reinterpret_cast<const uint4*>(x + c);
+        acc = dot2(wv.x, xv.x, acc);
+        acc = dot2(wv.y, xv.y, acc);
+        acc = dot2(wv.z, xv.z, acc);
+        acc = dot2(wv.w, xv.w, acc);
+    }
+    return group_sum<64>(acc);
+}
+
 // 16 bytes per lane from global memory straight into LDS (global_load_lds_dwordx4,
 // non-temporal): lane l's bytes land at lds + 16*l.  `lds` must be the same for
 // every lane of the wave (it goes to M0).  The transfer is tracked by vmcnt

@@ -437,12 +437,14 @@ gdsllm_affine_experts experts_of(const AffineEntry& a, const char* where) {
     return experts_of(std::get<0>(a), shape, std::get<2>(a), std::get<3>(a), std::get<4>(a), std::get<5>(a), where);
 }
 
-// Decode MoE MLP after routing with the shared expert and the combine fused:
-// entries = (gate, up, down, shared_gate, shared_up, shared_down); returns
-// [1, hidden] = clamp(routed + fp16(sigmoid(g)) * shared), or None for shapes
-// outside the fused kernels.
-std::optional<torch::Tensor> moe_step_affine_q4(torch::Tensor x, std::vector<AffineEntry> entries, torch::Tensor top_k_indices,
-                                 torch::Tensor top_k_weights, torch::Tensor shared_gate_logit) {
+// Decode MoE MLP after routing with the shared expert, its gate and the
+// combine fused: entries = (gate, up, down, shared_gate, shared_up,
+// shared_down), shared_gate_weight fp16 [1, hidden]; returns [1, hidden] =
+// clamp(routed + fp16(sigmoid(g)) * shared), or None for shapes outside the
+// fused kernels.
+std::optional<torch::Tensor> moe_step_affine_q4(torch::Tensor x, std::vector<AffineEntry> entries,
+                                                torch::Tensor top_k_indices, torch::Tensor top_k_weights,
+                                                torch::Tensor shared_gate_weight) {
     const char* where = "moe_step_affine_q4";
     if (entries.size() != 6)
         throw std::runtime_error(std::string(where) + ": expects gate, up, down, shared gate, shared up, shared down");
@@ -454,17 +456,19 @@ std::optional<torch::Tensor> moe_step_affine_q4(torch::Tensor x, std::vector<Aff
     if (xf.numel() != e[0].in_dim)
         throw std::runtime_error(std::string(where) + ": input size " + std::to_string(xf.numel()) +
                                  " != hidden " + std::to_string(e[0].in_dim));
+    torch::Tensor sg = shared_gate_weight.contiguous();
+    check_x(sg, dev, where);
+    if (sg.numel() != e[0].in_dim)
+        throw std::runtime_error(std::string(where) + ": shared gate weight must hold hidden values");
     torch::Tensor idx = top_k_indices.reshape({-1}).to(torch::TensorOptions().dtype(torch::kInt32).device(torch::kCUDA, dev)).contiguous();
     torch::Tensor wts = top_k_weights.reshape({-1}).to(torch::TensorOptions().dtype(torch::kFloat16).device(torch::kCUDA, dev)).contiguous();
-    torch::Tensor gl = shared_gate_logit.reshape({-1}).to(torch::TensorOptions().dtype(torch::kFloat16).device(torch::kCUDA, dev)).contiguous();
     const int64_t k = idx.numel();
     if (wts.numel() != k) throw std::runtime_error(std::string(where) + ": indices and weights differ in length");
-    if (gl.numel() != 1) throw std::runtime_error(std::string(where) + ": one shared-gate logit per token");
-    const size_t ws_bytes = gdsllm_moe_gather_workspace_size(k + 1, e[0].out_dim);
+    const size_t ws_bytes = gdsllm_moe_step_workspace_size(k, e[0].out_dim);
     torch::Tensor ws = torch::empty({static_cast<int64_t>(ws_bytes)}, torch::TensorOptions().dtype(torch::kUInt8).device(torch::kCUDA, dev));
     torch::Tensor out = torch::empty({1, e[2].out_dim}, fp16_on(dev));
     const int rc = gdsllm_moe_step_affine_q4(&e[0], &e[1], &e[2], &e[3], &e[4], &e[5], xf.data_ptr(),
-                                             idx.data_ptr<int32_t>(), wts.data_ptr(), k, gl.data_ptr(), out.data_ptr(),
+                                             idx.data_ptr<int32_t>(), wts.data_ptr(), k, sg.data_ptr(), out.data_ptr(),
                                              ws.data_ptr(), ws_bytes, stream_of(dev));
     if (rc == GDSLLM_ERR_UNSUPPORTED) return std::nullopt;  // the caller runs the separate launches
     check(rc, where);
@@ -681,7 +685,7 @@ PYBIND11_MODULE(gds_io_ext, m) {
     m.def("moe_step_affine_q4", &moe_step_affine_q4,
           "Decode MoE MLP after routing (top-k experts, shared expert, sigmoid-gated combine) in two launches.",
           py::arg("x"), py::arg("entries"), py::arg("top_k_indices"), py::arg("top_k_weights"),
-          py::arg("shared_gate_logit"));
+          py::arg("shared_gate_weight"));
     m.def("fused_dequant_gemm", &fused_dequant_gemm, "Prefill Q4_0 dequant-GEMM on MFMA: x [T, K] -> [T, M].",
           py::arg("handle"), py::arg("x"), py::arg("weight_shape"), py::arg("gguf_type"), py::arg("offset"));
     m.def("gemv_f16", &gemv_f16, "fp16-weight GEMV (router, shared-expert gate): x [..., K] -> [..., M].",

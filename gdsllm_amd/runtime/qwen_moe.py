@@ -108,10 +108,10 @@ def _entry(m: dict) -> tuple:
 
 
 def moe_step(x: torch.Tensor, weights: Dict, top_k_indices: torch.Tensor, top_k_weights: torch.Tensor):
-    """The decode MoE MLP of runtime/qwen_moe.py:455-513 for one token in three
-    launches: the fp16 shared-expert-gate GEMV, then one launch for the gate/up
-    rows of the top-k experts and the shared expert, and one for their down
-    rows with the sigmoid-gated combine and clamp.  Returns (1, 1, hidden), or
+    """The decode MoE MLP of runtime/qwen_moe.py:455-513 for one token in two
+    launches: one for the gate/up rows of the top-k experts and the shared
+    expert (and the fp16 shared-expert gate logit), one for their down rows
+    with the sigmoid-gated combine and clamp.  Returns (1, 1, hidden), or
     None when the layer has no affine_q4 shared expert with an fp16 gate or its
     shapes are outside the fused kernels (the caller then runs the separate
     launches)."""
@@ -120,10 +120,9 @@ def moe_step(x: torch.Tensor, weights: Dict, top_k_indices: torch.Tensor, top_k_
     if any(not isinstance(m, dict) for m in shared) or not isinstance(sg, torch.Tensor):
         return None
     routed = [weights[f"{p}.weight"] for p in _EXPERT_PROJ]
-    gate_logit = ext().gemv_f16(sg, x)
     out = ext().moe_step_affine_q4(
         x.reshape(-1), [_entry(m) for m in routed + shared],
-        top_k_indices.reshape(-1), top_k_weights.reshape(-1), gate_logit.reshape(-1),
+        top_k_indices.reshape(-1), top_k_weights.reshape(-1), sg.reshape(-1),
     )
     return None if out is None else out.view(1, 1, -1)
 

@@ -201,20 +201,22 @@ int gdsllm_moe_gather_affine_q4(const gdsllm_affine_experts* gate,
 /* The whole decode MoE MLP of qwen_moe.py:455-513 after routing, in two
  * launches: the top_k routed experts and the shared expert (one-expert
  * descriptors shared_gate/shared_up [1][F][H], shared_down [1][H][F]) share
- * the gate/up launch, and the down launch also applies the shared expert and
- * the combine: y = clamp(fp16(sum_k w_k * down_k(h_k)) +
- * fp16(fp16(sigmoid(g)) * fp16(shared_down(h_s))), +-65504) with g the fp16
- * shared-gate logit (from gdsllm_gemv_f16), the rounding of
+ * the gate/up launch, which also computes the shared-expert gate logit
+ * g = fp16(shared_gate_weight . x) (fp16 [H], the bits gdsllm_gemv_f16 gives);
+ * the down launch applies the shared expert and the combine:
+ * y = clamp(fp16(sum_k w_k * down_k(h_k)) +
+ * fp16(fp16(sigmoid(g)) * fp16(shared_down(h_s))), +-65504), the rounding of
  * gdsllm_moe_combine.  No counterpart in the reference, which issues ~40
  * launches for it.  Needs the row-span shapes of gdsllm_moe_gather_affine_q4
- * with top_k + 1 slots and a shared expert of the routed width and grouping
- * (else GDSLLM_ERR_UNSUPPORTED); workspace_bytes >=
- * gdsllm_moe_gather_workspace_size(top_k + 1, F).                            */
+ * with top_k + 1 slots, a shared expert of the routed width and grouping, and
+ * x and shared_gate_weight on the 16-byte grid (else GDSLLM_ERR_UNSUPPORTED);
+ * workspace_bytes >= gdsllm_moe_step_workspace_size(top_k, F).              */
+size_t gdsllm_moe_step_workspace_size(int64_t top_k, int64_t ffn_dim);
 int gdsllm_moe_step_affine_q4(const gdsllm_affine_experts* gate, const gdsllm_affine_experts* up,
                               const gdsllm_affine_experts* down, const gdsllm_affine_experts* shared_gate,
                               const gdsllm_affine_experts* shared_up, const gdsllm_affine_experts* shared_down,
                               const void* x, const int32_t* idx, const void* routing_weights, int64_t top_k,
-                              const void* shared_gate_logit, void* y, void* workspace, size_t workspace_bytes,
+                              const void* shared_gate_weight, void* y, void* workspace, size_t workspace_bytes,
                               void* stream);
 
 /* --------------------------------------- on-device MoE routing, epilogue --

@@ -160,26 +160,28 @@ def test_moe_step_validation():
     H, F = 2048, 512
     gate, up, down = _experts(N=F, K=H), _experts(N=F, K=H), _experts(N=H, K=F)
     sg, su, sd = _experts(E=1, N=F, K=H), _experts(E=1, N=F, K=H), _experts(E=1, N=H, K=F)
-    ws = lib.gdsllm_moe_gather_workspace_size(5, F)
+    ws = lib.gdsllm_moe_step_workspace_size(4, F)
+    assert ws >= lib.gdsllm_moe_gather_workspace_size(5, F) + 2
 
-    def call(g=gate, u=up, d=down, a=sg, b=su, c=sd, k=4, wsb=ws, gl=16, x=16):
-        return lib.gdsllm_moe_step_affine_q4(*(ctypes.byref(e) for e in (g, u, d, a, b, c)), x, 16, 16, k, gl, 16,
+    def call(g=gate, u=up, d=down, a=sg, b=su, c=sd, k=4, wsb=ws, sgw=16, x=16):
+        return lib.gdsllm_moe_step_affine_q4(*(ctypes.byref(e) for e in (g, u, d, a, b, c)), x, 16, 16, k, sgw, 16,
                                              16, wsb, None)
 
     assert call(k=0) == 1 and "top_k" in _err()
     assert call(k=64) == 1
-    assert call(wsb=lib.gdsllm_moe_gather_workspace_size(4, F)) == 1 and "workspace" in _err()
+    assert call(wsb=lib.gdsllm_moe_gather_workspace_size(5, F)) == 1 and "workspace" in _err()
     assert call(d=_experts(N=F, K=H)) == 1 and "disagree" in _err()
     assert call(c=_experts(E=1, N=1024, K=F)) == 1 and "shared" in _err()
-    assert call(gl=None) == 1 and "null" in _err()
-    assert call(gl=17) == 1 and "misaligned" in _err()
+    assert call(sgw=None) == 1 and "null" in _err()
+    assert call(sgw=17) == 1 and "misaligned" in _err()
     assert call(x=8) == 2  # x off the 16-byte grid: separate launches
+    assert call(sgw=8) == 2  # gate row off the 16-byte grid
     small = dict(g=_experts(N=F, K=1024), u=_experts(N=F, K=1024), d=_experts(N=1024, K=F),
                  a=_experts(E=1, N=F, K=1024), b=_experts(E=1, N=F, K=1024), c=_experts(E=1, N=1024, K=F))
     assert call(**small) == 2 and "separate" in _err()  # hidden not a multiple of 2048
     wide = dict(a=_experts(E=1, N=1024, K=H), b=_experts(E=1, N=1024, K=H), c=_experts(E=1, N=H, K=1024))
     assert call(**wide) == 2  # shared width differs from the routed width
-    assert call(k=32, wsb=lib.gdsllm_moe_gather_workspace_size(33, F)) == 2  # 33 slots, 4 per lane group: > 8
+    assert call(k=32, wsb=lib.gdsllm_moe_step_workspace_size(32, F)) == 2  # 33 slots, 4 per lane group: > 8
 
 
 @pytest.mark.parametrize("name", ["gdsllm_embed_q4_0", "gdsllm_embed_q8_0"])
@@ -249,7 +251,7 @@ def test_extension_module_surface():
         "embed_gguf": ["handle", "token_ids", "shape", "gguf_type", "offset"],
         "dequant_int8": ["weight", "scale", "output"],
         "int8_linear": ["weight", "scale", "x"],
-        "moe_step_affine_q4": ["x", "entries", "top_k_indices", "top_k_weights", "shared_gate_logit"],
+        "moe_step_affine_q4": ["x", "entries", "top_k_indices", "top_k_weights", "shared_gate_weight"],
     }
     for name, args in expected.items():
         fn = getattr(m, name)

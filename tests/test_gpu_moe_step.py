@@ -1,11 +1,13 @@
-"""The fused decode MoE step (gdsllm_moe_step_affine_q4): routed top-k experts
-and the shared expert in one gate/up launch, their down rows with the
-sigmoid-gated combine in one more (runtime/qwen_moe.py:455-513 after routing).
+"""The fused decode MoE step (gdsllm_moe_step_affine_q4): routed top-k experts,
+the shared expert and its fp16 gate logit in one gate/up launch, their down
+rows with the sigmoid-gated combine in one more (runtime/qwen_moe.py:455-513
+after routing).
 
 Its output is bit-identical to the separate launches it replaces (the top-k
-gather, a one-expert gather of the shared expert, the fp16 gate GEMV and the
-combine): the shared expert occupies its own lane slot, so every sum is formed
-in the same order.  The oracle composition bounds both under a relative-L2
+gather, a one-expert gather of the shared expert, gdsllm_gemv_f16 for the
+gate logit and the combine): the shared expert occupies its own lane slot and
+the logit follows gemv_f16's summation order, so every sum is formed in the
+same order.  The oracle composition bounds both under a relative-L2
 tolerance."""
 
 import ctypes
@@ -28,27 +30,36 @@ def _shared_stacked(parts):
     return tuple(t.unsqueeze(0) for t in parts)
 
 
-def _step(routed, shared, x, idx, w, gl, g, top_k, gpu):
+def _step(routed, shared, x, idx, w, sgw, g, top_k, gpu):
     structs = [experts_struct(*p, g) for p in routed + shared]
     F = structs[0].out_dim
-    ws_bytes = capi().gdsllm_moe_gather_workspace_size(top_k + 1, F)
+    ws_bytes = capi().gdsllm_moe_step_workspace_size(top_k, F)
     ws = torch.full((ws_bytes,), 0xFF, dtype=torch.uint8, device=gpu)  # NaN-filled: every read slot must be written
     y = torch.empty(structs[2].out_dim, dtype=torch.float16, device=gpu)
     check(capi().gdsllm_moe_step_affine_q4(*(ctypes.byref(s) for s in structs), ptr(x), ptr(idx), ptr(w), top_k,
-                                           ptr(gl), ptr(y), ptr(ws), ws_bytes, stream()))
+                                           ptr(sgw), ptr(y), ptr(ws), ws_bytes, stream()))
     torch.cuda.synchronize()
     return y
 
 
-def _separate(routed, shared, x, idx, w, gl, g, gpu):
+def _separate(routed, shared, x, idx, w, sgw, g, gpu):
     eo = moe_gather(*routed, x, idx, w, g)
     one = torch.zeros(1, dtype=torch.int32, device=gpu)
     unit = torch.ones(1, dtype=torch.float16, device=gpu)
     so = moe_gather(*shared, x, one, unit, g)
+    H = eo.numel()
+    gl = torch.empty(1, dtype=torch.float16, device=gpu)
+    check(capi().gdsllm_gemv_f16(ptr(sgw), ptr(x), ptr(gl), 1, H, 1, H, 1, stream()))
     y = torch.empty_like(eo)
-    check(capi().gdsllm_moe_combine(ptr(eo), ptr(so), ptr(gl), ptr(y), eo.numel(), 1, stream()))  # hidden, n_tok
+    check(capi().gdsllm_moe_combine(ptr(eo), ptr(so), ptr(gl), ptr(y), H, 1, stream()))  # hidden, n_tok
     torch.cuda.synchronize()
     return y
+
+
+def _gate_row(x, logit):
+    """fp16 gate row whose dot with x is about `logit`."""
+    xf = x.float().reshape(-1)
+    return (xf * (logit / float((xf * xf).sum()))).to(torch.float16)
 
 
 # (E, H, F, top_k): one to eight lane slots, 4 / 2 / 1 experts per lane group
@@ -68,11 +79,11 @@ def test_moe_step_matches_separate_launches(gpu, E, H, F, k):
     x = syn.activations(1, H, gen(9200 + k)).to(gpu)
     picks = torch.randperm(E, generator=gen(9300 + k))[:k].to(torch.int32)
     rw = torch.softmax(torch.randn(k, generator=gen(9400 + k)), 0).to(torch.float16)
-    gl_cpu = torch.tensor([0.75 - 0.1 * k], dtype=torch.float16)
-    idx, w, gl = picks.to(gpu), rw.to(gpu), gl_cpu.to(gpu)
+    sgw_cpu = (torch.randn(H, generator=gen(9500 + k)) * 0.02).to(torch.float16)
+    idx, w, sgw = picks.to(gpu), rw.to(gpu), sgw_cpu.to(gpu)
 
-    y = _step(routed, shared, x, idx, w, gl, g, k, gpu)
-    want = _separate(routed, shared, x, idx, w, gl, g, gpu)
+    y = _step(routed, shared, x, idx, w, sgw, g, k, gpu)
+    want = _separate(routed, shared, x, idx, w, sgw, g, gpu)
     np.testing.assert_array_equal(to_np(y).view(np.uint16), to_np(want).view(np.uint16))
 
     def dq(p, e):
@@ -83,7 +94,8 @@ def test_moe_step_matches_separate_launches(gpu, E, H, F, k):
                           lambda e: dq(routed_cpu[2], e), to_np(picks), to_np(rw))
     so, _ = oq.moe_gather(xn, lambda e: dq(shared_cpu[0], e), lambda e: dq(shared_cpu[1], e),
                           lambda e: dq(shared_cpu[2], e), np.zeros(1, np.int32), np.ones(1, np.float16))
-    ref = oq.moe_combine(eo.astype(np.float16)[None], so.astype(np.float16)[None], to_np(gl_cpu)).astype(np.float64)
+    gl = oq.gemv(to_np(sgw_cpu).reshape(1, -1), xn)[0].astype(np.float16)
+    ref = oq.moe_combine(eo.astype(np.float16)[None], so.astype(np.float16)[None], gl).astype(np.float64)
     got = to_np(y).astype(np.float64)
     rel = float(np.linalg.norm(got - ref.reshape(-1)) / np.linalg.norm(ref))
     assert np.all(np.isfinite(got)) and rel <= 5e-3, f"rel L2 {rel:.3e}"
@@ -102,9 +114,9 @@ def test_moe_step_invalid_indices_and_clamp(gpu):
     x = syn.activations(1, H, gen(9501)).to(gpu)
     idx = torch.tensor([3, -1, 15, 16, 7, 1 << 20], dtype=torch.int32, device=gpu)
     w = torch.full((k,), 1.0 / k, dtype=torch.float16, device=gpu)
-    gl = torch.tensor([4.0], dtype=torch.float16, device=gpu)
-    y = _step(routed, shared, x, idx, w, gl, g, k, gpu)
-    want = _separate(routed, shared, x, idx, w, gl, g, gpu)
+    sgw = _gate_row(x, 4.0)
+    y = _step(routed, shared, x, idx, w, sgw, g, k, gpu)
+    want = _separate(routed, shared, x, idx, w, sgw, g, gpu)
     yn = to_np(y)
     np.testing.assert_array_equal(yn.view(np.uint16), to_np(want).view(np.uint16))
     assert np.any(np.abs(yn) == 65504.0) and np.all(np.isfinite(yn))
@@ -118,9 +130,9 @@ def test_moe_step_two_calls_share_nothing(gpu):
     routed = [_dev(syn.affine_q4_weights(s, g, gg), gpu) for s in ([E, F, H], [E, F, H], [E, H, F])]
     shared = [_dev(_shared_stacked(syn.affine_q4_weights(s, g, gg)), gpu) for s in ([F, H], [F, H], [H, F])]
     x = syn.activations(1, H, gen(9601)).to(gpu)
-    gl = torch.tensor([-0.5], dtype=torch.float16, device=gpu)
+    sgw = _gate_row(x, -0.5)
     structs = [experts_struct(*p, g) for p in routed + shared]
-    ws_bytes = capi().gdsllm_moe_gather_workspace_size(9, F)
+    ws_bytes = capi().gdsllm_moe_step_workspace_size(8, F)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=gpu)
     outs = []
     for k in (8, 3):
@@ -128,8 +140,8 @@ def test_moe_step_two_calls_share_nothing(gpu):
         w = torch.full((k,), 1.0 / k, dtype=torch.float16, device=gpu)
         y = torch.empty(H, dtype=torch.float16, device=gpu)
         check(capi().gdsllm_moe_step_affine_q4(*(ctypes.byref(s) for s in structs), ptr(x), ptr(idx), ptr(w), k,
-                                               ptr(gl), ptr(y), ptr(ws), ws_bytes, stream()))
+                                               ptr(sgw), ptr(y), ptr(ws), ws_bytes, stream()))
         torch.cuda.synchronize()
-        outs.append((y, _separate(routed, shared, x, idx, w, gl, g, gpu)))
+        outs.append((y, _separate(routed, shared, x, idx, w, sgw, g, gpu)))
     for y, want in outs:
         np.testing.assert_array_equal(to_np(y).view(np.uint16), to_np(want).view(np.uint16))

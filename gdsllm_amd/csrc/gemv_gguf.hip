@@ -677,8 +677,13 @@ __global__ __launch_bounds__(kWaves * 64) void gguf_gemv_rows(const RowsTarget t
     // dummy when the wave has no stage); waiting for all but the weight
     // transfers then waits for x only.  A compute unit returns its requests in
     // order, so every wave's x is requested before any wave's weights.
+    // Top wave priority while x is issued: x requests of a workgroup that
+    // starts next to running ones leave ahead of their weight requests
+    // (11008x4096 at batch 1: 7.006 against 7.038 us per call).
+    __builtin_amdgcn_s_setprio(3);
     rows_xraw_issue<NB>(xp, X, ldx, K, NW, wave, kWaves, lane);
     __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_s_setprio(0);
     rows_issue<F, 0, C, PAIRED>(buf, stage_at(0), X, row_bytes, goff, T > 0, lane);
     wait_vmcnt<C>();
     lds_barrier();  // every wave's share of x has landed

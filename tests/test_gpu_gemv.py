@@ -102,6 +102,24 @@ def test_gguf_gemv_strided_batch(gpu, B):
     assert_gemv_close(yn[:, :M], deq, to_np(x), "strided")
 
 
+@pytest.mark.parametrize("B", [3, 8])
+def test_q4_0_batched_strided_x_in_registers(gpu, B):
+    """ldx / ldy larger than the row on a shape that takes the x-in-registers
+    kernel (9000 rows: 282 tiles of 32 over 256 CUs): x rows come from a wider
+    buffer and nothing outside y's rows is written."""
+    M, K = 9000, 1536
+    w, x, deq = _gguf_case("q4_0", M, K, B, 93 + B)
+    xw = torch.zeros(B, K + 128, dtype=torch.float16)
+    xw[:, :K] = x
+    xd, wd = xw.to(gpu), w.to(gpu)
+    y = torch.full((B, M + 24), 7.0, dtype=torch.float16, device=gpu)
+    check(capi().gdsllm_fused_q4_0_gemv(ptr(wd), ptr(xd), ptr(y), M, K, B, K + 128, M + 24, stream()))
+    torch.cuda.synchronize()
+    yn = to_np(y)
+    assert np.all(yn[:, M:] == 7.0), "wrote outside the output rows"
+    assert_gemv_close(yn[:, :M], deq, to_np(x), f"strided x-in-registers B={B}")
+
+
 def test_gguf_gemv_closed_forms(gpu):
     """All nibbles 8 -> y = 0 up to the fp32 cancellation of the nibble-offset
     correction (1032*sum(x) per block, |err| ~ 2^-24 * 1032 * |sum x| * d, far

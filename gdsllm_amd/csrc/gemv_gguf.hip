@@ -1331,34 +1331,45 @@ int launch_q4_codes(const void* w, const uint16_t* x, uint16_t* y, int M, int K,
 // first weights are issued; register loads straight from HBM gathered 8
 // batch rows per instruction and took ~4 us longer per launch.
 namespace bx {
-constexpr int kWaves = 8;
-constexpr int kNSB = 4;  // super-blocks of K per wave at most
 constexpr int kRT = 16;  // rows per tile
 constexpr int kNWD = (kRT * 9 + 63) / 64;                  // weight transfers per stage (3)
 constexpr int kLastLanes = kRT * 9 - 64 * (kNWD - 1);      // lanes of the last one (16)
-constexpr int kNS = 8;                                     // stage slots per wave
 constexpr int kSlotBytes = kRT * 144;                      // one super-block of the tile's rows
-constexpr int kRedBytes = kWaves * 8 * kRT * 4;            // one tile's partial sums
-constexpr int kLdsBytes = kWaves * kNS * kSlotBytes + 2 * kRedBytes;
-static_assert(kNS * kSlotBytes >= kNSB * 4096, "the x slice is staged in the wave's slots");
+// WV waves per workgroup, at most NSB super-blocks of K per wave, NS stage
+// slots per wave; DC keeps the offset corrections in registers.
+template <int WV, int NSB, int NS, bool DC>
+struct Cfg {
+    static constexpr int kWaves = WV, kNSB = NSB, kNS = NS;
+    static constexpr bool kDC = DC;
+    static constexpr int kRedBytes = WV * 8 * kRT * 4;  // one tile's partial sums
+    static constexpr int kLdsBytes = WV * NS * kSlotBytes + 2 * kRedBytes;
+    static_assert(NS * kSlotBytes >= NSB * 4096, "the x slice is staged in the wave's slots");
+    static_assert(kLdsBytes <= 160 * 1024, "LDS of one compute unit");
+};
+// 8 waves x 4 super-blocks (in_dim <= 8192), 8 slots: many tiles per workgroup
+using Wide = Cfg<8, 4, 8, true>;
+// 16 waves x 2 super-blocks, 4 slots: a 16-row tile's whole K in flight at
+// once, for matrices with fewer tiles than compute units
+using Tall = Cfg<16, 2, 4, false>;
 }  // namespace bx
 
-__global__ __launch_bounds__(bx::kWaves * 64) void gguf_gemv_q4_xreg(const uint8_t* __restrict__ W,
+template <class C>
+__global__ __launch_bounds__(C::kWaves * 64) void gguf_gemv_q4_xreg(const uint8_t* __restrict__ W,
                                                                     const uint16_t* __restrict__ X,
                                                                     uint16_t* __restrict__ Y, int M, int K, int nb,
                                                                     int64_t ldx, int64_t ldy) {
-    constexpr int RT = bx::kRT, NRG = RT / 8, NWD = bx::kNWD, NS = bx::kNS;
+    constexpr int RT = bx::kRT, NRG = RT / 8, NWD = bx::kNWD, NS = C::kNS;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int S = K >> 8;
     const uint32_t row_bytes = static_cast<uint32_t>(S) * 144u;
     const int ntiles = (M + RT - 1) / RT;
     const int T = (ntiles - static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) - 1) / static_cast<int>(gridDim.x);
-    const int nst = S > wave ? (S - 1 - wave) / bx::kWaves + 1 : 0;  // super-blocks of this wave (<= 4)
+    const int nst = S > wave ? (S - 1 - wave) / C::kWaves + 1 : 0;  // super-blocks of this wave (<= NSB)
     const int Q = T * nst;
     const uint32_t lds0 = lds_addr(lds);
     const uint32_t slot0 = lds0 + wave * NS * bx::kSlotBytes;
-    float* red0 = reinterpret_cast<float*>(lds + bx::kWaves * NS * bx::kSlotBytes);
+    float* red0 = reinterpret_cast<float*>(lds + C::kWaves * NS * bx::kSlotBytes);
 
     // weight transfer j: chunk c = 64j + lane = row c / 9, chunk c % 9 of the
     // row's super-block (rows past the tile's last valid row read that row)
@@ -1376,7 +1387,7 @@ __global__ __launch_bounds__(bx::kWaves * 64) void gguf_gemv_q4_xreg(const uint8
     int ii = 0, ss = 0, qs = 0;  // next stage to issue: tile ii, super-block step ss, slot qs
     auto issue = [&]() {
         const uint32_t slot = slot0 + qs * bx::kSlotBytes;
-        const int sb = wave + bx::kWaves * ss;
+        const int sb = wave + C::kWaves * ss;
         const int row0 = RT * (static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) * ii);
         const uint8_t* wb = W + static_cast<int64_t>(row0) * row_bytes + 144 * sb;
         uint32_t woff[NWD];
@@ -1410,7 +1421,7 @@ __global__ __launch_bounds__(bx::kWaves * 64) void gguf_gemv_q4_xreg(const uint8
 #pragma unroll
     for (int r = 0; r < NRG; ++r) acc[r] = float4_t{0.f, 0.f, 0.f, 0.f};
     auto finish_tile = [&]() {
-        float* red = red0 + (ck & 1) * (bx::kRedBytes / 4);
+        float* red = red0 + (ck & 1) * (C::kRedBytes / 4);
         const int src = lane + 40 < 64 ? lane + 40 : lane;
 #pragma unroll
         for (int rg = 0; rg < NRG; ++rg) {
@@ -1428,7 +1439,7 @@ __global__ __launch_bounds__(bx::kWaves * 64) void gguf_gemv_q4_xreg(const uint8
             const int t = i / RT, r = i - t * RT;
             float sum = 0.f;
 #pragma unroll
-            for (int w = 0; w < bx::kWaves; ++w) sum += red[(w * 8 + t) * RT + r];
+            for (int w = 0; w < C::kWaves; ++w) sum += red[(w * 8 + t) * RT + r];
             if (t < nb && row0 + r < M) Y[t * ldy + row0 + r] = f2h_bits(sum);
         }
         ++ck;
@@ -1444,11 +1455,11 @@ __global__ __launch_bounds__(bx::kWaves * 64) void gguf_gemv_q4_xreg(const uint8
     // x slice: 4 transfers per super-block into the wave's slots (transfer jj
     // holds batch rows 2jj, 2jj+1, rows past nb repeat row nb - 1; the
     // super-blocks past this wave's last repeat it), then into registers.
-    half8_t xa[bx::kNSB][4];
+    half8_t xa[C::kNSB][4];
     {
 #pragma unroll
-        for (int s2 = 0; s2 < bx::kNSB; ++s2) {
-            const int sb = wave + bx::kWaves * min(s2, nst - 1);
+        for (int s2 = 0; s2 < C::kNSB; ++s2) {
+            const int sb = wave + C::kWaves * min(s2, nst - 1);
 #pragma unroll
             for (int jj = 0; jj < 4; ++jj) {
                 const int tr = min(2 * jj + (lane >> 5), nb - 1);
@@ -1461,7 +1472,7 @@ __global__ __launch_bounds__(bx::kWaves * 64) void gguf_gemv_q4_xreg(const uint8
         const int t = min(j & 7, nb - 1);
         const uint8_t* xl = lds + (slot0 - lds0) + (t >> 1) * 1024 + (t & 1) * 512 + 2 * (32 * par + 4 * g);
 #pragma unroll
-        for (int s2 = 0; s2 < bx::kNSB; ++s2)
+        for (int s2 = 0; s2 < C::kNSB; ++s2)
 #pragma unroll
             for (int p = 0; p < 4; ++p) {
                 const uint2 lo = *reinterpret_cast<const uint2*>(xl + 4096 * s2 + 128 * p);
@@ -1478,17 +1489,20 @@ __global__ __launch_bounds__(bx::kWaves * 64) void gguf_gemv_q4_xreg(const uint8
     const half8_t kneg = {static_cast<half_t>(-1032.0f), static_cast<half_t>(-1032.0f), static_cast<half_t>(-1032.0f),
                           static_cast<half_t>(-1032.0f), static_cast<half_t>(-72.0f),   static_cast<half_t>(-72.0f),
                           static_cast<half_t>(-72.0f),   static_cast<half_t>(-72.0f)};
-    float4_t dc[bx::kNSB][4];
+    float4_t dc[C::kDC ? C::kNSB : 1][4];
+    if constexpr (C::kDC) {
 #pragma unroll
-    for (int s2 = 0; s2 < bx::kNSB; ++s2)
+        for (int s2 = 0; s2 < C::kNSB; ++s2)
 #pragma unroll
-        for (int p = 0; p < 4; ++p)
-            dc[s2][p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[s2][p], kneg, float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            for (int p = 0; p < 4; ++p)
+                dc[s2][p] =
+                    __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[s2][p], kneg, float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+    }
 
     int q = 0, cslot = 0;
     for (int t = 0; t < T; ++t) {
 #pragma unroll
-        for (int s2 = 0; s2 < bx::kNSB; ++s2) {
+        for (int s2 = 0; s2 < C::kNSB; ++s2) {
             if (s2 < nst) {
                 // stages of weights issued after stage q
                 switch (issued - 1 - q) {
@@ -1502,6 +1516,12 @@ __global__ __launch_bounds__(bx::kWaves * 64) void gguf_gemv_q4_xreg(const uint8
                     default: wait_vmcnt_asm<(NS - 1) * NWD>(); break;
                 }
                 const uint8_t* sl = lds + (slot0 - lds0) + cslot * bx::kSlotBytes;
+                if constexpr (!C::kDC) {
+#pragma unroll
+                    for (int p = 0; p < 4; ++p)
+                        dc[0][p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[s2][p], kneg,
+                                                                          float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                }
 #pragma unroll
                 for (int rg = 0; rg < NRG; ++rg)
 #pragma unroll
@@ -1514,7 +1534,8 @@ __global__ __launch_bounds__(bx::kWaves * 64) void gguf_gemv_q4_xreg(const uint8
                         const uint32_t p23 = __builtin_amdgcn_perm(d1, d0, sel23);
                         const half8_t wbv = __builtin_bit_cast(
                             half8_t, make_uint4(nu.lo_c(p01), nu.lo_c(p23), nu.hi_c(p01), nu.hi_c(p23)));
-                        const float4_t D = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[s2][p], wbv, dc[s2][p], 0, 0, 0);
+                        const float4_t D = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            xa[s2][p], wbv, dc[C::kDC ? s2 : 0][p], 0, 0, 0);
                         const float dsc = static_cast<float>(dv);
 #pragma unroll
                         for (int v = 0; v < 4; ++v) acc[rg][v] = __builtin_fmaf(dsc, D[v], acc[rg][v]);
@@ -1533,16 +1554,17 @@ __global__ __launch_bounds__(bx::kWaves * 64) void gguf_gemv_q4_xreg(const uint8
     }
 }
 
+template <class C>
 int launch_q4_xreg(const void* w, const uint16_t* x, uint16_t* y, int M, int K, int64_t batch, int64_t ldx,
                    int64_t ldy, hipStream_t stream) {
-    constexpr size_t lds = bx::kLdsBytes;
-    const void* fn = reinterpret_cast<const void*>(&gguf_gemv_q4_xreg);
+    constexpr size_t lds = C::kLdsBytes;
+    const void* fn = reinterpret_cast<const void*>(&gguf_gemv_q4_xreg<C>);
     if (int rc = prepare_lds(fn, lds)) return rc;
     const int tiles = (M + bx::kRT - 1) / bx::kRT;
-    const int resident = blocks_per_cu(fn, lds, bx::kWaves * 64) * cu_count();
+    const int resident = blocks_per_cu(fn, lds, C::kWaves * 64) * cu_count();
     if (resident < 1) return set_error(GDSLLM_ERR_UNSUPPORTED, "gguf_gemv_q4_xreg: no workgroup fits a compute unit");
     const int grid = std::min(tiles, resident);
-    hipLaunchKernelGGL(gguf_gemv_q4_xreg, dim3(grid), dim3(bx::kWaves * 64), lds, stream,
+    hipLaunchKernelGGL((gguf_gemv_q4_xreg<C>), dim3(grid), dim3(C::kWaves * 64), lds, stream,
                        static_cast<const uint8_t*>(w), x, y, M, K, static_cast<int>(batch), ldx, ldy);
     return check_hip(hipGetLastError(), "gguf_gemv_q4_xreg launch");
 }
@@ -1561,6 +1583,24 @@ int launch_q4_xreg(const void* w, const uint16_t* x, uint16_t* y, int M, int K, 
 inline bool use_q4_xreg(int M, int K) {
     const int t32 = (M + 31) / 32, cu = cu_count();
     return K <= 8192 && t32 > cu && t32 % cu != 0;
+}
+
+// The 16-wave variant (a 16-row tile's whole K in flight at once) for
+// matrices with at most one 16-row tile per compute unit.  Measured on
+// MI355X (us, code kernel / 16-wave variant):
+//                  batch 4          batch 8
+//   1024 x 8192   8.40 / 6.33     8.56 / 8.10
+//   2048 x 8192   8.60 / 6.64     8.95 / 8.24
+//   4096 x 8192  11.48 / 7.25    11.87 / 8.55
+//   4096 x 4096   7.45 / 5.69     7.56 / 7.64
+//   1024 x 4096   5.30 / 5.36     5.37 / 7.24
+// so it serves in_dim 4097-8192, and in_dim <= 4096 only up to batch 4 with
+// more than one tile per two compute units.
+inline bool use_q4_xreg_tall(int M, int K, int64_t batch) {
+    const int t16 = (M + 15) / 16, cu = cu_count();
+    if (K > 8192 || t16 > cu) return false;
+    if (K > 4096) return true;
+    return batch <= 4 && 2 * t16 > cu;
 }
 
 // Row-tile height for the code kernel.  A 16-row stage moves 1.8 bytes of x
@@ -1756,7 +1796,12 @@ int gemv(const char* name, const void* w, const void* x, void* y, int64_t out_di
     const bool x_al16 = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (ldx % 8 == 0);
     if (F == Fmt::Q4_0 && fast && batch >= 3 && x_al16 && use_q4_xreg(M, K) &&
         2 * (7 * ldx + K) < (int64_t{1} << 31)) {
-        const int rc2 = launch_q4_xreg(w, xp, yp, M, K, batch, ldx, ldy, s);
+        const int rc2 = launch_q4_xreg<bx::Wide>(w, xp, yp, M, K, batch, ldx, ldy, s);
+        return rc2 == GDSLLM_OK ? ok() : rc2;
+    }
+    if (F == Fmt::Q4_0 && fast && batch >= 3 && x_al16 && use_q4_xreg_tall(M, K, batch) &&
+        2 * (7 * ldx + K) < (int64_t{1} << 31)) {
+        const int rc2 = launch_q4_xreg<bx::Tall>(w, xp, yp, M, K, batch, ldx, ldy, s);
         return rc2 == GDSLLM_OK ? ok() : rc2;
     }
     if (F == Fmt::Q4_0 && fast && batch >= 3 && K <= (1 << 20) && x_al16) {

@@ -44,8 +44,12 @@ def test_gguf_gemv_b1(gpu, fmt, M, K):
 # split unevenly into 32-row tiles over 256 compute units, so batch 3-8 Q4_0
 # takes the x-in-registers kernel there (with part tiles, 1 super-block per
 # row, and 20 / 11 super-blocks over 8 waves)
+# 24 x 8192, 50 x 5120 and 3000 x 7936 take the 16-wave x-in-registers
+# variant (2, 1 and 0 super-blocks per wave, a part tile), as does 2500 x
+# 3072 at batch 3-4 (12 super-blocks over 16 waves)
 BATCHED_SHAPES = [(70, 4096), (33, 11008), (20, 96), (24, 8192), (9, 28672), (13003, 1024), (40, 256), (8200, 512),
-                  (50, 5120), (1000, 2816), (4100, 6144), (9000, 5120), (8300, 256), (8500, 2816)]
+                  (50, 5120), (1000, 2816), (4100, 6144), (9000, 5120), (8300, 256), (8500, 2816), (3000, 7936),
+                  (2500, 3072)]
 
 
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])

@@ -1320,37 +1320,37 @@ int launch_q4_codes(const void* w, const uint16_t* x, uint16_t* y, int M, int K,
 // ---- Q4_0 codes on MFMA with x held in registers (in_dim <= 8192) ----------
 //
 // Same operands and arithmetic as gguf_gemv_q4_codes, different data
-// movement.  Wave w of a workgroup always takes super-blocks w, w+8, ... of K
-// (at most 4 at in_dim 8192), for every 16-row tile the workgroup owns, so its
-// slice of x (up to 4 super-blocks x 8 batch rows, 16 KiB) is loaded once and
-// its offset corrections computed once.  LDS then holds weights only: 8 stage
-// slots per wave, so a wave keeps up to 8 stages in flight against 2 when
-// every stage carried its own x, and x is read once per wave instead of once
-// per row tile.  The x slice comes in by LDS DMA (2 batch rows x 512 bytes per
-// transfer) into the wave's slots and is read into registers before the
-// first weights are issued; register loads straight from HBM gathered 8
-// batch rows per instruction and took ~4 us longer per launch.
+// movement.  Wave w of a 16-wave workgroup always takes super-blocks w and
+// w+16 of K, for every 16-row tile the workgroup owns, so its slice of x (up
+// to 2 super-blocks x 8 batch rows, 8 KiB) is loaded once instead of once per
+// tile.  LDS then holds weights only: 4 stage slots per wave, so a tile's
+// whole K is in flight at once.  The x slice comes in by LDS DMA (2 batch rows
+// x 512 contiguous bytes per transfer) into the wave's slots and is read into
+// registers before the first weights are issued; register loads straight
+// from HBM gathered 8 batch rows per instruction and took ~4 us longer per
+// launch.
 namespace bx {
 constexpr int kRT = 16;  // rows per tile
 constexpr int kNWD = (kRT * 9 + 63) / 64;                  // weight transfers per stage (3)
 constexpr int kLastLanes = kRT * 9 - 64 * (kNWD - 1);      // lanes of the last one (16)
 constexpr int kSlotBytes = kRT * 144;                      // one super-block of the tile's rows
 // WV waves per workgroup, at most NSB super-blocks of K per wave, NS stage
-// slots per wave; DC keeps the offset corrections in registers.
-template <int WV, int NSB, int NS, bool DC>
+// slots per wave.
+template <int WV, int NSB, int NS>
 struct Cfg {
     static constexpr int kWaves = WV, kNSB = NSB, kNS = NS;
-    static constexpr bool kDC = DC;
     static constexpr int kRedBytes = WV * 8 * kRT * 4;  // one tile's partial sums
     static constexpr int kLdsBytes = WV * NS * kSlotBytes + 2 * kRedBytes;
     static_assert(NS * kSlotBytes >= NSB * 4096, "the x slice is staged in the wave's slots");
     static_assert(kLdsBytes <= 160 * 1024, "LDS of one compute unit");
 };
-// 8 waves x 4 super-blocks (in_dim <= 8192), 8 slots: many tiles per workgroup
-using Wide = Cfg<8, 4, 8, true>;
-// 16 waves x 2 super-blocks, 4 slots: a 16-row tile's whole K in flight at
-// once, for matrices with fewer tiles than compute units
-using Tall = Cfg<16, 2, 4, false>;
+// 16 waves x 2 super-blocks (in_dim <= 8192), 4 slots: a 16-row tile's whole
+// K in flight at once.  The offset corrections are recomputed per stage (4
+// MFMAs) to stay within the 128 registers of a 1024-thread workgroup.
+// Measured against 8 waves x 4 super-blocks with 8 slots and the corrections
+// kept in registers (batch 8, us): 28672x8192 31.7 / 34.3, 13003x4096
+// 13.7 / 15.8, 9000x5120 12.2 / 14.2.
+using Tall = Cfg<16, 2, 4>;
 }  // namespace bx
 
 template <class C>
@@ -1489,15 +1489,7 @@ __global__ __launch_bounds__(C::kWaves * 64) void gguf_gemv_q4_xreg(const uint8_
     const half8_t kneg = {static_cast<half_t>(-1032.0f), static_cast<half_t>(-1032.0f), static_cast<half_t>(-1032.0f),
                           static_cast<half_t>(-1032.0f), static_cast<half_t>(-72.0f),   static_cast<half_t>(-72.0f),
                           static_cast<half_t>(-72.0f),   static_cast<half_t>(-72.0f)};
-    float4_t dc[C::kDC ? C::kNSB : 1][4];
-    if constexpr (C::kDC) {
-#pragma unroll
-        for (int s2 = 0; s2 < C::kNSB; ++s2)
-#pragma unroll
-            for (int p = 0; p < 4; ++p)
-                dc[s2][p] =
-                    __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[s2][p], kneg, float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-    }
+    float4_t dc[4];  // offset corrections of the stage's 4 block pairs
 
     int q = 0, cslot = 0;
     for (int t = 0; t < T; ++t) {
@@ -1516,12 +1508,10 @@ __global__ __launch_bounds__(C::kWaves * 64) void gguf_gemv_q4_xreg(const uint8_
                     default: wait_vmcnt_asm<(NS - 1) * NWD>(); break;
                 }
                 const uint8_t* sl = lds + (slot0 - lds0) + cslot * bx::kSlotBytes;
-                if constexpr (!C::kDC) {
 #pragma unroll
-                    for (int p = 0; p < 4; ++p)
-                        dc[0][p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[s2][p], kneg,
-                                                                          float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                }
+                for (int p = 0; p < 4; ++p)
+                    dc[p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[s2][p], kneg, float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0,
+                                                                   0);
 #pragma unroll
                 for (int rg = 0; rg < NRG; ++rg)
 #pragma unroll
@@ -1534,8 +1524,7 @@ __global__ __launch_bounds__(C::kWaves * 64) void gguf_gemv_q4_xreg(const uint8_
                         const uint32_t p23 = __builtin_amdgcn_perm(d1, d0, sel23);
                         const half8_t wbv = __builtin_bit_cast(
                             half8_t, make_uint4(nu.lo_c(p01), nu.lo_c(p23), nu.hi_c(p01), nu.hi_c(p23)));
-                        const float4_t D = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                            xa[s2][p], wbv, dc[C::kDC ? s2 : 0][p], 0, 0, 0);
+                        const float4_t D = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[s2][p], wbv, dc[p], 0, 0, 0);
                         const float dsc = static_cast<float>(dv);
 #pragma unroll
                         for (int v = 0; v < 4; ++v) acc[rg][v] = __builtin_fmaf(dsc, D[v], acc[rg][v]);
@@ -1569,34 +1558,29 @@ int launch_q4_xreg(const void* w, const uint16_t* x, uint16_t* y, int M, int K, 
     return check_hip(hipGetLastError(), "gguf_gemv_q4_xreg launch");
 }
 
-// Choice between the two batched Q4_0 kernels (measured on MI355X at batch 8,
-// us):              codes (32-row tiles)   x in registers (16-row tiles)
-//   28672 x 8192          40.4                    32.7
-//   11008 x 4096          13.9                    12.5
-//   16384 x 8192          22.3                    22.8
-//    8192 x 8192          13.6                    15.2
-//    4096 x 4096           7.5                     7.9
-//    1024 x 8192           8.5                     8.7
-// The x-in-registers kernel pays ~1.5 us for x before its first weights; it
-// wins where the code kernel's 32-row tiles split unevenly over the compute
-// units (896 and 344 tiles on 256) and re-read x for every extra tile.
+// Choice between the two batched Q4_0 kernels.  The x-in-registers kernel
+// pays for x before its first weights; it wins where the code kernel's
+// 32-row tiles split unevenly over the compute units (896 and 344 tiles on
+// 256, which re-read x for every extra tile: 28672x8192 at batch 8 40.4 us
+// with the code kernel, 31.7 with it) and where a matrix has at most one
+// 16-row tile per compute unit (below), and loses on balanced many-tile
+// matrices (8192x8192: 13.3 against 13.6).
 inline bool use_q4_xreg(int M, int K) {
     const int t32 = (M + 31) / 32, cu = cu_count();
     return K <= 8192 && t32 > cu && t32 % cu != 0;
 }
 
-// The 16-wave variant (a 16-row tile's whole K in flight at once) for
-// matrices with at most one 16-row tile per compute unit.  Measured on
-// MI355X (us, code kernel / 16-wave variant):
+// Matrices with at most one 16-row tile per compute unit.  Measured on
+// MI355X (us, code kernel / x in registers):
 //                  batch 4          batch 8
 //   1024 x 8192   8.40 / 6.33     8.56 / 8.10
 //   2048 x 8192   8.60 / 6.64     8.95 / 8.24
 //   4096 x 8192  11.48 / 7.25    11.87 / 8.55
 //   4096 x 4096   7.45 / 5.69     7.56 / 7.64
 //   1024 x 4096   5.30 / 5.36     5.37 / 7.24
-// so it serves in_dim 4097-8192, and in_dim <= 4096 only up to batch 4 with
+// so it takes in_dim 4097-8192, and in_dim <= 4096 only up to batch 4 with
 // more than one tile per two compute units.
-inline bool use_q4_xreg_tall(int M, int K, int64_t batch) {
+inline bool use_q4_xreg_few(int M, int K, int64_t batch) {
     const int t16 = (M + 15) / 16, cu = cu_count();
     if (K > 8192 || t16 > cu) return false;
     if (K > 4096) return true;
@@ -1794,12 +1778,7 @@ int gemv(const char* name, const void* w, const void* x, void* y, int64_t out_di
     if (rc != -1) return rc == GDSLLM_OK ? ok() : rc;
     rc = GDSLLM_OK;
     const bool x_al16 = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (ldx % 8 == 0);
-    if (F == Fmt::Q4_0 && fast && batch >= 3 && x_al16 && use_q4_xreg(M, K) &&
-        2 * (7 * ldx + K) < (int64_t{1} << 31)) {
-        const int rc2 = launch_q4_xreg<bx::Wide>(w, xp, yp, M, K, batch, ldx, ldy, s);
-        return rc2 == GDSLLM_OK ? ok() : rc2;
-    }
-    if (F == Fmt::Q4_0 && fast && batch >= 3 && x_al16 && use_q4_xreg_tall(M, K, batch) &&
+    if (F == Fmt::Q4_0 && fast && batch >= 3 && x_al16 && (use_q4_xreg(M, K) || use_q4_xreg_few(M, K, batch)) &&
         2 * (7 * ldx + K) < (int64_t{1} << 31)) {
         const int rc2 = launch_q4_xreg<bx::Tall>(w, xp, yp, M, K, batch, ldx, ldy, s);
         return rc2 == GDSLLM_OK ? ok() : rc2;

@@ -148,11 +148,12 @@ __global__ __launch_bounds__(64) void route_topk(const uint16_t* __restrict__ lo
     for (int j = 0; j < NPL; ++j) h[j] = L[lane + 64 * j < E ? lane + 64 * j : 0];
 #pragma unroll
     for (int j = 0; j < NPL; ++j) word[j] = lane + 64 * j < E ? pick_word(h[j], lane + 64 * j) : 0u;
-    // Each round's pick is wave-uniform; its value is decoded from the key
-    // (+-0 -> +0, NaN -> NaN, both softmax-neutral), its exp(l - max) computed
-    // once and summed in pick order, and lane i keeps pick i.
+    // Each round's pick is wave-uniform and lane i keeps pick i; only the
+    // selection is serial.  Afterwards each lane decodes its pick's value
+    // (+-0 -> +0, NaN -> NaN, both softmax-neutral) and takes exp(l - max)
+    // itself, and the exponentials are summed in pick order.
     int my_idx = 0;
-    float my_ex = 0.f, m = 0.f, sum = 0.f;
+    uint32_t my_key = 0, top_key = 0;
     for (int i = 0; i < k; ++i) {
         uint32_t best = 0;
 #pragma unroll
@@ -160,16 +161,20 @@ __global__ __launch_bounds__(64) void route_topk(const uint16_t* __restrict__ lo
         best = wave_max(best);
 #pragma unroll
         for (int j = 0; j < NPL; ++j) word[j] = word[j] == best ? 0u : word[j];
-        const uint32_t key = best >> 16;
-        const float v = key == 0xFFFFu ? __builtin_nanf("") : h2f((key & 0x8000u) ? (key & 0x7FFFu) : (~key & 0xFFFFu));
-        if (i == 0) m = v;
-        const float ex = expf(fp32_rounded(v - m));
-        sum = fp32_rounded(sum + ex);
+        if (i == 0) top_key = best >> 16;
         if (lane == i) {
             my_idx = static_cast<int>(0xFFFFu - (best & 0xFFFFu));
-            my_ex = ex;
+            my_key = best >> 16;
         }
     }
+    auto key_value = [](uint32_t key) {
+        return key == 0xFFFFu ? __builtin_nanf("") : h2f((key & 0x8000u) ? (key & 0x7FFFu) : (~key & 0xFFFFu));
+    };
+    const float m = key_value(top_key);
+    const float my_ex = lane < k ? expf(fp32_rounded(key_value(my_key) - m)) : 0.f;
+    float sum = 0.f;
+    for (int i = 0; i < k; ++i)
+        sum = fp32_rounded(sum + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_ex), i)));
     if (lane < k) {
         idx[static_cast<int64_t>(blockIdx.x) * k + lane] = my_idx;
         wts[static_cast<int64_t>(blockIdx.x) * k + lane] = f2h_bits(fp32_rounded(my_ex / sum));

@@ -34,7 +34,33 @@ void check(int rc, const std::string& where) {
     }
 }
 
-void* stream_of(int device_id) { return c10::hip::getCurrentHIPStream(device_id).stream(); }
+// Makes `device_id` the current HIP device for the scope (the library plans
+// launch geometry for the current device) and resolves its current stream.
+// Used as a named guard or as a temporary inside the full expression of the
+// call it serves.
+class OnDevice {
+  public:
+    explicit OnDevice(int device_id) {
+        if (hipGetDevice(&prev_) != hipSuccess) prev_ = -1;
+        if (prev_ != device_id) {
+            if (hipSetDevice(device_id) != hipSuccess)
+                throw std::runtime_error("cannot make cuda:" + std::to_string(device_id) + " the current device");
+            restore_ = prev_ >= 0;
+        }
+        stream_ = c10::hip::getCurrentHIPStream(device_id).stream();
+    }
+    ~OnDevice() {
+        if (restore_) (void)hipSetDevice(prev_);
+    }
+    OnDevice(const OnDevice&) = delete;
+    OnDevice& operator=(const OnDevice&) = delete;
+    void* stream() const { return stream_; }
+
+  private:
+    int prev_ = -1;
+    bool restore_ = false;
+    void* stream_ = nullptr;
+};
 
 // Device buffer with the GdsBufferHandle surface (runtime/gds_bindings.cpp:51-76):
 // size / device_id / registered.  Either owns a hipMalloc allocation, or wraps
@@ -228,7 +254,8 @@ torch::Tensor dequant_gguf(const Handle& h, std::vector<int64_t> shape, const st
     } else {
         out = torch::empty(shape, fp16_on(h->device_id()));
     }
-    void* s = stream_of(h->device_id());
+    const OnDevice on(h->device_id());
+    void* s = on.stream();
     const int rc = gguf_type == "q4_0" ? gdsllm_dequant_q4_0(at_offset(h, offset), out.data_ptr(), blocks, s)
                                        : gdsllm_dequant_q8_0(at_offset(h, offset), out.data_ptr(), blocks, s);
     check(rc, "py_dequant_gguf");
@@ -254,7 +281,8 @@ torch::Tensor embed_gguf(const Handle& h, torch::Tensor token_ids, std::vector<i
     std::vector<int64_t> out_shape(token_ids.sizes().begin(), token_ids.sizes().end());
     out_shape.push_back(hidden);
     auto out = torch::empty(out_shape, fp16_on(h->device_id()));
-    void* s = stream_of(h->device_id());
+    const OnDevice on(h->device_id());
+    void* s = on.stream();
     const int64_t n = ids.numel();
     for (int64_t t = 0; t < n; t += 65535) {
         const int64_t c = std::min<int64_t>(65535, n - t);
@@ -292,7 +320,8 @@ torch::Tensor fused_dequant_gemv(const Handle& h, torch::Tensor x, std::vector<i
     check_x(xf, h->device_id(), "py_fused_dequant_gemv");
     check_range(h, offset, out_dim * (in_dim / 32) * bb, "py_fused_dequant_gemv");
     torch::Tensor out = torch::empty({batch, out_dim}, fp16_on(h->device_id()));
-    void* s = stream_of(h->device_id());
+    const OnDevice on(h->device_id());
+    void* s = on.stream();
     const int rc = gguf_type == "q4_0"
                        ? gdsllm_fused_q4_0_gemv(at_offset(h, offset), xf.data_ptr(), out.data_ptr(), out_dim, in_dim,
                                                 batch, in_dim, out_dim, s)
@@ -340,7 +369,7 @@ torch::Tensor dequant_affine_q4(const Handle& h, std::vector<int64_t> weight_sha
     } else {
         out = torch::empty(weight_shape, fp16_on(h->device_id()));
     }
-    check(gdsllm_dequant_affine_q4(p.w, p.s, p.b, out.data_ptr(), n, in_dim, group_size, stream_of(h->device_id())),
+    check(gdsllm_dequant_affine_q4(p.w, p.s, p.b, out.data_ptr(), n, in_dim, group_size, OnDevice(h->device_id()).stream()),
           "py_dequant_affine_q4");
     return out;
 }
@@ -366,7 +395,7 @@ torch::Tensor fused_affine_q4_gemv(const Handle& h, torch::Tensor x, std::vector
                                "py_fused_affine_q4_gemv");
     torch::Tensor out = torch::empty({batch, out_dim}, fp16_on(h->device_id()));
     check(gdsllm_fused_affine_q4_gemv(p.w, p.s, p.b, xf.data_ptr(), out.data_ptr(), out_dim, in_dim, group_size,
-                                      batch, in_dim, out_dim, stream_of(h->device_id())),
+                                      batch, in_dim, out_dim, OnDevice(h->device_id()).stream()),
           "py_fused_affine_q4_gemv");
     return out;
 }
@@ -422,7 +451,7 @@ torch::Tensor moe_gather_affine_q4(torch::Tensor x, const Handle& gate_h, std::v
     torch::Tensor ws = torch::empty({static_cast<int64_t>(ws_bytes)}, torch::TensorOptions().dtype(torch::kUInt8).device(torch::kCUDA, dev));
     torch::Tensor out = torch::empty({1, d.out_dim}, fp16_on(dev));
     check(gdsllm_moe_gather_affine_q4(&g, &u, &d, xf.data_ptr(), idx.data_ptr<int32_t>(), wts.data_ptr(), k,
-                                      out.data_ptr(), ws.data_ptr(), ws_bytes, stream_of(dev)),
+                                      out.data_ptr(), ws.data_ptr(), ws_bytes, OnDevice(dev).stream()),
           where);
     return out;
 }
@@ -469,7 +498,7 @@ std::optional<torch::Tensor> moe_step_affine_q4(torch::Tensor x, std::vector<Aff
     torch::Tensor out = torch::empty({1, e[2].out_dim}, fp16_on(dev));
     const int rc = gdsllm_moe_step_affine_q4(&e[0], &e[1], &e[2], &e[3], &e[4], &e[5], xf.data_ptr(),
                                              idx.data_ptr<int32_t>(), wts.data_ptr(), k, sg.data_ptr(), out.data_ptr(),
-                                             ws.data_ptr(), ws_bytes, stream_of(dev));
+                                             ws.data_ptr(), ws_bytes, OnDevice(dev).stream());
     if (rc == GDSLLM_ERR_UNSUPPORTED) return std::nullopt;  // the caller runs the separate launches
     check(rc, where);
     return out;
@@ -493,7 +522,7 @@ torch::Tensor fused_dequant_gemm(const Handle& h, torch::Tensor x, std::vector<i
     out_shape.back() = out_dim;
     torch::Tensor out = torch::empty(out_shape, fp16_on(h->device_id()));
     check(gdsllm_dequant_gemm_q4_0(at_offset(h, offset), xf.data_ptr(), out.data_ptr(), out_dim, in_dim, tokens,
-                                   in_dim, out_dim, stream_of(h->device_id())),
+                                   in_dim, out_dim, OnDevice(h->device_id()).stream()),
           where);
     return out;
 }
@@ -524,7 +553,7 @@ torch::Tensor gemv_f16(torch::Tensor weight, torch::Tensor x) {
         const int64_t nb = std::min<int64_t>(8, rows - r0);
         check(gdsllm_gemv_f16(w.data_ptr(), static_cast<const at::Half*>(xf.data_ptr()) + r0 * in_dim,
                               static_cast<at::Half*>(out.data_ptr()) + r0 * out_dim, out_dim, in_dim, nb, in_dim,
-                              out_dim, stream_of(dev)),
+                              out_dim, OnDevice(dev).stream()),
               where);
     }
     return out;
@@ -560,7 +589,7 @@ torch::Tensor dequant_int8(torch::Tensor weight, torch::Tensor scale, c10::optio
         out = torch::empty(w.sizes(), s.options());
     }
     check(gdsllm_dequant_int8(w.data_ptr(), s.data_ptr(), out.data_ptr(), w.size(0), w.size(1),
-                              stream_of(w.get_device())),
+                              OnDevice(w.get_device()).stream()),
           where);
     return out;
 }
@@ -593,7 +622,7 @@ torch::Tensor int8_linear(torch::Tensor weight, torch::Tensor scale, torch::Tens
     torch::Tensor out = torch::empty(out_shape, xf.options());
     if (rows == 0) return out;
     check(gdsllm_fused_int8_gemv(w.data_ptr(), s.data_ptr(), xf.data_ptr(), out.data_ptr(), out_dim, in_dim, rows,
-                                 in_dim, out_dim, stream_of(w.get_device())),
+                                 in_dim, out_dim, OnDevice(w.get_device()).stream()),
           where);
     return out;
 }
@@ -608,7 +637,7 @@ py::tuple moe_route_topk(torch::Tensor logits, int64_t top_k) {
     torch::Tensor idx = torch::empty(shape, l.options().dtype(torch::kInt32));
     torch::Tensor w = torch::empty(shape, l.options());
     check(gdsllm_moe_route_topk(l.data_ptr(), E, n, E, top_k, idx.data_ptr<int32_t>(), w.data_ptr(),
-                                stream_of(l.get_device())),
+                                OnDevice(l.get_device()).stream()),
           where);
     return py::make_tuple(idx, w);
 }
@@ -623,7 +652,7 @@ torch::Tensor moe_combine(torch::Tensor expert_out, torch::Tensor shared_out, to
     const int64_t H = e.size(-1), n = H ? e.numel() / H : 0;
     if (g.numel() != n) throw std::runtime_error(std::string(where) + ": one gate logit per row expected");
     torch::Tensor y = torch::empty_like(e);
-    check(gdsllm_moe_combine(e.data_ptr(), s.data_ptr(), g.data_ptr(), y.data_ptr(), H, n, stream_of(e.get_device())),
+    check(gdsllm_moe_combine(e.data_ptr(), s.data_ptr(), g.data_ptr(), y.data_ptr(), H, n, OnDevice(e.get_device()).stream()),
           where);
     return y;
 }

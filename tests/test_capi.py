@@ -75,7 +75,7 @@ def test_affine_gemv_validation():
     assert fn(16, 16, 16, 16, 16, 4, 96, 64, 1, 96, 4, None) == 1 and "group_size" in _err()
     assert fn(16, 16, 16, 16, 16, 4, 64, 12, 1, 64, 4, None) == 1
     assert fn(16, 16, 16, 16, 16, 4, 64, 64, 9, 64, 4, None) == 1
-    assert fn(16, 16, 16, 16, 16, 4, 64, 64, 1, 64, 4, None) != 0 or True  # valid shape: not called (no GPU)
+    assert fn(16, 16, 16, 16, None, 4, 64, 64, 1, 64, 4, None) == 1 and "null" in _err()  # y missing
     assert fn(None, None, None, None, None, 0, 64, 64, 1, 64, 0, None) == 0
 
 
@@ -298,3 +298,14 @@ def test_route_and_combine_validation():
     assert lib.gdsllm_moe_combine(16, 16, 16, 16, 0, 1, None) == 0
     assert lib.gdsllm_moe_combine(16, None, 16, 16, 8, 1, None) == 1 and "null" in _err()
     assert lib.gdsllm_moe_combine(16, 17, 16, 16, 8, 1, None) == 1 and "aligned" in _err()
+
+
+def test_measurement_helpers_validation():
+    lib = capi()
+    assert lib.gdsllm_read_stream(16, 64, 0, 1, 16, None) == 1 and "workgroups" in _err()
+    assert lib.gdsllm_read_stream(16, -16, 4, 1, 16, None) == 1
+    assert lib.gdsllm_read_stream(None, 0, 4, 1, None, None) == 0  # nothing to read
+    assert lib.gdsllm_read_stream(None, 64, 4, 1, 16, None) == 1 and "null" in _err()
+    assert lib.gdsllm_read_stream(16, 40, 4, 1, 16, None) == 1 and "aligned" in _err()
+    assert lib.gdsllm_read_stream(8, 64, 4, 1, 16, None) == 1 and "aligned" in _err()
+    assert lib.gdsllm_empty_launch(0, None) == 1 and "workgroups" in _err()

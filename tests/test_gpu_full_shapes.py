@@ -1,0 +1,86 @@
+"""Parity at the benchmark configurations' own shapes, where the launch
+geometry and the kernel chosen differ from the smaller test shapes:
+
+* the LLaMA-70B layer projections (q/o 8192x8192, k/v 1024x8192, gate/up
+  28672x8192, down 8192x28672) at batch 1, 2, 4 and 8;
+* the LLaMA-7B lm_head 32000x4096 as the batch-1 GEMV and as the 512-token
+  prefill GEMM, and the 512-token GEMMs of gate/up 11008x4096 and down
+  4096x11008.
+
+Weights are generated on the device (same distributions as the benchmark);
+the whole matrix is multiplied, and a seeded sample of 512 output rows (every
+row when there are at most 1024) is checked against the oracle's float64
+product over those rows' exact dequantized weights, under the GEMV tolerance
+(relative L2 <= 2e-3, per-row error <= 1e-2 of ||w_r * x||).  Every output
+must be finite.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_gemv_close, capi, check, oq, ptr, stream, syn, to_np
+
+pytestmark = pytest.mark.gpu
+
+LAYER_70B = [(8192, 8192), (1024, 8192), (28672, 8192), (8192, 28672)]
+
+
+def _weights(M, K, seed, dev):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    return syn.q4_0_weights(M, K, g)
+
+
+def _sample_rows(M, seed, n=512):
+    if M <= 1024:
+        return np.arange(M)
+    return np.sort(np.random.default_rng(seed).choice(M, n, replace=False))
+
+
+def _check_rows(y, w, x, rows, K, what):
+    yn = to_np(y).astype(np.float32)
+    assert np.isfinite(yn).all(), f"{what}: non-finite output"
+    deq = oq.dequant_q4_0(to_np(w[torch.as_tensor(rows, device=w.device)])).reshape(len(rows), K)
+    rel, mx = assert_gemv_close(yn[:, rows].astype(np.float16), deq, to_np(x), what)
+    print(f"{what}: rel_l2={rel:.2e} max_norm={mx:.2e}")
+
+
+@pytest.mark.parametrize("B", [1, 2, 4, 8])
+@pytest.mark.parametrize("M,K", LAYER_70B, ids=[f"{m}x{k}" for m, k in LAYER_70B])
+def test_q4_0_gemv_70b_layer_shapes(gpu, M, K, B):
+    seed = 3000 + M // 1024 + K // 1024 + B
+    w = _weights(M, K, seed, gpu)
+    x = syn.activations(B, K, torch.Generator().manual_seed(seed + 1))
+    xd = x.to(gpu)
+    y = torch.empty(B, M, dtype=torch.float16, device=gpu)
+    check(capi().gdsllm_fused_q4_0_gemv(ptr(w), ptr(xd), ptr(y), M, K, B, K, M, stream()))
+    torch.cuda.synchronize()
+    _check_rows(y, w, x, _sample_rows(M, seed), K, f"70B {M}x{K} B={B}")
+
+
+def test_q4_0_lm_head_gemv(gpu):
+    """LLaMA-7B lm_head 32000x4096 at batch 1 (the last GEMV of a decode step)."""
+    M, K = 32000, 4096
+    w = _weights(M, K, 3101, gpu)
+    x = syn.activations(1, K, torch.Generator().manual_seed(3102))
+    xd = x.to(gpu)
+    y = torch.empty(1, M, dtype=torch.float16, device=gpu)
+    check(capi().gdsllm_fused_q4_0_gemv(ptr(w), ptr(xd), ptr(y), M, K, 1, K, M, stream()))
+    torch.cuda.synchronize()
+    _check_rows(y, w, x, _sample_rows(M, 3101), K, "lm_head B=1")
+
+
+PREFILL_7B = [(32000, 4096), (11008, 4096), (4096, 11008)]
+
+
+@pytest.mark.parametrize("M,K", PREFILL_7B, ids=[f"{m}x{k}" for m, k in PREFILL_7B])
+def test_q4_0_prefill_gemm_512_tokens(gpu, M, K):
+    T = 512
+    seed = 3200 + M // 1024 + K // 1024
+    w = _weights(M, K, seed, gpu)
+    x = syn.activations(T, K, torch.Generator().manual_seed(seed + 1))
+    xd = x.to(gpu)
+    y = torch.empty(T, M, dtype=torch.float16, device=gpu)
+    check(capi().gdsllm_dequant_gemm_q4_0(ptr(w), ptr(xd), ptr(y), M, K, T, K, M, stream()))
+    torch.cuda.synchronize()
+    _check_rows(y, w, x, _sample_rows(M, seed), K, f"prefill T{T} {M}x{K}")

@@ -98,7 +98,8 @@ def test_moe_step_matches_separate_launches(gpu, E, H, F, k):
     ref = oq.moe_combine(eo.astype(np.float16)[None], so.astype(np.float16)[None], gl).astype(np.float64)
     got = to_np(y).astype(np.float64)
     rel = float(np.linalg.norm(got - ref.reshape(-1)) / np.linalg.norm(ref))
-    assert np.all(np.isfinite(got)) and rel <= 5e-3, f"rel L2 {rel:.3e}"
+    print(f"moe step E{E} H{H} F{F} k{k}: rel L2 {rel:.2e}")
+    assert np.all(np.isfinite(got)) and rel <= oq.GEMV_REL_L2, f"rel L2 {rel:.3e}"
 
 
 def test_moe_step_invalid_indices_and_clamp(gpu):

@@ -78,5 +78,5 @@ def test_runtime_moe_mlp_decode(gpu, E, H, F, Fs, g, k):
     want = oq.moe_combine(eo[None, :], so[None, :], gl).astype(np.float64).reshape(-1)
     got = to_np(y).astype(np.float64).reshape(-1)
     rel = float(np.linalg.norm(got - want) / np.linalg.norm(want))
-    assert np.all(np.isfinite(got)) and rel <= 5e-3, f"runtime MoE MLP rel L2 {rel:.3e}"
     print(f"runtime moe rel={rel:.2e}")
+    assert np.all(np.isfinite(got)) and rel <= oq.GEMV_REL_L2, f"runtime MoE MLP rel L2 {rel:.3e}"

@@ -161,6 +161,24 @@ def test_q4_0_matches_exact_rounding():
                 assert int(g[j]) == to_f16_bits(v), (i, j)
 
 
+def test_cpu_baseline_dequant_is_the_oracle_bit_for_bit():
+    """The torch restatement timed as the CPU baseline dequantizes exactly as
+    the oracle does (same bits, signed zeros and special scales included), and
+    its GEMV is the fp32 product of those weights."""
+    from oracle import cpu_baseline
+
+    raw = _random_q4_blocks(256, 11)
+    got = cpu_baseline.dequant_q4_0(torch.from_numpy(raw.copy())).numpy().view(np.uint16)
+    assert np.array_equal(got, oq.dequant_q4_0(raw).view(np.uint16))
+    M, K, B = 24, 256, 2
+    w = syn.q4_0_weights(M, K, torch.Generator().manual_seed(12))
+    x = syn.activations(B, K, torch.Generator().manual_seed(13))
+    y = cpu_baseline.q4_0_gemv(w, x, M, K).numpy()
+    deq = oq.dequant_q4_0(w.numpy()).reshape(M, K)
+    rel, mx = oq.gemv_errors(y.astype(np.float64), oq.gemv(deq, x.numpy()), oq.row_norms(deq, x.numpy()))
+    assert rel <= oq.GEMV_REL_L2 and mx <= oq.GEMV_MAX_NORM
+
+
 def test_q8_0_matches_exact_rounding():
     rng = np.random.default_rng(2)
     n = 64

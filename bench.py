@@ -94,7 +94,29 @@ class Q4Gemv:
         self.check(self.lib.gdsllm_fused_q4_0_gemv(w.data_ptr(), x.data_ptr(), y.data_ptr(), m, k, 1, k, m, s))
 
 
+def _gpu_delay() -> None:
+    """Keeps the GPU busy for a few milliseconds so that everything enqueued
+    after it (the start event, the graph replays, the end event) is queued
+    before the GPU reaches the start event: the timed region then holds GPU
+    time only, not host enqueue latency."""
+    import torch
+
+    torch.cuda._sleep(5_000_000)
+
+
+def _capture(fn):
+    import torch
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    return graph
+
+
 def bench_gemv(args, dev):
+    """Exactly `steps` launches, all replayed from HIP graphs: steps // c
+    replays of a graph of c = min(steps, chunk) launches, then one graph of the
+    remaining steps % c launches."""
     import torch
 
     from gdsllm_amd import synthetic as syn
@@ -109,26 +131,32 @@ def bench_gemv(args, dev):
         gemv(copies[i % n], x, ys[i % n], M0, K0)
     torch.cuda.synchronize()
 
-    chunk = args.chunk
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for i in range(chunk):
-            gemv(copies[i % n], x, ys[i % n], M0, K0)
-    graph.replay()
+    K = args.steps
+    c = min(K, args.chunk)
+    reps, rem = divmod(K, c)
+
+    def launches(count):
+        return lambda: [gemv(copies[i % n], x, ys[i % n], M0, K0) for i in range(count)]
+
+    full = _capture(launches(c))
+    tail = _capture(launches(rem)) if rem else None
+    full.replay()
+    if tail is not None:
+        tail.replay()
     torch.cuda.synchronize()
 
-    K = args.steps
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
+    _gpu_delay()
     start.record()
-    for _ in range(K // chunk):
-        graph.replay()
-    for i in range(K % chunk):
-        gemv(copies[i % n], x, ys[i % n], M0, K0)
+    for _ in range(reps):
+        full.replay()
+    if tail is not None:
+        tail.replay()
     end.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(end)
-    return {"ms": ms, "weights0": copies[0], "x": x, "y0": ys[0].clone()}
+    return {"ms": ms, "launches_timed": reps * c + rem, "graph_launches": c, "weights0": copies[0], "x": x,
+            "y0": ys[0].clone()}
 
 
 def bench_decode_sweep(args, dev):
@@ -191,13 +219,12 @@ def _replay_ms(capture, reps: int, warm: int = 3) -> float:
 
     capture()
     torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        capture()
+    graph = _capture(capture)
     for _ in range(warm):
         graph.replay()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    _gpu_delay()
     start.record()
     for _ in range(reps):
         graph.replay()
@@ -282,7 +309,7 @@ def bench_int8_layer(dev, layers_rotated: int = 2, reps: int = 50, ref_reps: int
             "layers_rotated": layers_rotated, "reference_expression_us_per_layer": round(ref_ms * 1e3, 1)}
 
 
-def bench_moe(dev, calls: int = 64, reps: int = 20):
+def bench_moe(dev, calls: int = 64, reps: int = 20, decode_step: bool = True):
     """Affine-Q4 top-10 expert-gather MLP, 512 experts, hidden 4096, ffn 1024,
     group 64, batch 1; every call in the graph uses its own fresh random
     distinct top-10 picks from the 3.6 GB resident pool."""
@@ -327,6 +354,8 @@ def bench_moe(dev, calls: int = 64, reps: int = 20):
     out = {"us_per_call": round(ms * 1e3, 3), "bytes_per_call": nbytes,
            "GB_s": round(nbytes / (ms * 1e-3) / 1e9, 1), "pct_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / 80, 1),
            "launches_per_call": 2, "pool_bytes": sum(t.numel() * t.element_size() for p in pools for t in p)}
+    if not decode_step:
+        return out
 
     # The whole decode MoE step on the device, no host round trip: fp16 router
     # GEMV (512 x 4096), top-k + softmax, the top-10 gather, the shared expert
@@ -409,6 +438,55 @@ def bench_moe(dev, calls: int = 64, reps: int = 20):
     return out
 
 
+def bench_ceiling(dev, copies: int = 16, calls: int = 64, reps: int = 10):
+    """What one launch can do on this device, for the headline's size:
+    a plain read of 25,392,640 B (the headline call's algorithmic bytes,
+    rotating over `copies` slices of one 406 MB buffer, as the headline
+    rotates its weights) at several grid sizes, one launch reading all 406 MB,
+    and the time per launch of an empty kernel, all back to back in HIP graphs."""
+    import torch
+
+    from gdsllm_amd import capi, check
+
+    lib = capi()
+    nb = ALGO_BYTES_CFG0
+    buf = torch.randint(0, 256, (copies * nb,), dtype=torch.uint8, device=dev,
+                        generator=torch.Generator(device=dev).manual_seed(1010))
+    sink = torch.zeros(1 << 16, dtype=torch.int32, device=dev)
+    key = 0x9E3779B9
+
+    def read_ms(nbytes, wg, n, rot):
+        def run():
+            st = torch.cuda.current_stream().cuda_stream
+            for i in range(n):
+                check(lib.gdsllm_read_stream(buf.data_ptr() + (i % rot) * nbytes, nbytes, wg, key, sink.data_ptr(),
+                                             st))
+        return _replay_ms(run, reps) / n
+
+    by_wg = {wg: read_ms(nb, wg, calls, copies) * 1e3 for wg in (1024, 2048, 4096, 8192)}
+    best_wg = min(by_wg, key=by_wg.get)
+    us = by_wg[best_wg]
+    whole = {wg: read_ms(copies * nb, wg, 4, 1) * 1e3 for wg in (4096, 16384, 65536)}
+    best_whole = min(whole, key=whole.get)
+
+    def empty_us(wg):
+        def run():
+            st = torch.cuda.current_stream().cuda_stream
+            for _ in range(calls):
+                check(lib.gdsllm_empty_launch(wg, st))
+        return _replay_ms(run, reps) / calls * 1e3
+
+    return {"read_25MB": {"bytes": nb, "us": round(us, 3), "GB_s": round(nb / (us * 1e-6) / 1e9, 1),
+                          "frac_of_peak": round(nb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "workgroups": best_wg,
+                          "us_by_workgroups": {str(k): round(v, 3) for k, v in by_wg.items()}},
+            "read_406MB_one_launch": {"bytes": copies * nb, "us": round(whole[best_whole], 2),
+                                      "GB_s": round(copies * nb / (whole[best_whole] * 1e-6) / 1e9, 1),
+                                      "workgroups": best_whole},
+            "empty_launch_us": {"256_workgroups": round(empty_us(256), 3), "2048_workgroups": round(empty_us(2048), 3)},
+            "method": "16-byte non-temporal loads, 256-thread workgroups, grid-stride, 4 loads in flight per thread; "
+                      "graph replays between HIP events"}
+
+
 LAYER_70B = [(8192, 8192), (1024, 8192), (1024, 8192), (8192, 8192), (28672, 8192), (28672, 8192), (8192, 28672)]
 
 
@@ -464,9 +542,41 @@ def bench_prefill(dev, layers, lm_head, tokens: int = 512, reps: int = 3):
 
     ms = _replay_ms(run, reps, warm=1)
     flops = 2 * tokens * (N_LAYERS * sum(m * k for m, k in LAYER_SHAPES) + LM_HEAD[0] * LM_HEAD[1])
+
+    # Per shape: the fused kernel against the reference's route, the bit-exact
+    # dequant into an fp16 scratch matrix followed by the vendor GEMM
+    # (hipBLASLt through torch.mm), runtime/llama.py:160-166.
+    lib = capi()
+    per_shape = {}
+    shapes = [((4096, 4096), layers[0][0]), ((11008, 4096), layers[0][4]), ((4096, 11008), layers[0][6]),
+              (LM_HEAD, lm_head)]
+    for (m, k), w in shapes:
+        wdq = torch.empty(m, k, dtype=torch.float16, device=dev)
+        yr = torch.empty(tokens, m, dtype=torch.float16, device=dev)
+
+        def fused():
+            gemm(w, m, k)
+
+        def dequant():
+            check(lib.gdsllm_dequant_q4_0(w.data_ptr(), wdq.data_ptr(), m * k // 32,
+                                          torch.cuda.current_stream().cuda_stream))
+
+        def matmul():
+            torch.mm(xs[k], wdq.t(), out=yr)
+
+        def route():
+            dequant()
+            matmul()
+
+        f_us, d_us, mm_us, r_us = (_replay_ms(fn, 20) * 1e3 for fn in (fused, dequant, matmul, route))
+        fl = 2 * tokens * m * k
+        per_shape[f"{m}x{k}"] = {"fused_us": round(f_us, 2), "fused_TFLOP_s": round(fl / (f_us * 1e-6) / 1e12, 1),
+                                 "dequant_then_hipblaslt_us": round(r_us, 2), "dequant_us": round(d_us, 2),
+                                 "hipblaslt_fp16_gemm_us": round(mm_us, 2), "fused_faster": bool(f_us < r_us)}
+        del wdq, yr
     return {"ms_per_chunk": round(ms, 3), "tokens": tokens, "tok_s": round(tokens / (ms * 1e-3), 1),
             "TFLOP_s": round(flops / (ms * 1e-3) / 1e12, 1), "flop_per_chunk": flops,
-            "pct_of_fp16_dense_peak": round(flops / (ms * 1e-3) / 1e12 / 25, 1)}
+            "pct_of_fp16_dense_peak": round(flops / (ms * 1e-3) / 1e12 / 25, 1), "per_shape": per_shape}
 
 
 def bench_load(dev, layers: int = 2, reps: int = 3, tokens: int = 512, emb_reps: int = 20):
@@ -527,41 +637,119 @@ def bench_load(dev, layers: int = 2, reps: int = 3, tokens: int = 512, emb_reps:
         shutil.rmtree(d, ignore_errors=True)
 
 
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
+def _median_s(fn, seconds: float, min_runs: int = 10, max_runs: int = 200, warm: int = 2) -> tuple[float, int]:
+    """Median wall time of fn() over at least min_runs timed runs after `warm`
+    untimed ones, continuing while the time budget lasts (at most max_runs)."""
+    for _ in range(warm):
+        fn()
+    times, t_all = [], time.perf_counter()
+    while len(times) < min_runs or (time.perf_counter() - t_all < seconds and len(times) < max_runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
 def cpu_baseline(weights_dev, x_dev, y_gpu, seconds: float):
-    """Oracle-side torch restatement of dequant -> F.linear (fp32) on the host
-    cores, timed over a bounded number of calls; also checks the GPU result."""
+    """Oracle-side torch restatement of the reference's route for one Q4_0
+    projection (bit-exact dequant, then F.linear in fp32) on the host cores:
+    dequant-only and dequant + matmul timed separately as medians of >= 10 runs
+    after 2 warm-ups; also checks the GPU result against the oracle.  Threads:
+    os.cpu_count(), limited to the cores this process may run on and to
+    OMP_NUM_THREADS when set (the host share a one-GPU job is given)."""
     import numpy as np
     import torch
 
     from oracle import cpu_baseline as cb
     from oracle import quant as oq
 
-    w = weights_dev.cpu()
-    x = x_dev.cpu()
-    y_cpu = cb.q4_0_gemv(w, x, M0, K0)  # warm-up
-    calls, t0 = 0, time.perf_counter()
-    while True:
-        cb.q4_0_gemv(w, x, M0, K0)
-        calls += 1
-        el = time.perf_counter() - t0
-        if (el >= seconds and calls >= 3) or calls >= 200:
-            break
-    per_call = el / calls
+    ncpu = os.cpu_count() or 1
+    allowed = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else ncpu
+    threads = min(ncpu, allowed)
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        threads = min(threads, max(1, int(os.environ["OMP_NUM_THREADS"])))
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        w = weights_dev.cpu()
+        x = x_dev.cpu()
+        deq_s, deq_runs = _median_s(lambda: cb.dequant_q4_0(w), seconds / 3)
+        tot_s, tot_runs = _median_s(lambda: cb.q4_0_gemv(w, x, M0, K0), seconds * 2 / 3)
+        used = torch.get_num_threads()
+        y_cpu = cb.q4_0_gemv(w, x, M0, K0)
+    finally:
+        torch.set_num_threads(prev)
     deq = cb.dequant_q4_0(w).view(M0, K0).numpy()
     xn = x.numpy()
     ref, norms = oq.gemv(deq, xn), oq.row_norms(deq, xn)
     rel, mx = oq.gemv_errors(y_gpu.cpu().numpy().astype(np.float64), ref, norms)
     rel_c, _ = oq.gemv_errors(y_cpu.numpy().astype(np.float64), ref, norms)
     return {
-        "value": round(ALGO_BYTES_CFG0 / per_call / 1e9, 3),
+        "value": round(ALGO_BYTES_CFG0 / tot_s / 1e9, 3),
         "unit": "GB/s",
-        "us_per_call": round(per_call * 1e6, 1),
-        "cores": torch.get_num_threads(),
+        "us_per_call": round(tot_s * 1e6, 1),
+        "dequant_only_us": round(deq_s * 1e6, 1),
+        "cores": used,
+        "os_cpu_count": ncpu,
+        "cpus_allowed": allowed,
+        "torch_threads": used,
+        "cpu_model": _cpu_model(),
         "kind": "port",
-        "sample": f"{calls} calls of the 11008x4096 Q4_0 b=1 GEMV (bit-exact torch dequant + fp32 F.linear), "
-                  f"one weight copy, {el:.1f} s",
+        "sample": f"11008x4096 Q4_0 b=1 GEMV (bit-exact torch dequant, then fp32 F.linear, fp16 out), one weight "
+                  f"copy: median of {tot_runs} calls (dequant alone: median of {deq_runs}) after 2 warm-ups",
     }, {"gpu_rel_l2": rel, "gpu_max_norm": mx, "cpu_rel_l2": rel_c,
         "ok": bool(rel <= oq.GEMV_REL_L2 and mx <= oq.GEMV_MAX_NORM)}
+
+
+def profile_case(case: str, reps: int, dev) -> int:
+    """One workload launched `reps` times eagerly (no graph), for a profiler's
+    kernel trace or counters; prints one JSON line and returns 0."""
+    import torch
+
+    from gdsllm_amd import capi, check
+    from gdsllm_amd import synthetic as syn
+
+    kind, _, spec = case.partition(":")
+    st = torch.cuda.current_stream().cuda_stream
+    gen = torch.Generator(device=dev).manual_seed(1020)
+    if kind in ("gemm", "gemv"):
+        m, k, t = (int(v) for v in spec.split(","))
+        w = syn.q4_0_weights(m, k, gen)
+        x = syn.activations(t, k, gen)
+        y = torch.empty(t, m, dtype=torch.float16, device=dev)
+        fn = capi().gdsllm_dequant_gemm_q4_0 if kind == "gemm" else capi().gdsllm_fused_q4_0_gemv
+        launch = lambda: check(fn(w.data_ptr(), x.data_ptr(), y.data_ptr(), m, k, t, k, m, st))  # noqa: E731
+    elif kind == "moe":
+        res = bench_moe(dev, calls=reps, reps=1, decode_step=False)
+        print(json.dumps({"profile_case": case, "calls": reps, "us_per_call": res["us_per_call"]}), flush=True)
+        return 0
+    else:
+        print(f"bench.py: unknown --profile-case {case!r}", file=sys.stderr)
+        return 2
+    launch()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        launch()
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    print(json.dumps({"profile_case": case, "launches": reps, "wall_us_per_launch": round(el * 1e6 / reps, 2)}),
+          flush=True)
+    return 0
 
 
 def main() -> int:
@@ -573,8 +761,13 @@ def main() -> int:
     ap.add_argument("--chunk", type=int, default=64, help="launches per captured graph")
     ap.add_argument("--sweep-tokens", type=int, default=100, help="timed 7B decode-sweep tokens (0 = skip)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget (0 = skip)")
-    ap.add_argument("--configs", default="q8,moe,70b,prefill,load,int8",
-                    help="comma list of extra workloads to measure: q8 (Q8_0 7B layer), moe (top-10 expert "
+    ap.add_argument("--profile-case", default="",
+                    help="run only one workload, eagerly, for a profiler: gemm:M,K,T (Q4_0 prefill GEMM), "
+                         "gemv:M,K,B (Q4_0 GEMV), moe (top-10 gather, fresh picks per call); then exit")
+    ap.add_argument("--profile-reps", type=int, default=10, help="launches of --profile-case")
+    ap.add_argument("--configs", default="ceiling,q8,moe,70b,prefill,load,int8",
+                    help="comma list of extra workloads to measure: ceiling (plain read of the headline's bytes, "
+                         "empty launch), q8 (Q8_0 7B layer), moe (top-10 expert "
                          "gather), 70b (Q4_0 70B layer, B=1..8), prefill (512-token MFMA GEMM), load (7B layer "
                          "file -> HBM, embedding row gather), int8 (per-column int8 7B layer); '' = none")
     args = ap.parse_args()
@@ -595,10 +788,12 @@ def main() -> int:
         print("bench.py: no HIP device visible", file=sys.stderr)
         return 1
     dev = torch.device("cuda:0")
+    if args.profile_case:
+        return profile_case(args.profile_case, args.profile_reps, dev)
 
     g = bench_gemv(args, dev)
     ms_total = g["ms"]
-    us_per_call = ms_total * 1e3 / args.steps
+    us_per_call = ms_total * 1e3 / g["launches_timed"]
     gbs = ALGO_BYTES_CFG0 / (us_per_call * 1e-6) / 1e9
     print(f"# q4_0 gemv 11008x4096 b=1: {us_per_call:.3f} us/call, {gbs:.1f} GB/s "
           f"({100 * gbs / HBM_PEAK_GBS:.1f}% of {HBM_PEAK_GBS:.0f})", file=sys.stderr, flush=True)
@@ -616,12 +811,13 @@ def main() -> int:
               f"(unfused 225 launches: {sweep['unfused']['tok_s']} tok/s)", file=sys.stderr, flush=True)
 
     wanted = {c.strip() for c in args.configs.split(",") if c.strip()}
-    unknown = wanted - {"q8", "moe", "70b", "prefill", "load", "int8"}
+    unknown = wanted - {"ceiling", "q8", "moe", "70b", "prefill", "load", "int8"}
     if unknown:
         print(f"bench.py: unknown --configs entries {sorted(unknown)}", file=sys.stderr)
         return 2
     configs = {}
-    runs = [("q8", "q8_0_layer_7b_b1", lambda: bench_q8_layer(dev)),
+    runs = [("ceiling", "ceiling_single_launch", lambda: bench_ceiling(dev, args.copies)),
+            ("q8", "q8_0_layer_7b_b1", lambda: bench_q8_layer(dev)),
             ("moe", "moe_affine_q4_top10", lambda: bench_moe(dev)),
             ("70b", "q4_0_layer_70b", lambda: bench_70b_layer(dev)),
             ("prefill", "prefill_7b_512",
@@ -650,14 +846,15 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_total / args.steps, 6),
+        "ms_per_step": round(ms_total / g["launches_timed"], 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "q4_0->fp16, fp32 acc",
         "data": "synthetic",
         "config": {"workload": "GGUF Q4_0 fused dequant+GEMV, W 11008x4096 (LLaMA-7B gate_proj), batch 1",
-                   "weight_copies_rotated": args.copies, "graph_chunk": args.chunk,
+                   "weight_copies_rotated": args.copies, "graph_launches": g["graph_launches"],
+                   "launches_timed": g["launches_timed"],
                    "algorithmic_bytes_per_step": ALGO_BYTES_CFG0},
         "us_per_call": round(us_per_call, 3),
         "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),

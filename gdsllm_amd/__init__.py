@@ -60,6 +60,8 @@ SIGNATURES = {
     "gdsllm_gemv_f16": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp]),
     "gdsllm_moe_route_topk": (ctypes.c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp]),
     "gdsllm_moe_combine": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
+    "gdsllm_read_stream": (ctypes.c_int, [_c_vp, _c_i64, _c_i64, ctypes.c_uint32, _c_vp, _c_vp]),
+    "gdsllm_empty_launch": (ctypes.c_int, [_c_i64, _c_vp]),
 }
 
 _LIB = None

@@ -260,6 +260,17 @@ int gdsllm_dequant_gemm_q4_0(const void* weight, const void* x, void* y,
                              int64_t out_dim, int64_t in_dim, int64_t tokens,
                              int64_t ldx, int64_t ldy, void* stream);
 
+/* ------------------------------------------------------ measurement helpers --
+ * Not on the matvec path and with no counterpart in the reference: reference
+ * kernels the benchmark measures the GEMV against on the same device.
+ * gdsllm_read_stream reads `bytes` at src once (16-byte non-temporal loads,
+ * `workgroups` workgroups of 256 threads) and discards the data; sink must
+ * hold `workgroups` uint32 (written only when a workgroup's XOR of its data
+ * equals `key`).  gdsllm_empty_launch launches a kernel with no work.       */
+int gdsllm_read_stream(const void* src, int64_t bytes, int64_t workgroups, uint32_t key, void* sink,
+                       void* stream);
+int gdsllm_empty_launch(int64_t workgroups, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -309,3 +309,4 @@ def test_measurement_helpers_validation():
     assert lib.gdsllm_read_stream(16, 40, 4, 1, 16, None) == 1 and "aligned" in _err()
     assert lib.gdsllm_read_stream(8, 64, 4, 1, 16, None) == 1 and "aligned" in _err()
     assert lib.gdsllm_empty_launch(0, None) == 1 and "workgroups" in _err()
+

@@ -25,6 +25,8 @@
 
 #include <type_traits>
 
+#include <mutex>
+
 #include "common.h"
 
 namespace gdsllm {
@@ -1091,11 +1093,48 @@ static int check_experts(const gdsllm_affine_experts* p, const char* what, std::
     return 0;
 }
 
-extern "C" int gdsllm_moe_gather_affine_q4(const gdsllm_affine_experts* gate, const gdsllm_affine_experts* up,
-                                           const gdsllm_affine_experts* down, const void* x, const int32_t* idx,
-                                           const void* routing_weights, int64_t top_k, void* y, void* workspace,
-                                           size_t workspace_bytes, void* stream) {
-    const std::string n = "moe_gather_affine_q4";
+// ---- the same gather without a caller workspace ---------------------------------
+// For callers that cannot allocate device memory (code under HIP graph
+// capture, serving loops, harnesses that forbid it): the gather's gate/up/h
+// workspace is a fixed device array of kNoAllocScratchBytes instead.  Each
+// device the library runs on holds its own copy of the array until the process
+// ends; its address on a device is looked up once, with that device current,
+// and cached.  Phase 1 writes every workspace entry phase 2 reads, so nothing
+// is cleared and a call does not depend on what an earlier call left there.
+// Calls that overlap on one device (several streams, several host threads)
+// share the array and race: they must be ordered by the caller.
+constexpr size_t kNoAllocScratchBytes = size_t(1) << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+static std::mutex g_scratch_mutex;
+static void* g_scratch_ptr[kMaxScratchDevices];
+
+// Device address of `scratch` on the current device.
+static int scratch_on_current_device(void** out) {
+    int dev = 0;
+    if (int rc = check_hip(hipGetDevice(&dev), "moe_gather_affine_q4_noalloc: hipGetDevice")) return rc;
+    if (dev < 0 || dev >= kMaxScratchDevices)
+        return set_error(GDSLLM_ERR_UNSUPPORTED, "moe_gather_affine_q4_noalloc: device index out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        if (int rc = check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)),
+                               "moe_gather_affine_q4_noalloc: hipGetSymbolAddress(scratch)"))
+            return rc;
+        if (!p) return set_error(GDSLLM_ERR_HIP, "moe_gather_affine_q4_noalloc: null scratch address");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return GDSLLM_OK;
+}
+
+// workspace == nullptr with fixed_ws: the fixed `scratch` array (looked up
+// after every argument check, so a rejected call makes no HIP call).
+static int moe_gather_impl(const std::string& n, const gdsllm_affine_experts* gate, const gdsllm_affine_experts* up,
+                           const gdsllm_affine_experts* down, const void* x, const int32_t* idx,
+                           const void* routing_weights, int64_t top_k, void* y, void* workspace,
+                           size_t workspace_bytes, void* stream, bool fixed_ws = false) {
     std::string err;
     if (check_experts(gate, "gate", err) || check_experts(up, "up", err) || check_experts(down, "down", err))
         return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": " + err);
@@ -1106,21 +1145,23 @@ extern "C" int gdsllm_moe_gather_affine_q4(const gdsllm_affine_experts* gate, co
         gate->group_size != up->group_size || up->num_experts != gate->num_experts ||
         down->num_experts != gate->num_experts)
         return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": gate/up [E,F,H] and down [E,H,F] shapes disagree");
-    if (!x || !idx || !routing_weights || !y || !workspace)
+    if (!x || !idx || !routing_weights || !y || (!workspace && !fixed_ws))
         return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": null pointer");
     if (reinterpret_cast<uintptr_t>(x) % 2 || reinterpret_cast<uintptr_t>(y) % 2 ||
         reinterpret_cast<uintptr_t>(routing_weights) % 2 || reinterpret_cast<uintptr_t>(idx) % 4 ||
         reinterpret_cast<uintptr_t>(workspace) % 16)
         return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": misaligned pointer");
     if (workspace_bytes < gdsllm_moe_gather_workspace_size(top_k, F))
-        return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": workspace too small (" + std::to_string(workspace_bytes) +
-                                                          " < " +
-                                                          std::to_string(gdsllm_moe_gather_workspace_size(top_k, F)) +
-                                                          ")");
+        return set_error(GDSLLM_ERR_INVALID_ARGUMENT,
+                         n + (fixed_ws ? ": top_k * ffn too large for the fixed workspace (" : ": workspace too small (") +
+                             std::to_string(gdsllm_moe_gather_workspace_size(top_k, F)) + " bytes needed, " +
+                             std::to_string(workspace_bytes) + " available)");
     const size_t budget = static_cast<size_t>(max_lds_bytes());
     const size_t lds1 = static_cast<size_t>(H / 32) * kRec, lds2 = static_cast<size_t>(top_k) * (F / 32) * kRec;
     if (lds1 > budget || lds2 > budget)
         return set_error(GDSLLM_ERR_UNSUPPORTED, n + ": hidden or top_k*ffn too large for LDS staging");
+    if (fixed_ws)
+        if (int rc = scratch_on_current_device(&workspace)) return rc;
     hipStream_t s = as_stream(stream);
     auto* gu = static_cast<uint16_t*>(workspace);
     const auto* xp = static_cast<const uint16_t*>(x);
@@ -1182,6 +1223,24 @@ extern "C" int gdsllm_moe_gather_affine_q4(const gdsllm_affine_experts* gate, co
     }
     if (int rc = check_hip(hipGetLastError(), "moe_down launch")) return rc;
     return ok();
+}
+
+extern "C" int gdsllm_moe_gather_affine_q4(const gdsllm_affine_experts* gate, const gdsllm_affine_experts* up,
+                                           const gdsllm_affine_experts* down, const void* x, const int32_t* idx,
+                                           const void* routing_weights, int64_t top_k, void* y, void* workspace,
+                                           size_t workspace_bytes, void* stream) {
+    return moe_gather_impl("moe_gather_affine_q4", gate, up, down, x, idx, routing_weights, top_k, y, workspace,
+                           workspace_bytes, stream);
+}
+
+extern "C" size_t gdsllm_moe_gather_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int gdsllm_moe_gather_affine_q4_noalloc(const gdsllm_affine_experts* gate, const gdsllm_affine_experts* up,
+                                                   const gdsllm_affine_experts* down, const void* x,
+                                                   const int32_t* idx, const void* routing_weights, int64_t top_k,
+                                                   void* y, void* stream) {
+    return moe_gather_impl("moe_gather_affine_q4_noalloc", gate, up, down, x, idx, routing_weights, top_k, y, nullptr,
+                           kNoAllocScratchBytes, stream, /*fixed_ws=*/true);
 }
 
 extern "C" int gdsllm_moe_step_affine_q4(const gdsllm_affine_experts* gate, const gdsllm_affine_experts* up,

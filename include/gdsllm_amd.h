@@ -198,6 +198,22 @@ int gdsllm_moe_gather_affine_q4(const gdsllm_affine_experts* gate,
                                 const void* routing_weights, int64_t top_k,
                                 void* y, void* workspace, size_t workspace_bytes,
                                 void* stream);
+/* The same gather with no workspace argument and no allocation of any kind:
+ * its gate/up/h workspace is a fixed device array of
+ * gdsllm_moe_gather_noalloc_max_bytes() bytes (1 MiB) inside the library, one
+ * per device, held until the process ends.  No counterpart in the reference;
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Rejects
+ * top_k * ffn_dim whose workspace (gdsllm_moe_gather_workspace_size) exceeds
+ * that size.  Calls that overlap on one device share the array and race: the
+ * caller orders them (one stream, or events between streams).               */
+size_t gdsllm_moe_gather_noalloc_max_bytes(void);
+int gdsllm_moe_gather_affine_q4_noalloc(const gdsllm_affine_experts* gate,
+                                        const gdsllm_affine_experts* up,
+                                        const gdsllm_affine_experts* down,
+                                        const void* x, const int32_t* idx,
+                                        const void* routing_weights, int64_t top_k,
+                                        void* y, void* stream);
 /* The whole decode MoE MLP of qwen_moe.py:455-513 after routing, in two
  * launches: the top_k routed experts and the shared expert (one-expert
  * descriptors shared_gate/shared_up [1][F][H], shared_down [1][H][F]) share

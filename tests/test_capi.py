@@ -310,3 +310,19 @@ def test_measurement_helpers_validation():
     assert lib.gdsllm_read_stream(8, 64, 4, 1, 16, None) == 1 and "aligned" in _err()
     assert lib.gdsllm_empty_launch(0, None) == 1 and "workgroups" in _err()
 
+
+def test_moe_gather_noalloc_validation():
+    """The scratch-backed gather rejects what its fixed 1 MiB workspace cannot
+    hold, and every argument error, before any HIP call."""
+    lib = capi()
+    assert lib.gdsllm_moe_gather_noalloc_max_bytes() == 1 << 20
+    H = 2048
+    big = [_experts(E=64, N=n, K=kk) for n, kk in ((4096, H), (4096, H), (H, 4096))]
+    rc = lib.gdsllm_moe_gather_affine_q4_noalloc(*(ctypes.byref(e) for e in big), 16, 16, 16, 64, 16, None)
+    assert rc == 1 and "fixed workspace" in _err()  # 64 * 3 * 4096 * 2 bytes > 1 MiB
+    ok_shape = [_experts(N=n, K=kk) for n, kk in ((1024, H), (1024, H), (H, 1024))]
+    call = lambda k=10, idx=16, x=16: lib.gdsllm_moe_gather_affine_q4_noalloc(  # noqa: E731
+        *(ctypes.byref(e) for e in ok_shape), x, idx, 16, k, 16, None)
+    assert call(k=0) == 1 and "top_k" in _err()
+    assert call(idx=18) == 1 and "misaligned" in _err()
+    assert call(x=None) == 1 and "null" in _err()

@@ -68,9 +68,11 @@ __device__ __forceinline__ uint4 load8h(const uint16_t* p, bool aligned16) {
 }
 
 // Records for NB rows of x (row b at X + b*ldx), `chunks` chunks each.
+// Returns whether this thread met an x that is not finite.
 template <int NB>
-__device__ void build_xprep_plain(uint8_t* xp, const uint16_t* __restrict__ X, int chunks, int64_t ldx, bool al16) {
+__device__ bool build_xprep_plain(uint8_t* xp, const uint16_t* __restrict__ X, int chunks, int64_t ldx, bool al16) {
     const int items = NB * chunks * 4;
+    bool nonfinite = false;
     for (int base = 0; base < items; base += kThreads) {
         const int it = base + threadIdx.x;
         const bool live = it < items;
@@ -88,10 +90,30 @@ __device__ void build_xprep_plain(uint8_t* xp, const uint16_t* __restrict__ X, i
             *reinterpret_cast<float*>(rec + 64) = corr;
             *reinterpret_cast<float*>(rec + 68) = sum;
         }
+        nonfinite |= live && !__builtin_isfinite(sum);
     }
+    return nonfinite;
 }
 
-// Dot of one 32-element chunk with its prepared record: s*(S - corr) + b*sum.
+// Exact nibbles: the unpacked pairs (1024 + q, 64 + q) enter the dot
+// products as q itself (one packed fp16 subtract per pair, exact), so the fp32
+// sum runs over nib * x with the reference's magnitudes; the chunk is then
+// s * sum(nib * x) + b * sum(x) and the offset correction drops out.  The
+// offset form sum((1024 + q) * x) - 1024 * sum(x) loses about 10 bits to
+// cancellation when one x dwarfs the rest (an activation near 65504).  A row
+// whose sum is not finite (an infinite or NaN x, where the factored form and
+// the reference's per-element (nib*s + b)*x differ) is recomputed by
+// affine_row_exact.
+constexpr bool kAffineExact = true;
+constexpr uint32_t kNeg1024 = 0xE400E400u;  // fp16 -1024 in both halves
+constexpr uint32_t kNeg64 = 0xD400D400u;    // -64
+__device__ __forceinline__ uint32_t unbias_nib(uint32_t a, uint32_t neg_bias_pair) {
+    if constexpr (!kAffineExact) return a;
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, a) + __builtin_bit_cast(half2_t, neg_bias_pair));
+}
+
+// Dot of one 32-element chunk with its prepared record: s*(S - corr) + b*sum
+// (s*S + b*sum with exact nibbles).
 __device__ __forceinline__ float chunk_dot(uint4 w, const uint8_t* rec, float s, float b) {
     const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
     float S = 0.f;
@@ -99,13 +121,33 @@ __device__ __forceinline__ float chunk_dot(uint4 w, const uint8_t* rec, float s,
     for (int q = 0; q < 4; ++q) {
         const uint4 xv = *reinterpret_cast<const uint4*>(rec + 16 * q);
         const uint32_t v = wd[q], vs = v >> 8;
-        S = dot2(nib_lo_pair(v), xv.x, S);
-        S = dot2(nib_hi_pair(v), xv.y, S);
-        S = dot2(nib_lo_pair(vs), xv.z, S);
-        S = dot2(nib_hi_pair(vs), xv.w, S);
+        S = dot2(unbias_nib(nib_lo_pair(v), kNeg1024), xv.x, S);
+        S = dot2(unbias_nib(nib_hi_pair(v), kNeg64), xv.y, S);
+        S = dot2(unbias_nib(nib_lo_pair(vs), kNeg1024), xv.z, S);
+        S = dot2(unbias_nib(nib_hi_pair(vs), kNeg64), xv.w, S);
     }
     const float2 cs = *reinterpret_cast<const float2*>(rec + 64);
-    return __builtin_fmaf(s, S - cs.x, b * cs.y);
+    return __builtin_fmaf(s, kAffineExact ? S : S - cs.x, b * cs.y);
+}
+
+// The reference's per-element arithmetic for one row (kernel_fused_affine_q4_gemv,
+// runtime/affine_q4_dequant.cu:118-128): sum over k of (nib*s + b)*x[k] in
+// fp32, one lane, serially.  The slow path for a row whose fast sum is not
+// finite, so that +-inf and NaN come out where the reference's do.
+__device__ __forceinline__ float affine_row_exact(const uint32_t* __restrict__ w, const uint16_t* __restrict__ s,
+                                               const uint16_t* __restrict__ b, const uint16_t* __restrict__ x, int K,
+                                               int gsize) {
+    float acc = 0.f;
+    for (int i = 0; i < K / 8; ++i) {
+        const uint32_t v = w[i];
+        const int G = (8 * i) / gsize;
+        const float sf = h2f(s[G]), bf = h2f(b[G]);
+        for (int n = 0; n < 8; ++n) {
+            const float val = fp32_rounded(static_cast<float>((v >> (4 * n)) & 15u) * sf + bf);
+            acc = __builtin_fmaf(val, h2f(x[8 * i + n]), acc);
+        }
+    }
+    return acc;
 }
 
 // Where one row of a GEMV lives and where its result goes.
@@ -125,6 +167,10 @@ struct PlainRows {
         return true;
     }
     __device__ void store(int bidx, int row, float v) const { Y[bidx * ldy + row] = f2h_bits(v); }
+    __device__ bool locate_lane(int row, const uint32_t*& w, const uint16_t*& s, const uint16_t*& b, int K,
+                                int gpr) const {
+        return locate(row, w, s, b, K, gpr);
+    }
 };
 
 // Gate/up rows of the selected experts: row r -> slot k = r / (2F),
@@ -150,7 +196,80 @@ struct GateUpRows {
         return true;
     }
     __device__ void store(int, int row, float v) const { out[row] = f2h_bits(v); }
+    __device__ bool locate_lane(int row, const uint32_t*& w, const uint16_t*& s, const uint16_t*& b, int K,
+                                int gpr) const {
+        return locate(row, w, s, b, K, gpr);
+    }
 };
+
+// Dynamic LDS a kernel of this file may take: the device's limit less what
+// the workgroup-wide flag reduction (__syncthreads_or) keeps for itself.
+inline size_t lds_budget() { return static_cast<size_t>(max_lds_bytes()) - 256; }
+
+// Rows whose x (or h) holds an infinite or NaN value take the reference's
+// per-element arithmetic instead of the factored s*sum(nib*x) + b*sum(x):
+// nib = 0 gives 0*inf = NaN in the factored form where the reference has
+// b*inf.  The whole workgroup (or wave) switches when any element of its x is
+// not finite, in a branch of its own, so the fast loop keeps its registers.
+
+// Row `row` of `rows`, batch row bidx of x, per element (one lane).
+template <class Rows>
+__device__ __forceinline__ void store_exact_row(const Rows& rows, int bidx, int row, const uint16_t* __restrict__ X,
+                                                int64_t ldx, int K, int gsize) {
+    const uint32_t* w;
+    const uint16_t *s, *b;
+    const float v = rows.locate_lane(row, w, s, b, K, K / gsize) ? affine_row_exact(w, s, b, X + bidx * ldx, K, gsize)
+                                                                 : 0.f;
+    rows.store(bidx, row, v);
+}
+
+// One output row o of the gather's phase 2 with the reference's per-element
+// arithmetic: sum over the valid slots k of w_k * (down[e_k][o] . h_k).  Slots
+// k < top_k take expert idx[k] and weight rw[k]; with `shared` the one slot is
+// expert 0 of `down` (the shared expert's descriptors) with weight 1 and h
+// slot top_k.  h_k: with FROM_GU the fp16 gate/up outputs [k][2][F] at src
+// (h = fp16(fp16(silu(g)) * u)), else h [k][F] at src.  The slow path for a
+// row whose fast sum is not finite.
+template <bool FROM_GU>
+__device__ __forceinline__ float moe_down_row_exact(const gdsllm_affine_experts& down,
+                                                    const int32_t* __restrict__ idx,
+                                                    const uint16_t* __restrict__ rw, int top_k, int o,
+                                                    const uint16_t* __restrict__ src, bool shared) {
+    const int F = static_cast<int>(down.in_dim), gsize = static_cast<int>(down.group_size), gpr = F / gsize;
+    float acc = 0.f;
+    const int nk = shared ? 1 : top_k;
+    for (int k = 0; k < nk; ++k) {
+        const int e = shared ? 0 : idx[k];
+        if (e < 0 || e >= down.num_experts) continue;
+        const int hk = shared ? top_k : k;
+        const uint32_t* w = reinterpret_cast<const uint32_t*>(static_cast<const char*>(down.weight) +
+                                                              e * down.weight_stride) + static_cast<int64_t>(o) * (F / 8);
+        const uint16_t* sp = reinterpret_cast<const uint16_t*>(static_cast<const char*>(down.scales) +
+                                                               e * down.scale_stride) + static_cast<int64_t>(o) * gpr;
+        const uint16_t* bp = reinterpret_cast<const uint16_t*>(static_cast<const char*>(down.biases) +
+                                                               e * down.bias_stride) + static_cast<int64_t>(o) * gpr;
+        float dot = 0.f;
+        for (int i = 0; i < F / 8; ++i) {
+            const uint32_t v = w[i];
+            const int G = (8 * i) / gsize;
+            const float sf = h2f(sp[G]), bf = h2f(bp[G]);
+            for (int n = 0; n < 8; ++n) {
+                const int jj = 8 * i + n;
+                float h;
+                if constexpr (FROM_GU) {
+                    const float g = h2f(src[static_cast<int64_t>(hk) * 2 * F + jj]);
+                    const float sg = h2f(f2h_bits(g / (1.0f + expf(-g))));
+                    h = h2f(f2h_bits(sg * h2f(src[static_cast<int64_t>(hk) * 2 * F + F + jj])));
+                } else {
+                    h = h2f(src[static_cast<int64_t>(hk) * F + jj]);
+                }
+                dot = __builtin_fmaf(fp32_rounded(static_cast<float>((v >> (4 * n)) & 15u) * sf + bf), h, dot);
+            }
+        }
+        acc = __builtin_fmaf(shared ? 1.0f : h2f(rw[k]), dot, acc);
+    }
+    return acc;
+}
 
 // Generic affine GEMV: LR lanes share a row (64/LR rows per wave pass), each
 // lane walks chunks lane%LR, +LR, ... of its row; loads are issued kU items
@@ -160,8 +279,7 @@ __global__ __launch_bounds__(kThreads) void affine_gemv(Rows rows, const uint16_
                                                         int64_t ldx, int x_al16) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int CPR = K / 32;
-    build_xprep_plain<NB>(smem, X, CPR, ldx, x_al16 != 0);
-    __syncthreads();
+    const bool nonfinite = __syncthreads_or(build_xprep_plain<NB>(smem, X, CPR, ldx, x_al16 != 0));
 
     constexpr int RW = 64 / LR;
     const int lane = threadIdx.x & 63;
@@ -173,6 +291,15 @@ __global__ __launch_bounds__(kThreads) void affine_gemv(Rows rows, const uint16_
     const int gw = blockIdx.x * kWaves + (threadIdx.x >> 6);
     const int my_passes = gw < passes ? (passes - 1 - gw) / TW + 1 : 0;
     const int n_items = my_passes * CPL;
+    if (nonfinite) {
+        // lane l < RW takes row l of each of this wave's passes
+        for (int pass = gw; pass < passes; pass += TW) {
+            const int row = pass * RW + lane;
+            if (lane < RW && row < rows.M)
+                for (int b = 0; b < NB; ++b) store_exact_row(rows, b, row, X, ldx, K, gsize);
+        }
+        return;
+    }
 
     float acc[NB];
 #pragma unroll
@@ -240,6 +367,7 @@ __global__ __launch_bounds__(kThreads) void moe_down(gdsllm_affine_experts down,
     const int gsize = static_cast<int>(down.group_size);
     const int CPR = F / 32;
     // prepared h records: [top_k][CPR]
+    bool h_nonfinite = false;
     {
         const int items = top_k * CPR * 4;
         for (int base = 0; base < items; base += kThreads) {
@@ -273,9 +401,10 @@ __global__ __launch_bounds__(kThreads) void moe_down(gdsllm_affine_experts down,
                 *reinterpret_cast<float*>(rec + 64) = corr;
                 *reinterpret_cast<float*>(rec + 68) = sum;
             }
+            h_nonfinite |= live && !__builtin_isfinite(sum);
         }
     }
-    __syncthreads();
+    const bool nonfinite = __syncthreads_or(h_nonfinite);
 
     constexpr int RW = 64 / LR;
     const int lane = threadIdx.x & 63;
@@ -285,6 +414,13 @@ __global__ __launch_bounds__(kThreads) void moe_down(gdsllm_affine_experts down,
     const int passes = (H + RW - 1) / RW;
     const int TW = gridDim.x * kWaves;
     const int gw = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    if (nonfinite) {
+        for (int pass = gw; pass < passes; pass += TW) {
+            const int o = pass * RW + lane;
+            if (lane < RW && o < H) Y[o] = f2h_bits(moe_down_row_exact<true>(down, idx, rw, top_k, o, gu, false));
+        }
+        return;
+    }
     for (int pass = gw; pass < passes; pass += TW) {
         const int o = pass * RW + sub;
         float acc = 0.f;
@@ -330,7 +466,9 @@ __global__ __launch_bounds__(kThreads) void moe_down(gdsllm_affine_experts down,
             }
         }
         acc = group_sum<LR>(acc);
-        if (li == 0 && o < H) Y[o] = f2h_bits(acc);
+        if (li == 0 && o < H) {
+            Y[o] = f2h_bits(acc);
+        }
     }
 }
 
@@ -467,12 +605,19 @@ __device__ __forceinline__ float chunk_dot_p(uint4 w, const uint32_t* p, float c
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const uint32_t v = wd[q], vs = v >> 8;
-        S = dot2(nu.lo(v), p[4 * q + 0], S);
-        S = dot2(nu.hi(v), p[4 * q + 1], S);
-        S = dot2(nu.lo(vs), p[4 * q + 2], S);
-        S = dot2(nu.hi(vs), p[4 * q + 3], S);
+        if constexpr (kAffineExact) {
+            S = dot2(unbias_nib(nu.lo_c(v), kNeg1024), p[4 * q + 0], S);
+            S = dot2(unbias_nib(nu.hi_c(v), kNeg64), p[4 * q + 1], S);
+            S = dot2(unbias_nib(nu.lo_c(vs), kNeg1024), p[4 * q + 2], S);
+            S = dot2(unbias_nib(nu.hi_c(vs), kNeg64), p[4 * q + 3], S);
+        } else {
+            S = dot2(nu.lo(v), p[4 * q + 0], S);
+            S = dot2(nu.hi(v), p[4 * q + 1], S);
+            S = dot2(nu.lo(vs), p[4 * q + 2], S);
+            S = dot2(nu.hi(vs), p[4 * q + 3], S);
+        }
     }
-    return __builtin_fmaf(s, S - corr, b * sum);
+    return __builtin_fmaf(s, kAffineExact ? S : S - corr, b * sum);
 }
 
 // Sum over aligned groups of N lanes (N = 1, 2, 4, 8, 16), every lane of the
@@ -569,6 +714,25 @@ struct GateUpPairsT : std::conditional_t<SH, SharedSlot, NoSharedSlot> {
         const int rem = v - k * 2 * F;
         gu[(2 * k + (rem & 1)) * F + (rem >> 1)] = f2h_bits(val);
     }
+    // locate for one lane on its own (no wave-wide reads): the slow path
+    __device__ bool locate_lane(int v, const uint32_t*& w, const uint16_t*& s, const uint16_t*& b, int K,
+                                int gpr) const {
+        const int k = v / (2 * F);
+        const int rem = v - k * 2 * F;
+        const int n = rem >> 1;
+        const gdsllm_affine_experts& p = proj(k, rem & 1);
+        int e = k < M / (2 * F) ? idx[k] : -1;
+        if constexpr (SH)
+            if (k == this->shared_slot) e = 0;
+        if (e < 0 || e >= p.num_experts) return false;
+        w = reinterpret_cast<const uint32_t*>(static_cast<const char*>(p.weight) + e * p.weight_stride) +
+            static_cast<int64_t>(n) * (K / 8);
+        s = reinterpret_cast<const uint16_t*>(static_cast<const char*>(p.scales) + e * p.scale_stride) +
+            static_cast<int64_t>(n) * gpr;
+        b = reinterpret_cast<const uint16_t*>(static_cast<const char*>(p.biases) + e * p.bias_stride) +
+            static_cast<int64_t>(n) * gpr;
+        return true;
+    }
 };
 using GateUpPairs = GateUpPairsT<false>;
 using GateUpPairsShared = GateUpPairsT<true>;
@@ -638,10 +802,39 @@ __global__ __launch_bounds__(kThreads) void affine_rows(Rows rows, const uint16_
         }
     issue(gw);
     XChunk xc[NB][CPL];
+    bool x_nonfinite = false;
 #pragma unroll
     for (int b = 0; b < NB; ++b)
 #pragma unroll
-        for (int i = 0; i < CPL; ++i) make_xchunk(xc[b][i], xr[b][i]);
+        for (int i = 0; i < CPL; ++i) {
+            make_xchunk(xc[b][i], xr[b][i]);
+            x_nonfinite |= !__builtin_isfinite(xc[b][i].sum);
+        }
+    if (__builtin_amdgcn_ballot_w64(x_nonfinite) != 0) {
+        // the reference's per-element arithmetic for this wave's rows: lane l
+        // takes row l of each stage (gate/up pairs: the even lane both rows of
+        // its pair, then h)
+        wait_vmcnt<0>();
+        for (int t = 0; t < T; ++t) {
+            const int row = (gw + t * TW) * RPS + lane;
+            if constexpr (IsGateUp<Rows>::value) {
+                if (lane < RPS && (lane & 1) == 0 && row + 1 < rows.M) {
+                    const uint32_t *wg, *wu;
+                    const uint16_t *sg, *bg, *su, *bu;
+                    const float g = rows.locate_lane(row, wg, sg, bg, K, gpr) ? affine_row_exact(wg, sg, bg, X, K, gsize) : 0.f;
+                    const float u = rows.locate_lane(row + 1, wu, su, bu, K, gpr) ? affine_row_exact(wu, su, bu, X, K, gsize) : 0.f;
+                    rows.store(0, row, g);
+                    rows.store(0, row + 1, u);
+                    const int k = row / (2 * rows.F);
+                    rows.h[k * rows.F + ((row - k * 2 * rows.F) >> 1)] = silu_mul_h(g, u);
+                }
+            } else {
+                if (lane < RPS && row < rows.M)
+                    for (int b = 0; b < NB; ++b) store_exact_row(rows, b, row, X, ldx, K, gsize);
+            }
+        }
+        return;
+    }
 
     for (int t = 0; t < T; ++t) {
         const int st = gw + t * TW;
@@ -795,6 +988,7 @@ __global__ __launch_bounds__(NT) void moe_down_rows(gdsllm_affine_experts down, 
     };
     if (T > 0) issue(gw);
     // prepared h records [top_k][CPR], one quarter (8 elements) per item
+    bool h_nonfinite = false;
     {
         for (int base = 0; base < items; base += NT) {
             const int it = base + threadIdx.x;
@@ -823,10 +1017,36 @@ __global__ __launch_bounds__(NT) void moe_down_rows(gdsllm_affine_experts down, 
                 *reinterpret_cast<float*>(rec + 64) = corr;
                 *reinterpret_cast<float*>(rec + 68) = sum;
             }
+            h_nonfinite |= live && !__builtin_isfinite(sum);
         }
     }
-    __syncthreads();
+    const bool nonfinite = __syncthreads_or(h_nonfinite);
     if (T == 0) return;
+    // combine of the routed sum v and the shared expert's vs for output row o
+    auto combine_store = [&](int o, float v, float vs) {
+        if constexpr (SH) {
+            const float g = h2f(graw);
+            const float sw = h2f(f2h_bits(fp32_rounded(1.0f / fp32_rounded(1.0f + expf(-g)))));
+            const float sc = h2f(f2h_bits(fp32_rounded(sw * h2f(f2h_bits(vs)))));
+            float r = h2f(f2h_bits(fp32_rounded(h2f(f2h_bits(v)) + sc)));
+            if (r > 65504.0f) r = 65504.0f;  // NaN compares false both ways and stays NaN
+            if (r < -65504.0f) r = -65504.0f;
+            Y[o] = f2h_bits(r);
+        } else {
+            Y[o] = f2h_bits(v);
+        }
+    };
+    if (nonfinite) {
+        // the reference's per-element arithmetic: lane r < R takes row r of each stage
+        wait_vmcnt<0>();
+        for (int t = 0; t < T; ++t) {
+            const int o = (gw + t * TW) * R + lane;
+            if (lane < R && o < H)
+                combine_store(o, moe_down_row_exact<false>(down, idx, rw, top_k, o, hbuf, false),
+                              SH ? moe_down_row_exact<false>(sdown, idx, rw, top_k, o, hbuf, true) : 0.f);
+        }
+        return;
+    }
 
     for (int t = 0; t < T; ++t) {
         const int st = gw + t * TW;
@@ -882,20 +1102,8 @@ __global__ __launch_bounds__(NT) void moe_down_rows(gdsllm_affine_experts down, 
         const float v = lanes64(acc);
         const int o = st * R + (R == 2 ? (lane >> 5) : 0);
         const bool writer = (lane & 31) == 0 && (R == 2 || lane == 0) && o < H;
-        if constexpr (SH) {
-            const float vs = lanes64(accs);
-            if (writer) {
-                const float g = h2f(graw);
-                const float sw = h2f(f2h_bits(fp32_rounded(1.0f / fp32_rounded(1.0f + expf(-g)))));
-                const float sc = h2f(f2h_bits(fp32_rounded(sw * h2f(f2h_bits(vs)))));
-                float r = h2f(f2h_bits(fp32_rounded(h2f(f2h_bits(v)) + sc)));
-                if (r > 65504.0f) r = 65504.0f;  // NaN compares false both ways and stays NaN
-                if (r < -65504.0f) r = -65504.0f;
-                Y[o] = f2h_bits(r);
-            }
-        } else if (writer) {
-            Y[o] = f2h_bits(v);
-        }
+        const float vs = SH ? lanes64(accs) : 0.f;
+        if (writer) combine_store(o, v, vs);
     }
 }
 
@@ -1030,7 +1238,7 @@ extern "C" int gdsllm_fused_affine_q4_gemv(const void* weight, const void* scale
         const int rc = batch == 1 ? dispatch_rows<1>(rows, xp, K, g, ldx, s) : dispatch_rows<2>(rows, xp, K, g, ldx, s);
         return rc ? rc : ok();
     }
-    const size_t budget = static_cast<size_t>(max_lds_bytes());
+    const size_t budget = lds_budget();
     if (fast && static_cast<size_t>(K / 32) * kRec <= budget) {
         int64_t b0 = 0;
         while (b0 < batch) {
@@ -1156,7 +1364,7 @@ static int moe_gather_impl(const std::string& n, const gdsllm_affine_experts* ga
                          n + (fixed_ws ? ": top_k * ffn too large for the fixed workspace (" : ": workspace too small (") +
                              std::to_string(gdsllm_moe_gather_workspace_size(top_k, F)) + " bytes needed, " +
                              std::to_string(workspace_bytes) + " available)");
-    const size_t budget = static_cast<size_t>(max_lds_bytes());
+    const size_t budget = lds_budget();
     const size_t lds1 = static_cast<size_t>(H / 32) * kRec, lds2 = static_cast<size_t>(top_k) * (F / 32) * kRec;
     if (lds1 > budget || lds2 > budget)
         return set_error(GDSLLM_ERR_UNSUPPORTED, n + ": hidden or top_k*ffn too large for LDS staging");
@@ -1287,7 +1495,7 @@ extern "C" int gdsllm_moe_step_affine_q4(const gdsllm_affine_experts* gate, cons
     if (!rows_path || shared_gate->out_dim != F || shared_gate->group_size != gate->group_size ||
         shared_up->group_size != gate->group_size || shared_down->group_size != down->group_size)
         return set_error(GDSLLM_ERR_UNSUPPORTED, n + ": shape outside the fused step (use the separate launches)");
-    const size_t budget = static_cast<size_t>(max_lds_bytes());
+    const size_t budget = lds_budget();
     if (static_cast<size_t>(nslot) * cpr_f * kRec > budget || static_cast<size_t>(cpr_h) * kRec > budget)
         return set_error(GDSLLM_ERR_UNSUPPORTED, n + ": hidden or (top_k+1)*ffn too large for LDS staging");
     hipStream_t s = as_stream(stream);

@@ -35,6 +35,33 @@ namespace {
 
 enum class Fmt { Q4_0, Q8_0 };
 
+// Exact products: every weight pair enters the dot products as its exact value
+// (q - 8 for Q4_0, q for Q8_0: the exponent-trick pair minus its bias, exact
+// in packed fp16), so each product w*x is the reference's product and the fp32
+// sum has the reference's magnitude; no offset correction is subtracted.
+// Without it the sum runs over (1024 + q)*x and the correction c cancels it
+// afterwards, which loses about 10 bits to cancellation when one x dwarfs the
+// rest (an activation near 65504 against N(0, 1)) and turns an infinite x into
+// inf - inf = NaN on every row (the reference gives +-inf, NaN only where the
+// weight is 0).  The exact form costs one packed subtract per weight pair
+// (about 4% at 11008x4096, batch 1), so a window takes it only when its x calls
+// for it (load_slice); kRowsExact = false disables it (measurement only).
+// The batched kernels take the exact form always: the staged kernel
+// (kStagedExact), a fallback, and the Q4_0 MFMA kernels (kCodesExact), where
+// the weight operand is unbiased the same way and the offset-correction MFMAs
+// drop out.
+constexpr bool kRowsExact = true;
+constexpr bool kStagedExact = true;
+constexpr bool kCodesExact = true;
+
+// (a - bias) on both fp16 halves (v_pk_add_f16; exact for the pairs below).
+__device__ __forceinline__ uint32_t unbias_pair(uint32_t a, uint32_t neg_bias_pair) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, a) + __builtin_bit_cast(half2_t, neg_bias_pair));
+}
+constexpr uint32_t kNeg1032 = 0xE408E408u;  // fp16 -1032 in both halves
+constexpr uint32_t kNeg72 = 0xD480D480u;    // -72
+constexpr uint32_t kNeg1152 = 0xE480E480u;  // -1152
+
 template <Fmt F> struct Layout;
 template <> struct Layout<Fmt::Q4_0> {
     static constexpr int kBlockBytes = 18;
@@ -200,8 +227,12 @@ __device__ __forceinline__ void superblock_dot(const uint32_t* D, const uint8_t*
             for (int dd = 0; dd < 4; ++dd) {
                 const uint32_t v = q[dd];
                 const uint32_t vs = v >> 8;
-                const uint32_t p0 = nib_lo_pair(v), p1 = nib_hi_pair(v);
-                const uint32_t p2 = nib_lo_pair(vs), p3 = nib_hi_pair(vs);
+                uint32_t p0 = nib_lo_pair(v), p1 = nib_hi_pair(v);
+                uint32_t p2 = nib_lo_pair(vs), p3 = nib_hi_pair(vs);
+                if constexpr (kStagedExact) {
+                    p0 = unbias_pair(p0, kNeg1032), p1 = unbias_pair(p1, kNeg72);
+                    p2 = unbias_pair(p2, kNeg1032), p3 = unbias_pair(p3, kNeg72);
+                }
 #pragma unroll
                 for (int b = 0; b < NB; ++b) {
                     const uint4 xv = *reinterpret_cast<const uint4*>(xrec0 + b * rec_stride + (16 * i + 4 * dd) * 4);
@@ -228,10 +259,14 @@ __device__ __forceinline__ void superblock_dot(const uint32_t* D, const uint8_t*
             for (int dd = 0; dd < 8; dd += 2) {
                 // int8 -> biased byte u = q+128, then (u | 0x6400) = 1152 + q
                 const uint32_t u0 = q[dd] ^ 0x80808080u, u1 = q[dd + 1] ^ 0x80808080u;
-                const uint32_t p0 = (u0 & 0x00FF00FFu) | 0x64006400u;
-                const uint32_t p1 = ((u0 >> 8) & 0x00FF00FFu) | 0x64006400u;
-                const uint32_t p2 = (u1 & 0x00FF00FFu) | 0x64006400u;
-                const uint32_t p3 = ((u1 >> 8) & 0x00FF00FFu) | 0x64006400u;
+                uint32_t p0 = (u0 & 0x00FF00FFu) | 0x64006400u;
+                uint32_t p1 = ((u0 >> 8) & 0x00FF00FFu) | 0x64006400u;
+                uint32_t p2 = (u1 & 0x00FF00FFu) | 0x64006400u;
+                uint32_t p3 = ((u1 >> 8) & 0x00FF00FFu) | 0x64006400u;
+                if constexpr (kStagedExact) {
+                    p0 = unbias_pair(p0, kNeg1152), p1 = unbias_pair(p1, kNeg1152);
+                    p2 = unbias_pair(p2, kNeg1152), p3 = unbias_pair(p3, kNeg1152);
+                }
 #pragma unroll
                 for (int b = 0; b < NB; ++b) {
                     const uint4 xv = *reinterpret_cast<const uint4*>(xrec0 + b * rec_stride + (16 * i + 2 * dd) * 4);
@@ -245,8 +280,12 @@ __device__ __forceinline__ void superblock_dot(const uint32_t* D, const uint8_t*
         const float d = h2f(dbits);
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
-            const float corr = *reinterpret_cast<const float*>(xrec0 + b * rec_stride + 512 + 4 * i);
-            acc[b] = __builtin_fmaf(d, Sd[b] - corr, acc[b]);
+            if constexpr (kStagedExact) {
+                acc[b] = __builtin_fmaf(d, Sd[b], acc[b]);
+            } else {
+                const float corr = *reinterpret_cast<const float*>(xrec0 + b * rec_stride + 512 + 4 * i);
+                acc[b] = __builtin_fmaf(d, Sd[b] - corr, acc[b]);
+            }
         }
     }
 }
@@ -345,6 +384,7 @@ constexpr uint32_t kPair1152 = 0x64806480u;
 constexpr uint32_t kSelLo = 0x05040100u;
 constexpr uint32_t kSelHi = 0x07060302u;
 
+
 // A lane's x slice: fp16 pairs of blocks 2c, 2c+1 of the window in the order
 // the unpacked nibbles come out in (p[b][k]: block k), and each block's offset
 // correction: 1032*sum(x[0..16)) + 72*sum(x[16..32)) (Q4_0) or 1152*sum(x)
@@ -353,6 +393,7 @@ template <int NB>
 struct XSlice {
     uint32_t p[NB][2][16];
     float c[NB][2];
+    bool exact;  // wave-uniform: this window's x needs the exact products
 };
 
 // 32 raw fp16 of one block (r[i] = elements 2i, 2i+1) -> 16 pairs in unpack
@@ -413,39 +454,71 @@ __device__ __forceinline__ void rows_xraw_issue(uint8_t* xraw, const uint16_t* _
 
 // The slice of window w, read with the raw LDS helpers (no weight transfer
 // ever targets the x region), permuted into unpack order, with corrections.
+//
+// It also decides, for the whole wave, whether this window takes the exact
+// products (see kRowsExact): when some block of x holds a quarter or more of
+// the window's energy sum(x^2) of its batch row, or any energy is not finite
+// (an infinite or NaN x).  Below that share the offset-corrected sum stays
+// within 2e-4 of ||w * x|| per block (its error is about 2^-22 * 1032 *
+// sum|x| of the block, and sum|x| <= sqrt(32 * E / 4)); activations drawn
+// from one distribution never come near it, an outlier column does.
 template <Fmt F, int NB>
-__device__ __forceinline__ void load_slice(XSlice<NB>& xs, const uint8_t* xraw, int NW, int w, int lane) {
+__device__ __forceinline__ void load_slice(XSlice<NB>& xs, const uint8_t* xraw, int NW, int w, int K, int lane) {
     u32x4_t v[NB][8];
 #pragma unroll
     for (int b = 0; b < NB; ++b) lds_read16x8_sync(lds_addr(xraw + (b * NW + w) * 8192 + 16 * lane), v[b]);
+    // lane's two blocks lie inside in_dim (filler x past the end is ignored)
+    const bool valid = 4096 * w + 64 * lane < K;
+    bool risky = false;
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
+        float e[2];
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
             uint32_t r[16];
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) r[4 * i + e] = v[b][4 * k + i][e];
+                for (int j = 0; j < 4; ++j) r[4 * i + j] = v[b][4 * k + i][j];
             xs.c[b][k] = permute_block<F>(r, xs.p[b][k]);
+            float en = 0.f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) en = dot2(r[i], r[i], en);
+            e[k] = valid ? en : 0.f;
         }
+        // window energy of batch row b in every lane: lane-half swaps, then the 16-lane DPP sum
+        float tot = swap_sum32(e[0] + e[1], e[0] + e[1]);
+        tot = row16_sum(swap_sum16(tot, tot));
+#pragma unroll
+        for (int k = 0; k < 2; ++k) risky |= !(e[k] <= 0.f) && !(4.f * e[k] < tot);
     }
+    xs.exact = kRowsExact && __builtin_amdgcn_ballot_w64(risky) != 0;
 }
 
+
 // Adds the dot products of qs dword dd of one block with its x pairs to S.
-template <Fmt F>
+template <Fmt F, bool EXACT>
 __device__ __forceinline__ float dword_dot(uint32_t q, const uint32_t* xp, int dd, float S, const NibUnpack& nu) {
     if constexpr (F == Fmt::Q4_0) {
         const uint32_t vs = q >> 8;
-        S = dot2(nu.lo(q), xp[4 * dd + 0], S);
-        S = dot2(nu.hi(q), xp[4 * dd + 1], S);
-        S = dot2(nu.lo(vs), xp[4 * dd + 2], S);
-        S = dot2(nu.hi(vs), xp[4 * dd + 3], S);
+        if constexpr (EXACT) {
+            S = dot2(unbias_pair(nu.lo_c(q), kNeg1032), xp[4 * dd + 0], S);
+            S = dot2(unbias_pair(nu.hi_c(q), kNeg72), xp[4 * dd + 1], S);
+            S = dot2(unbias_pair(nu.lo_c(vs), kNeg1032), xp[4 * dd + 2], S);
+            S = dot2(unbias_pair(nu.hi_c(vs), kNeg72), xp[4 * dd + 3], S);
+        } else {
+            S = dot2(nu.lo(q), xp[4 * dd + 0], S);
+            S = dot2(nu.hi(q), xp[4 * dd + 1], S);
+            S = dot2(nu.lo(vs), xp[4 * dd + 2], S);
+            S = dot2(nu.hi(vs), xp[4 * dd + 3], S);
+        }
     } else {
         // biased byte u = q + 128 in the low byte of each half: 1024 + u
         const uint32_t u = q ^ 0x80808080u;
-        S = dot2(__builtin_amdgcn_perm(0x64646464u, u, 0x04020400u), xp[2 * dd], S);
-        S = dot2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030401u), xp[2 * dd + 1], S);
+        const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, u, 0x04020400u);
+        const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, u, 0x04030401u);
+        S = dot2(EXACT ? unbias_pair(p0, kNeg1152) : p0, xp[2 * dd], S);
+        S = dot2(EXACT ? unbias_pair(p1, kNeg1152) : p1, xp[2 * dd + 1], S);
     }
     return S;
 }
@@ -586,9 +659,9 @@ size_t rows_lds_bytes(int nw, int wpg) {
 // Rows R0 .. R0+NR-1 of a stage in LDS: lane c's blocks 2c, 2c+1 of each row
 // against its x slice, added to acc[b][R0+r].  The NR rows x 2 blocks x NB
 // dot-product chains interleave.
-template <Fmt F, int NB, int R0, int NR = 2>
-__device__ __forceinline__ void rows_pair(const uint8_t* buf, const XSlice<NB>& xs, float (&acc)[NB][4],
-                                          const NibUnpack& nu, int lane) {
+template <Fmt F, int NB, int R0, int NR, bool EXACT>
+__device__ __forceinline__ void rows_pair_impl(const uint8_t* buf, const XSlice<NB>& xs, float (&acc)[NB][4],
+                                               const NibUnpack& nu, int lane) {
     using L = Layout<F>;
     constexpr int kSegBytes = kSbPerWindow * L::kSbBytes;
     constexpr int kSpanDw = L::kBlockBytes / 2;  // dwords of a lane's 2 blocks
@@ -615,8 +688,8 @@ __device__ __forceinline__ void rows_pair(const uint8_t* buf, const XSlice<NB>& 
             const uint32_t q1 = D[r][kQd + 1 + dd];
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
-                Sx[b][r][0] = dword_dot<F>(q0, xs.p[b][0], dd, Sx[b][r][0], nu);
-                Sx[b][r][1] = dword_dot<F>(q1, xs.p[b][1], dd, Sx[b][r][1], nu);
+                Sx[b][r][0] = dword_dot<F, EXACT>(q0, xs.p[b][0], dd, Sx[b][r][0], nu);
+                Sx[b][r][1] = dword_dot<F, EXACT>(q1, xs.p[b][1], dd, Sx[b][r][1], nu);
             }
         }
 #pragma unroll
@@ -624,10 +697,26 @@ __device__ __forceinline__ void rows_pair(const uint8_t* buf, const XSlice<NB>& 
         const float d0 = h2f(D[r][0] & 0xFFFFu), d1 = h2f(D[r][kQd] >> 16);
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
-            acc[b][R0 + r] = __builtin_fmaf(d0, Sx[b][r][0] - xs.c[b][0], acc[b][R0 + r]);
-            acc[b][R0 + r] = __builtin_fmaf(d1, Sx[b][r][1] - xs.c[b][1], acc[b][R0 + r]);
+            if constexpr (EXACT) {
+                acc[b][R0 + r] = __builtin_fmaf(d0, Sx[b][r][0], acc[b][R0 + r]);
+                acc[b][R0 + r] = __builtin_fmaf(d1, Sx[b][r][1], acc[b][R0 + r]);
+            } else {
+                acc[b][R0 + r] = __builtin_fmaf(d0, Sx[b][r][0] - xs.c[b][0], acc[b][R0 + r]);
+                acc[b][R0 + r] = __builtin_fmaf(d1, Sx[b][r][1] - xs.c[b][1], acc[b][R0 + r]);
+            }
         }
     }
+}
+
+// The window's products, exact or offset-corrected as its x requires (a
+// wave-uniform branch).
+template <Fmt F, int NB, int R0, int NR = 2>
+__device__ __forceinline__ void rows_pair(const uint8_t* buf, const XSlice<NB>& xs, float (&acc)[NB][4],
+                                          const NibUnpack& nu, int lane) {
+    if (xs.exact)
+        rows_pair_impl<F, NB, R0, NR, true>(buf, xs, acc, nu, lane);
+    else
+        rows_pair_impl<F, NB, R0, NR, false>(buf, xs, acc, nu, lane);
 }
 
 // Rows of `target` times x (MODE 0: one matrix; 1: a group; 2: gate/up pairs); x must be 16-byte aligned
@@ -689,7 +778,7 @@ __global__ __launch_bounds__(kWaves * 64) void gguf_gemv_rows(const RowsTarget t
     lds_barrier();  // every wave's share of x has landed
 
     XSlice<NB> xs;
-    if (T > 0) load_slice<F, NB>(xs, xp, NW, 0, lane);
+    if (T > 0) load_slice<F, NB>(xs, xp, NW, 0, K, lane);
     int xwin = 0;
     float acc[NB][4];
 #pragma unroll
@@ -702,7 +791,7 @@ __global__ __launch_bounds__(kWaves * 64) void gguf_gemv_rows(const RowsTarget t
         const RowsStage st = stage_at(t);
         const bool next = t + 1 < T;
         if (win != xwin) {
-            load_slice<F, NB>(xs, xp, NW, win, lane);
+            load_slice<F, NB>(xs, xp, NW, win, K, lane);
             xwin = win;
         }
         // Lanes past the end of a partial window skip; rows past M compute on
@@ -1115,6 +1204,16 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void gguf_gemv_mfma(const uint8_t*
 // batch rows (4 KiB), moved by LDS DMA; every wave keeps two stages in flight.
 // At the end of a tile the waves' partial sums meet in LDS and are added in
 // wave order, so results do not depend on timing.
+// Weight operand of one block pair from its two permuted qs dwords: the
+// exponent-trick codes (1024 + q low nibbles, 64 + q high nibbles), or with
+// kCodesExact the exact q - 8 (the codes plus kneg = -1032 / -72, four packed
+// fp16 adds).
+__device__ __forceinline__ half8_t codes_operand(uint32_t p01, uint32_t p23, const NibUnpack& nu, half8_t kneg) {
+    const half8_t c = __builtin_bit_cast(half8_t, make_uint4(nu.lo_c(p01), nu.lo_c(p23), nu.hi_c(p01), nu.hi_c(p23)));
+    if constexpr (kCodesExact) return c + kneg;
+    return c;
+}
+
 namespace bq {
 constexpr int kWaves = 8;
 constexpr int kXStride = 1088;                  // LDS bytes per x transfer (2 batch rows + bank padding)
@@ -1228,7 +1327,9 @@ __global__ __launch_bounds__(bq::kWaves * 64) void gguf_gemv_q4_codes(const uint
             const uint2 lo = *reinterpret_cast<const uint2*>(xs + 128 * p);
             const uint2 hi = *reinterpret_cast<const uint2*>(xs + 128 * p + 32);
             xa[p] = __builtin_bit_cast(half8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
-            dc[p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[p], kneg, float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            dc[p] = kCodesExact ? float4_t{0.f, 0.f, 0.f, 0.f}
+                                : __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[p], kneg, float4_t{0.f, 0.f, 0.f, 0.f}, 0,
+                                                                         0, 0);
         }
 #pragma unroll
         for (int rg = 0; rg < NRG; ++rg)
@@ -1240,8 +1341,7 @@ __global__ __launch_bounds__(bq::kWaves * 64) void gguf_gemv_q4_codes(const uint
                 const half_t dv = __builtin_bit_cast(half_t, *reinterpret_cast<const uint16_t*>(wr + drd));
                 const uint32_t p01 = __builtin_amdgcn_perm(d1, d0, sel01);
                 const uint32_t p23 = __builtin_amdgcn_perm(d1, d0, sel23);
-                const half8_t wb =
-                    __builtin_bit_cast(half8_t, make_uint4(nu.lo_c(p01), nu.lo_c(p23), nu.hi_c(p01), nu.hi_c(p23)));
+                const half8_t wb = codes_operand(p01, p23, nu, kneg);
                 const float4_t D = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[p], wb, dc[p], 0, 0, 0);
                 const float dsc = static_cast<float>(dv);
 #pragma unroll
@@ -1510,8 +1610,9 @@ __global__ __launch_bounds__(C::kWaves * 64) void gguf_gemv_q4_xreg(const uint8_
                 const uint8_t* sl = lds + (slot0 - lds0) + cslot * bx::kSlotBytes;
 #pragma unroll
                 for (int p = 0; p < 4; ++p)
-                    dc[p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[s2][p], kneg, float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0,
-                                                                   0);
+                    dc[p] = kCodesExact ? float4_t{0.f, 0.f, 0.f, 0.f}
+                                        : __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[s2][p], kneg,
+                                                                                 float4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
                 for (int rg = 0; rg < NRG; ++rg)
 #pragma unroll
@@ -1522,8 +1623,7 @@ __global__ __launch_bounds__(C::kWaves * 64) void gguf_gemv_q4_xreg(const uint8_
                         const half_t dv = __builtin_bit_cast(half_t, *reinterpret_cast<const uint16_t*>(wr + drd));
                         const uint32_t p01 = __builtin_amdgcn_perm(d1, d0, sel01);
                         const uint32_t p23 = __builtin_amdgcn_perm(d1, d0, sel23);
-                        const half8_t wbv = __builtin_bit_cast(
-                            half8_t, make_uint4(nu.lo_c(p01), nu.lo_c(p23), nu.hi_c(p01), nu.hi_c(p23)));
+                        const half8_t wbv = codes_operand(p01, p23, nu, kneg);
                         const float4_t D = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[s2][p], wbv, dc[p], 0, 0, 0);
                         const float dsc = static_cast<float>(dv);
 #pragma unroll

@@ -115,6 +115,22 @@ def gemv(w_fp16: np.ndarray, x_fp16: np.ndarray) -> np.ndarray:
     return x @ w.T
 
 
+def gemv_ieee(w_fp16: np.ndarray, x_fp16: np.ndarray, rows_per_chunk: int = 256) -> np.ndarray:
+    """gemv with IEEE special values kept: y[b, r] = sum_k W[r, k] * x[b, k] as
+    float64 products summed element by element (no BLAS, which may skip zero
+    operands), so 0 * inf = NaN and inf + -inf = NaN exactly as the
+    reference's fp32 loop produces them (runtime/fused_gemv.cu:69-70,
+    runtime/affine_q4_dequant.cu:125-126; the IEEE results do not depend on
+    the summation order).  Finite sums equal gemv's."""
+    w = np.asarray(w_fp16, dtype=np.float16).astype(np.float64)
+    x = np.atleast_2d(np.asarray(x_fp16, dtype=np.float16)).astype(np.float64)
+    out = np.empty((x.shape[0], w.shape[0]))
+    with np.errstate(invalid="ignore", over="ignore"):
+        for r0 in range(0, w.shape[0], rows_per_chunk):
+            out[:, r0:r0 + rows_per_chunk] = (x[:, None, :] * w[None, r0:r0 + rows_per_chunk, :]).sum(-1)
+    return out
+
+
 def row_norms(w_fp16: np.ndarray, x_fp16: np.ndarray) -> np.ndarray:
     """||w_r * x_b||_2 for every (b, r): the scale of the fp32 accumulation error of row r."""
     w = np.asarray(w_fp16, dtype=np.float16).astype(np.float64)

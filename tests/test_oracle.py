@@ -242,6 +242,24 @@ def test_gemv_brute_force():
             assert abs(norms[b, r] - math.sqrt(sum((float(w[r, k]) * float(x[b, k])) ** 2 for k in range(K)))) < 1e-9
 
 
+def test_gemv_ieee_special_values():
+    """IEEE results of the reference's fp32 loop: a nonzero weight times inf
+    is +-inf, a zero weight times inf is NaN, +inf and -inf terms give NaN, NaN
+    propagates; finite inputs give gemv's value."""
+    inf, nan = np.inf, np.nan
+    w = np.array([[1.0, 0.5, 0.0], [0.0, 1.0, 1.0], [-2.0, 1.0, 0.0], [1.0, -1.0, 0.0]], np.float16)
+    x = np.array([[inf, 1.0, 2.0], [inf, inf, 1.0], [nan, 1.0, 1.0]], np.float16)
+    y = oq.gemv_ieee(w, x)
+    assert y[0, 0] == inf and np.isnan(y[0, 1]) and y[0, 2] == -inf and y[0, 3] == inf
+    assert y[1, 0] == inf and np.isnan(y[1, 1]) and np.isnan(y[1, 2]) and np.isnan(y[1, 3])
+    assert np.isnan(y[2]).all()
+    rng = np.random.default_rng(21)
+    wf = rng.normal(size=(7, 96)).astype(np.float16)
+    xf = rng.normal(size=(2, 96)).astype(np.float16)
+    ref = np.array([[math.fsum(float(a) * float(b) for a, b in zip(wr, xr)) for wr in wf] for xr in xf])
+    assert np.allclose(oq.gemv_ieee(wf, xf, rows_per_chunk=3), ref, rtol=1e-12, atol=1e-12)
+
+
 def test_gemv_closed_forms():
     M, K = 8, 256
     raw = syn.q4_0_weights(M, K, torch.Generator().manual_seed(5)).numpy().reshape(-1, 18).copy()

@@ -164,31 +164,21 @@ def bench_decode_sweep(args, dev):
 
     unfused: 225 single GEMV launches (7 per layer + lm_head), every GEMV
     reading a synthetic x of its in_dim.
-    fused: 129 launches with the reference layer's data flow (llama.py:212-256):
-    q/k/v in one grouped launch on x_attn, o on x_o, gate+up+SiLU in one launch
-    on x_mlp writing h, down on that h; lm_head last.  Same weights, same
-    224 + 1 projections.  Returns (ms fused, ms unfused, weights)."""
-    import ctypes
-
+    fused: the runtime's DecodeSweep, 129 launches with the reference layer's
+    data flow (llama.py:212-256): q/k/v in one grouped launch on the attention
+    input, o on the attention output, gate+up+SiLU in one launch writing h,
+    down on that h; lm_head last.  Same weights, same 224 + 1 projections.
+    Returns (ms fused, ms unfused, weights)."""
     import torch
 
-    from gdsllm_amd import capi, check
     from gdsllm_amd import synthetic as syn
 
     gemv = Q4Gemv()
-    lib = capi()
     gen = torch.Generator(device=dev).manual_seed(2004)
     layers = [[syn.q4_0_weights(m, k, gen) for m, k in LAYER_SHAPES] for _ in range(N_LAYERS)]
     lm_head = syn.q4_0_weights(*LM_HEAD, gen)
     xs = {k: syn.activations(1, k, gen) for k in (4096, 11008)}
     ys = {m: torch.empty(1, m, dtype=torch.float16, device=dev) for m in (4096, 11008, 32000)}
-    x_attn, x_o, x_mlp = (syn.activations(1, 4096, gen) for _ in range(3))
-    y_qkv = [torch.empty(1, 4096, dtype=torch.float16, device=dev) for _ in range(3)]
-    y_o, y_down = torch.empty(1, 4096, dtype=torch.float16, device=dev), torch.empty(1, 4096, dtype=torch.float16, device=dev)
-    h = torch.empty(1, 11008, dtype=torch.float16, device=dev)
-    qkv_w = [(ctypes.c_void_p * 3)(*[w.data_ptr() for w in lw[:3]]) for lw in layers]
-    qkv_y = (ctypes.c_void_p * 3)(*[y.data_ptr() for y in y_qkv])
-    qkv_m = (ctypes.c_int64 * 3)(4096, 4096, 4096)
 
     def token_unfused():
         for lw in layers:
@@ -196,18 +186,35 @@ def bench_decode_sweep(args, dev):
                 gemv(w, xs[k], ys[m], m, k)
         gemv(lm_head, xs[LM_HEAD[1]], ys[LM_HEAD[0]], *LM_HEAD)
 
-    def token_fused():
-        st = torch.cuda.current_stream().cuda_stream
-        for li, lw in enumerate(layers):
-            check(lib.gdsllm_fused_q4_0_gemv_group(3, qkv_w[li], qkv_y, qkv_m, x_attn.data_ptr(), 4096, 1, 4096, st))
-            gemv(lw[3], x_o, y_o, 4096, 4096)
-            check(lib.gdsllm_fused_q4_0_gate_up_silu(lw[4].data_ptr(), lw[5].data_ptr(), x_mlp.data_ptr(),
-                                                     h.data_ptr(), 11008, 4096, 1, 4096, 11008, st))
-            gemv(lw[6], h, y_down, 4096, 11008)
-        gemv(lm_head, x_attn, ys[LM_HEAD[0]], *LM_HEAD)
+    # fused: the runtime's decode-step driver (one HIP graph per token)
+    from gdsllm_amd.runtime import ext
+    from gdsllm_amd.runtime.scheduler import DecodeSweep
+
+    names = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj", "mlp.gate_proj",
+             "mlp.up_proj", "mlp.down_proj")
+
+    def entry(w, m, k):
+        return {"buffer": ext().GdsBufferHandle.from_tensor(w), "shape": [m, k], "gguf_type": "q4_0", "offset": 0}
+
+    sweep = DecodeSweep([{f"{n}.weight": entry(w, m, k) for n, w, (m, k) in zip(names, lw, LAYER_SHAPES)}
+                         for lw in layers], entry(lm_head, *LM_HEAD), batch=1, device=dev)
+    for b in [*sweep.attn_in, *sweep.attn_out, *sweep.mlp_in, sweep.final_in]:
+        b.copy_(syn.activations(1, b.shape[1], gen))
+    sweep.run()
+    torch.cuda.synchronize()
 
     ms_unfused = _replay_ms(token_unfused, args.sweep_tokens)
-    ms_fused = _replay_ms(token_fused, args.sweep_tokens)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for _ in range(3):
+        sweep.run()
+    torch.cuda.synchronize()
+    _gpu_delay()
+    start.record()
+    for _ in range(args.sweep_tokens):
+        sweep.run()
+    end.record()
+    torch.cuda.synchronize()
+    ms_fused = start.elapsed_time(end) / args.sweep_tokens
     return ms_fused, ms_unfused, (layers, lm_head)
 
 

@@ -657,6 +657,90 @@ torch::Tensor moe_combine(torch::Tensor expert_out, torch::Tensor shared_out, to
     return y;
 }
 
+// q/k/v-style projections sharing x in one launch (the decode step's
+// runtime/llama.py:212-214): one output [batch, out_dim_i] per matrix.
+std::vector<torch::Tensor> fused_dequant_gemv_group(const std::vector<Handle>& handles, torch::Tensor x,
+                                                    const std::vector<std::vector<int64_t>>& weight_shapes,
+                                                    const std::string& gguf_type,
+                                                    const std::vector<int64_t>& offsets) {
+    const char* where = "py_fused_dequant_gemv_group";
+    const size_t n = handles.size();
+    if (n < 1 || n > 4 || weight_shapes.size() != n || offsets.size() != n)
+        throw std::runtime_error(std::string(where) + ": 1 to 4 handles with one shape and offset each");
+    const int64_t bb = gguf_block_bytes(gguf_type, where);
+    const int64_t in_dim = weight_shapes[0].size() == 2 ? weight_shapes[0][1] : -1;
+    for (size_t i = 0; i < n; ++i) {
+        check_handle(handles[i], where);
+        if (weight_shapes[i].size() != 2 || weight_shapes[i][1] != in_dim)
+            throw std::runtime_error(std::string(where) + ": weight shapes must be [out_dim, in_dim] with one in_dim");
+        if (handles[i]->device_id() != handles[0]->device_id())
+            throw std::runtime_error(std::string(where) + ": buffers on different devices");
+        check_range(handles[i], offsets[i], weight_shapes[i][0] * (in_dim / 32) * bb, where);
+    }
+    if (in_dim % 32 != 0) throw std::runtime_error(std::string(where) + ": in_dim must be a multiple of 32");
+    torch::Tensor xf = x.contiguous();
+    const int64_t batch = in_dim > 0 ? xf.numel() / in_dim : 0;
+    if (batch < 1 || batch > 8 || batch * in_dim != xf.numel() || xf.size(-1) != in_dim)
+        throw std::runtime_error(std::string(where) + ": x must be [batch <= 8, in_dim]");
+    const int dev = handles[0]->device_id();
+    check_x(xf, dev, where);
+    std::vector<torch::Tensor> outs;
+    const void* w[4];
+    void* y[4];
+    int64_t m[4];
+    for (size_t i = 0; i < n; ++i) {
+        outs.push_back(torch::empty({batch, weight_shapes[i][0]}, fp16_on(dev)));
+        w[i] = at_offset(handles[i], offsets[i]);
+        y[i] = outs.back().data_ptr();
+        m[i] = weight_shapes[i][0];
+    }
+    const OnDevice on(dev);
+    const int rc = gguf_type == "q4_0"
+                       ? gdsllm_fused_q4_0_gemv_group(static_cast<int>(n), w, y, m, xf.data_ptr(), in_dim, batch,
+                                                      in_dim, on.stream())
+                       : gdsllm_fused_q8_0_gemv_group(static_cast<int>(n), w, y, m, xf.data_ptr(), in_dim, batch,
+                                                      in_dim, on.stream());
+    check(rc, where);
+    return outs;
+}
+
+// h = fp16(silu(fp16(gate . x)) * fp16(up . x)) in one launch (the MLP's
+// runtime/llama.py:253-256 before the down projection).  Returns None when
+// the shape is outside the fused kernel (batch > 2, in_dim % 256 != 0): the
+// caller then runs the projections separately.
+py::object fused_gate_up_silu(const Handle& gate, const Handle& up, torch::Tensor x,
+                              std::vector<int64_t> weight_shape, const std::string& gguf_type, int64_t gate_offset,
+                              int64_t up_offset) {
+    const char* where = "py_fused_gate_up_silu";
+    check_handle(gate, where);
+    check_handle(up, where);
+    if (weight_shape.size() != 2) throw std::runtime_error(std::string(where) + ": weight_shape must be [out_dim, in_dim]");
+    const int64_t out_dim = weight_shape[0], in_dim = weight_shape[1];
+    if (in_dim % 32 != 0) throw std::runtime_error(std::string(where) + ": in_dim must be a multiple of 32");
+    const int64_t bb = gguf_block_bytes(gguf_type, where);
+    check_range(gate, gate_offset, out_dim * (in_dim / 32) * bb, where);
+    check_range(up, up_offset, out_dim * (in_dim / 32) * bb, where);
+    if (gate->device_id() != up->device_id()) throw std::runtime_error(std::string(where) + ": buffers on different devices");
+    torch::Tensor xf = x.contiguous();
+    const int64_t batch = in_dim > 0 ? xf.numel() / in_dim : 0;
+    if (batch < 1 || batch * in_dim != xf.numel() || xf.size(-1) != in_dim)
+        throw std::runtime_error(std::string(where) + ": x must be [batch, in_dim]");
+    const int dev = gate->device_id();
+    check_x(xf, dev, where);
+    torch::Tensor h = torch::empty({batch, out_dim}, fp16_on(dev));
+    const OnDevice on(dev);
+    const int rc = gguf_type == "q4_0"
+                       ? gdsllm_fused_q4_0_gate_up_silu(at_offset(gate, gate_offset), at_offset(up, up_offset),
+                                                        xf.data_ptr(), h.data_ptr(), out_dim, in_dim, batch, in_dim,
+                                                        out_dim, on.stream())
+                       : gdsllm_fused_q8_0_gate_up_silu(at_offset(gate, gate_offset), at_offset(up, up_offset),
+                                                        xf.data_ptr(), h.data_ptr(), out_dim, in_dim, batch, in_dim,
+                                                        out_dim, on.stream());
+    if (rc == GDSLLM_ERR_UNSUPPORTED) return py::none();
+    check(rc, where);
+    return py::cast(h);
+}
+
 Handle from_tensor(const torch::Tensor& t) { return std::make_shared<GdsBufferHandle>(t); }
 
 }  // namespace
@@ -696,6 +780,13 @@ PYBIND11_MODULE(gds_io_ext, m) {
           py::arg("handle"), py::arg("token_ids"), py::arg("shape"), py::arg("gguf_type"), py::arg("offset") = 0);
     m.def("fused_dequant_gemv", &fused_dequant_gemv, "Fused dequant + GEMV for Q4_0/Q8_0 (decode).",
           py::arg("handle"), py::arg("x"), py::arg("weight_shape"), py::arg("gguf_type"), py::arg("offset"));
+    m.def("fused_dequant_gemv_group", &fused_dequant_gemv_group,
+          "Up to 4 fused dequant + GEMVs sharing x in one launch (decode q/k/v).", py::arg("handles"), py::arg("x"),
+          py::arg("weight_shapes"), py::arg("gguf_type"), py::arg("offsets"));
+    m.def("fused_gate_up_silu", &fused_gate_up_silu,
+          "fp16(silu(gate . x) * (up . x)) in one launch (decode MLP); None when the shape needs separate launches.",
+          py::arg("gate_handle"), py::arg("up_handle"), py::arg("x"), py::arg("weight_shape"), py::arg("gguf_type"),
+          py::arg("gate_offset"), py::arg("up_offset"));
     m.def("dequant_affine_q4", &dequant_affine_q4, "Dequantize affine Q4 (uint32 + scales + biases) to fp16.",
           py::arg("handle"), py::arg("weight_shape"), py::arg("weight_offset"), py::arg("scale_offset"),
           py::arg("bias_offset"), py::arg("group_size"), py::arg("output") = py::none());

@@ -12,6 +12,11 @@ the same contract:
     gds_io_ext.int8_linear: a fused GEMV at decode, a bit-exact dequant and one
     GEMM at prefill, instead of an fp32 copy of the whole matrix per call.
 Q8_0 prefill keeps the reference's dequant -> F.linear route.
+
+The decode step's fused launches are exposed as the reference's own units:
+qkv_projections (the three dequant_linear calls of runtime/llama.py:212-214 in
+one launch) and mlp (runtime/llama.py:247-256: gate, up and F.silu(gate)*up in
+one launch, then down).
 """
 
 from __future__ import annotations
@@ -62,3 +67,40 @@ def dequant_linear(
         # dequant and one GEMM (no fp32 copy of the matrix)
         return ext().int8_linear(w, weights[f"{name}.scale"], x)
     return F.linear(x, w)
+
+
+def _gguf_decode(x: torch.Tensor, metas) -> bool:
+    """Decode (x [B, 1, K], B <= 8) over GGUF weights of one type sharing a buffer device."""
+    return (x.dim() == 3 and x.shape[1] == 1 and x.shape[0] <= 8 and
+            all(isinstance(m, dict) and "gguf_type" in m for m in metas) and
+            len({m["gguf_type"] for m in metas}) == 1)
+
+
+def qkv_projections(x: torch.Tensor, weights: Dict, scratch: Optional[torch.Tensor] = None):
+    """(xq, xk, xv) = the q/k/v projections of runtime/llama.py:212-214; at
+    decode over GGUF weights one grouped launch reads x once for all three."""
+    names = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj")
+    metas = [weights[f"{n}.weight"] for n in names]
+    if _gguf_decode(x, metas):
+        batch = x.shape[0]
+        outs = ext().fused_dequant_gemv_group([m["buffer"] for m in metas], x.reshape(batch, -1),
+                                              [list(m["shape"]) for m in metas], metas[0]["gguf_type"],
+                                              [m["offset"] for m in metas])
+        return tuple(o.unsqueeze(1) for o in outs)
+    return tuple(dequant_linear(x, weights, n, scratch) for n in names)
+
+
+def mlp(x: torch.Tensor, weights: Dict, scratch: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """SwiGLU MLP (runtime/llama.py:247-256).  At decode over GGUF weights,
+    h = fp16(silu(gate x) * (up x)) comes from one launch that never writes
+    gate or up (torch's fp16 rounding of silu and of the product), then down."""
+    g, u = weights["mlp.gate_proj.weight"], weights["mlp.up_proj.weight"]
+    if _gguf_decode(x, (g, u)) and list(g["shape"]) == list(u["shape"]):
+        batch = x.shape[0]
+        h = ext().fused_gate_up_silu(g["buffer"], u["buffer"], x.reshape(batch, -1), list(g["shape"]),
+                                     g["gguf_type"], g["offset"], u["offset"])
+        if h is not None:
+            return dequant_linear(h.unsqueeze(1), weights, "mlp.down_proj", scratch)
+    gate = dequant_linear(x, weights, "mlp.gate_proj", scratch)
+    up = dequant_linear(x, weights, "mlp.up_proj", scratch)
+    return dequant_linear(F.silu(gate) * up, weights, "mlp.down_proj", scratch)

@@ -11,11 +11,15 @@ changes, both on the fast side of the same contract:
     at decode and the MFMA dequant-GEMM for Q4_0 prefill, instead of dequant
     into a temporary plus F.linear; an int8 lm_head goes through
     gds_io_ext.int8_linear instead of an fp32 copy of the matrix.
+
+DecodeSweep drives the projection work of a cached decode step (the
+reference's CachedScheduler.forward) as one HIP graph per token.
 """
 
 from __future__ import annotations
 
-from typing import Optional
+import ctypes
+from typing import Optional, Sequence
 
 import torch
 import torch.nn.functional as F
@@ -45,3 +49,118 @@ def _lm_head_proj(h: torch.Tensor, tensors: dict, key: str = "lm_head.weight",
     if w.dtype == torch.int8:
         return ext().int8_linear(w, tensors[key[: -len(".weight")] + ".scale"], h)
     return F.linear(h, w)
+
+
+_LAYER_PROJ = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
+               "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj")
+
+
+def _ptr(meta: dict) -> int:
+    return int(meta["buffer"].data_ptr) + int(meta["offset"])
+
+
+class DecodeSweep:
+    """The projection work of one decode step of CachedScheduler.forward
+    (runtime/scheduler.py:303-386) over resident GGUF layers, captured once
+    into a HIP graph and replayed per token.
+
+    Per layer, as transformer_block issues them (runtime/llama.py:259-285 via
+    :212-214 and :247-256): q/k/v on the attention input in one grouped
+    launch, o_proj on the attention output, gate/up/SiLU on the MLP input in
+    one launch writing h, down_proj on h; after the last layer, lm_head on
+    the final hidden state: 4 launches per layer + 1 (129 for LLaMA-7B, where
+    the reference issues 7 per layer + a dequant and a GEMM for lm_head).
+
+    Attention, RoPE, the norms and the residual adds are not matvec work and
+    stay with the caller, which writes each layer's inputs (attn_in[l],
+    attn_out[l], mlp_in[l]: fp16 [batch, hidden]; final_in: [batch, hidden])
+    before run() and reads q[l], k[l], v[l], o[l], h[l], down[l] and logits.
+
+    layers[l]: the layer's weight dict (entries {"buffer", "shape",
+    "gguf_type", "offset"} as ModelWeights.load_layer gives them); lm_head:
+    the lm_head entry.  All weights one GGUF type; batch 1 or 2 (the fused
+    gate/up/SiLU launch serves up to 2 rows).
+    """
+
+    def __init__(self, layers: Sequence[dict], lm_head: dict, batch: int = 1, device=None, use_graph: bool = True):
+        from gdsllm_amd import capi
+
+        if not layers:
+            raise ValueError("DecodeSweep: no layers")
+        if batch not in (1, 2):
+            raise ValueError("DecodeSweep: batch must be 1 or 2")
+        metas = [[lw[f"{p}.weight"] for p in _LAYER_PROJ] for lw in layers]
+        fmt = lm_head.get("gguf_type")
+        for lm in metas:
+            for m in lm:
+                if not isinstance(m, dict) or m.get("gguf_type") != fmt:
+                    raise ValueError("DecodeSweep: every projection and lm_head must be one GGUF type")
+        if fmt not in ("q4_0", "q8_0"):
+            raise ValueError(f"DecodeSweep: unsupported GGUF type {fmt!r}")
+        self.lib, self.fmt, self.batch, self.use_graph = capi(), fmt, batch, use_graph
+        self.metas, self.lm_head = metas, lm_head
+        dev = torch.device(device) if device is not None else torch.device("cuda", lm_head["buffer"].device_id)
+        H = int(metas[0][0]["shape"][1])
+        Fd = int(metas[0][4]["shape"][0])
+        for lm in metas:
+            if any(int(m["shape"][1]) != H for m in lm[:6]) or int(lm[6]["shape"][1]) != Fd or \
+                    int(lm[6]["shape"][0]) != H or [int(v) for v in lm[5]["shape"]] != [Fd, H]:
+                raise ValueError("DecodeSweep: layer shapes disagree")
+        self.hidden, self.ffn, self.vocab = H, Fd, int(lm_head["shape"][0])
+
+        def buf(n):
+            return torch.zeros(batch, n, dtype=torch.float16, device=dev)
+
+        L = len(metas)
+        self.attn_in = [buf(H) for _ in range(L)]
+        self.attn_out = [buf(int(lm[3]["shape"][1])) for lm in metas]
+        self.mlp_in = [buf(H) for _ in range(L)]
+        self.final_in = buf(int(lm_head["shape"][1]))
+        self.q, self.k, self.v, self.o = ([buf(int(lm[i]["shape"][0])) for lm in metas] for i in range(4))
+        self.h = [buf(Fd) for _ in range(L)]
+        self.down = [buf(H) for _ in range(L)]
+        self.logits = buf(self.vocab)
+        c_vp, c_i64 = ctypes.c_void_p, ctypes.c_int64
+        self._qkv = [((c_vp * 3)(*[_ptr(m) for m in lm[:3]]),
+                      (c_vp * 3)(self.q[i].data_ptr(), self.k[i].data_ptr(), self.v[i].data_ptr()),
+                      (c_i64 * 3)(*[int(m["shape"][0]) for m in lm[:3]])) for i, lm in enumerate(metas)]
+        self._graph = None
+
+    def _launch_all(self) -> None:
+        from gdsllm_amd import check
+
+        lib, B = self.lib, self.batch
+        gemv = lib.gdsllm_fused_q4_0_gemv if self.fmt == "q4_0" else lib.gdsllm_fused_q8_0_gemv
+        group = lib.gdsllm_fused_q4_0_gemv_group if self.fmt == "q4_0" else lib.gdsllm_fused_q8_0_gemv_group
+        gate_up = lib.gdsllm_fused_q4_0_gate_up_silu if self.fmt == "q4_0" else lib.gdsllm_fused_q8_0_gate_up_silu
+        s = torch.cuda.current_stream().cuda_stream
+        H, Fd = self.hidden, self.ffn
+        for i, lm in enumerate(self.metas):
+            w3, y3, m3 = self._qkv[i]
+            check(group(3, w3, y3, m3, self.attn_in[i].data_ptr(), H, B, H, s))
+            mo, ko = (int(v) for v in lm[3]["shape"])
+            check(gemv(_ptr(lm[3]), self.attn_out[i].data_ptr(), self.o[i].data_ptr(), mo, ko, B, ko, mo, s))
+            rc = gate_up(_ptr(lm[4]), _ptr(lm[5]), self.mlp_in[i].data_ptr(), self.h[i].data_ptr(), Fd, H, B, H, Fd, s)
+            if rc != 0:
+                check(rc)
+            check(gemv(_ptr(lm[6]), self.h[i].data_ptr(), self.down[i].data_ptr(), H, Fd, B, Fd, H, s))
+        mv, kv = self.vocab, int(self.lm_head["shape"][1])
+        check(gemv(_ptr(self.lm_head), self.final_in.data_ptr(), self.logits.data_ptr(), mv, kv, B, kv, mv, s))
+
+    def run(self) -> None:
+        """One token's projections on the current stream (asynchronous)."""
+        if not self.use_graph:
+            self._launch_all()
+            return
+        if self._graph is None:
+            self._launch_all()  # loads the kernels and plans the launches outside capture
+            torch.cuda.current_stream().synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                self._launch_all()
+            self._graph = graph
+        self._graph.replay()
+
+    @property
+    def launches_per_token(self) -> int:
+        return 4 * len(self.metas) + 1

@@ -252,6 +252,9 @@ def test_extension_module_surface():
         "dequant_int8": ["weight", "scale", "output"],
         "int8_linear": ["weight", "scale", "x"],
         "moe_step_affine_q4": ["x", "entries", "top_k_indices", "top_k_weights", "shared_gate_weight"],
+        "fused_dequant_gemv_group": ["handles", "x", "weight_shapes", "gguf_type", "offsets"],
+        "fused_gate_up_silu": ["gate_handle", "up_handle", "x", "weight_shape", "gguf_type", "gate_offset",
+                               "up_offset"],
     }
     for name, args in expected.items():
         fn = getattr(m, name)

@@ -586,6 +586,146 @@ def bench_prefill(dev, layers, lm_head, tokens: int = 512, reps: int = 3):
             "pct_of_fp16_dense_peak": round(flops / (ms * 1e-3) / 1e12 / 25, 1), "per_shape": per_shape}
 
 
+def bench_prefill_formats(dev, tokens: int = 512, reps: int = 20):
+    """Q8_0 and affine-Q4 (group 64) prefill on the MFMA dequant-GEMM at the
+    LLaMA-7B projection shapes with a 512-token chunk, per shape against the
+    reference's route: the dequant kernel into an fp16 scratch matrix, then the
+    vendor fp16 GEMM (hipBLASLt through torch.mm), runtime/llama.py:160-166 and
+    runtime/qwen_moe.py:69-73."""
+    import torch
+
+    from gdsllm_amd import capi, check
+    from gdsllm_amd import synthetic as syn
+
+    lib = capi()
+    gen = torch.Generator(device=dev).manual_seed(1007)
+    xs = {k: syn.activations(tokens, k, gen) for k in (4096, 11008)}
+    out = {}
+    layer_fused = {"q8_0": 0.0, "affine_g64": 0.0}
+    layer_route = {"q8_0": 0.0, "affine_g64": 0.0}
+    for m, k in sorted(set(LAYER_SHAPES)):
+        n_in_layer = LAYER_SHAPES.count((m, k))
+        y = torch.empty(tokens, m, dtype=torch.float16, device=dev)
+        wdq = torch.empty(m, k, dtype=torch.float16, device=dev)
+        w8 = syn.q8_0_weights(m, k, gen)
+        aw, asc, ab = syn.affine_q4_weights([m, k], 64, gen)
+        st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+        runs = {
+            "q8_0": (lambda: check(lib.gdsllm_dequant_gemm_q8_0(w8.data_ptr(), xs[k].data_ptr(), y.data_ptr(), m, k,
+                                                                 tokens, k, m, st())),
+                     lambda: check(lib.gdsllm_dequant_q8_0(w8.data_ptr(), wdq.data_ptr(), m * k // 32, st()))),
+            "affine_g64": (lambda: check(lib.gdsllm_dequant_gemm_affine_q4(aw.data_ptr(), asc.data_ptr(), ab.data_ptr(),
+                                                                           xs[k].data_ptr(), y.data_ptr(), m, k, 64,
+                                                                           tokens, k, m, st())),
+                           lambda: check(lib.gdsllm_dequant_affine_q4(aw.data_ptr(), asc.data_ptr(), ab.data_ptr(),
+                                                                      wdq.data_ptr(), m * k, k, 64, st()))),
+        }
+        mm_us = _replay_ms(lambda: torch.mm(xs[k], wdq.t(), out=y), reps) * 1e3
+        fl = 2 * tokens * m * k
+        for fmt, (fused, dq) in runs.items():
+            f_us = _replay_ms(fused, reps) * 1e3
+            d_us = _replay_ms(dq, reps) * 1e3
+            r_us = _replay_ms(lambda: (dq(), torch.mm(xs[k], wdq.t(), out=y)), reps) * 1e3
+            out.setdefault(fmt, {})[f"{m}x{k}"] = {
+                "fused_us": round(f_us, 2), "fused_TFLOP_s": round(fl / (f_us * 1e-6) / 1e12, 1),
+                "dequant_then_hipblaslt_us": round(r_us, 2), "dequant_us": round(d_us, 2),
+                "hipblaslt_fp16_gemm_us": round(mm_us, 2), "fused_faster": bool(f_us < r_us)}
+            layer_fused[fmt] += n_in_layer * f_us
+            layer_route[fmt] += n_in_layer * r_us
+        del w8, aw, asc, ab, wdq, y
+    for fmt in out:
+        out[fmt]["layer_7b_512_tokens"] = {"fused_us": round(layer_fused[fmt], 1),
+                                           "dequant_then_hipblaslt_us": round(layer_route[fmt], 1)}
+    return out
+
+
+def bench_moe_prefill(dev, tokens: int = 512, reps: int = 5):
+    """Routed-expert MLP of a 512-token prefill chunk over the resident
+    512-expert affine-Q4 pool (hidden 4096, ffn 1024, group 64, top-10, random
+    distinct picks per token): the grouped MFMA path (4 launches, no host
+    sync) against the reference's route for the same chunk, the per-expert loop
+    of runtime/qwen_moe.py:475-492 (host sync per slot, dequant of each expert's
+    three matrices, three fp16 GEMMs, weighted scatter-add)."""
+    import ctypes
+
+    import torch
+
+    from gdsllm_amd import AffineExperts, capi, check
+    from gdsllm_amd import synthetic as syn
+
+    E, H, Fd, g, k = 512, 4096, 1024, 64, 10
+    gen = torch.Generator(device=dev).manual_seed(1008)
+    pools = [syn.affine_q4_weights([E, Fd, H], g, gen), syn.affine_q4_weights([E, Fd, H], g, gen),
+             syn.affine_q4_weights([E, H, Fd], g, gen)]
+
+    def experts(p):
+        w, sc, bi = p
+        e, n, kw = w.shape
+        kk = kw * 8
+        return AffineExperts(w.data_ptr(), sc.data_ptr(), bi.data_ptr(), n * kw * 4, n * (kk // g) * 2,
+                             n * (kk // g) * 2, e, n, kk, g)
+
+    gate, up, down = (experts(p) for p in pools)
+    cg = torch.Generator().manual_seed(1009)
+    idx = torch.stack([torch.randperm(E, generator=cg)[:k] for _ in range(tokens)]).to(torch.int32).to(dev)
+    wts = torch.softmax(torch.randn(tokens, k, generator=cg), -1).to(torch.float16).to(dev)
+    x = syn.activations(tokens, H, gen)
+    y = torch.empty(tokens, H, dtype=torch.float16, device=dev)
+    lib = capi()
+    ws_bytes = lib.gdsllm_moe_prefill_workspace_size(tokens, k, Fd, H, E)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+
+    def run():
+        check(lib.gdsllm_moe_prefill_affine_q4(ctypes.byref(gate), ctypes.byref(up), ctypes.byref(down), x.data_ptr(),
+                                               H, idx.data_ptr(), wts.data_ptr(), tokens, k, y.data_ptr(), H,
+                                               ws.data_ptr(), ws_bytes, torch.cuda.current_stream().cuda_stream))
+
+    ms = _replay_ms(run, reps)
+    used = sorted(set(idx.reshape(-1).tolist()))
+    per_expert = 3 * (Fd * H // 2 + 2 * 2 * Fd * H // g)
+    wbytes = len(used) * per_expert
+    flops = 2 * tokens * k * 3 * Fd * H
+
+    # the reference's route, eagerly (it syncs to the host for every expert id)
+    gd = torch.empty(Fd, H, dtype=torch.float16, device=dev)
+    ud = torch.empty(Fd, H, dtype=torch.float16, device=dev)
+    dd = torch.empty(H, Fd, dtype=torch.float16, device=dev)
+
+    def deq(pool, e, out, n, kk):
+        w, sc, bi = (t[e] for t in pool)
+        check(lib.gdsllm_dequant_affine_q4(w.data_ptr(), sc.data_ptr(), bi.data_ptr(), out.data_ptr(), n * kk, kk, g,
+                                           torch.cuda.current_stream().cuda_stream))
+
+    def reference_route():
+        eo = torch.zeros(tokens, H, dtype=torch.float16, device=dev)
+        for j in range(k):
+            ids = idx[:, j]
+            for e in ids.unique().tolist():
+                mask = ids == e
+                xs_ = x[mask]
+                deq(pools[0], e, gd, Fd, H)
+                gate_o = torch.nn.functional.linear(xs_, gd)
+                deq(pools[1], e, ud, Fd, H)
+                up_o = torch.nn.functional.linear(xs_, ud)
+                deq(pools[2], e, dd, H, Fd)
+                down_o = torch.nn.functional.linear(torch.nn.functional.silu(gate_o) * up_o, dd)
+                eo[mask] += wts[mask, j].unsqueeze(-1) * down_o
+        return eo
+
+    reference_route()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ref = reference_route()
+    torch.cuda.synchronize()
+    ref_ms = (time.perf_counter() - t0) * 1e3
+    rel = float(torch.linalg.vector_norm((y.float() - ref.float())) / torch.linalg.vector_norm(ref.float()))
+    return {"us_per_chunk": round(ms * 1e3, 1), "tokens": tokens, "top_k": k, "experts_used": len(used),
+            "weight_bytes": wbytes, "weight_GB_s": round(wbytes / (ms * 1e-3) / 1e9, 1),
+            "TFLOP_s": round(flops / (ms * 1e-3) / 1e12, 1), "launches": 4, "host_syncs": 0,
+            "reference_route_ms": round(ref_ms, 2), "speedup_vs_reference_route": round(ref_ms / ms, 1),
+            "rel_l2_vs_reference_route": rel}
+
+
 def bench_load(dev, layers: int = 2, reps: int = 3, tokens: int = 512, emb_reps: int = 20):
     """Converted LLaMA-7B Q4_0 directory (files written first, so they are page-
     cache resident): one layer file (113 MB) into HBM through
@@ -772,10 +912,11 @@ def main() -> int:
                     help="run only one workload, eagerly, for a profiler: gemm:M,K,T (Q4_0 prefill GEMM), "
                          "gemv:M,K,B (Q4_0 GEMV), moe (top-10 gather, fresh picks per call); then exit")
     ap.add_argument("--profile-reps", type=int, default=10, help="launches of --profile-case")
-    ap.add_argument("--configs", default="ceiling,q8,moe,70b,prefill,load,int8",
+    ap.add_argument("--configs", default="ceiling,q8,moe,70b,prefill,prefill_fmt,moe_prefill,load",
                     help="comma list of extra workloads to measure: ceiling (plain read of the headline's bytes, "
                          "empty launch), q8 (Q8_0 7B layer), moe (top-10 expert "
-                         "gather), 70b (Q4_0 70B layer, B=1..8), prefill (512-token MFMA GEMM), load (7B layer "
+                         "gather), 70b (Q4_0 70B layer, B=1..8), prefill (512-token MFMA GEMM), prefill_fmt (Q8_0 "
+                         "and affine-Q4 prefill GEMMs), moe_prefill (512-token grouped-expert MLP), load (7B layer "
                          "file -> HBM, embedding row gather), int8 (per-column int8 7B layer); '' = none")
     args = ap.parse_args()
 
@@ -818,7 +959,7 @@ def main() -> int:
               f"(unfused 225 launches: {sweep['unfused']['tok_s']} tok/s)", file=sys.stderr, flush=True)
 
     wanted = {c.strip() for c in args.configs.split(",") if c.strip()}
-    unknown = wanted - {"ceiling", "q8", "moe", "70b", "prefill", "load", "int8"}
+    unknown = wanted - {"ceiling", "q8", "moe", "70b", "prefill", "prefill_fmt", "moe_prefill", "load", "int8"}
     if unknown:
         print(f"bench.py: unknown --configs entries {sorted(unknown)}", file=sys.stderr)
         return 2
@@ -829,6 +970,8 @@ def main() -> int:
             ("70b", "q4_0_layer_70b", lambda: bench_70b_layer(dev)),
             ("prefill", "prefill_7b_512",
              lambda: bench_prefill(dev, *sweep_weights) if sweep_weights is not None else None),
+            ("prefill_fmt", "prefill_q8_0_affine_7b_512", lambda: bench_prefill_formats(dev)),
+            ("moe_prefill", "moe_prefill_affine_q4_512", lambda: bench_moe_prefill(dev)),
             ("load", "load_7b_q4_0", lambda: bench_load(dev)),
             ("int8", "int8_layer_7b_b1", lambda: bench_int8_layer(dev))]
     for key, name, fn in runs:

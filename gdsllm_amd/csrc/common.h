@@ -32,6 +32,11 @@ int blocks_per_cu(const void* fn, size_t lds, int threads);
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Q4_0 prefill GEMM for in_dim % 32 == 0 off the split-K grid (gemm.hip);
+// arguments already validated.
+int dequant_gemm_q4_0_blockwise(const void* weight, const void* x, void* y, int M, int K, int T, int64_t ldx,
+                                int64_t ldy, hipStream_t stream);
+
 // ---------------------------------------------------------------- device side
 
 typedef _Float16 half_t;

@@ -504,26 +504,89 @@ std::optional<torch::Tensor> moe_step_affine_q4(torch::Tensor x, std::vector<Aff
     return out;
 }
 
-// Prefill: x [T, in_dim] fp16 -> [T, out_dim] fp16 on the MFMA dequant-GEMM.
-torch::Tensor fused_dequant_gemm(const Handle& h, torch::Tensor x, std::vector<int64_t> weight_shape,
-                                 const std::string& gguf_type, int64_t offset) {
+// Prefill: x [..., in_dim] fp16 -> [..., out_dim] fp16 on the MFMA dequant-GEMM
+// (Q4_0 or Q8_0).  None when the library cannot serve the shape or alignment
+// (the caller then takes the reference's dequant -> F.linear route).
+std::optional<torch::Tensor> fused_dequant_gemm(const Handle& h, torch::Tensor x, std::vector<int64_t> weight_shape,
+                                                const std::string& gguf_type, int64_t offset) {
     const char* where = "fused_dequant_gemm";
     check_handle(h, where);
     if (weight_shape.size() != 2) throw std::runtime_error(std::string(where) + ": weight_shape must be [out_dim, in_dim]");
-    if (gguf_type != "q4_0") throw std::runtime_error(std::string(where) + ": unsupported type '" + gguf_type + "'");
+    if (gguf_type != "q4_0" && gguf_type != "q8_0")
+        throw std::runtime_error(std::string(where) + ": unsupported type '" + gguf_type + "'");
+    const bool q4 = gguf_type == "q4_0";
     const int64_t out_dim = weight_shape[0], in_dim = weight_shape[1];
     torch::Tensor xf = x.contiguous();
     check_x(xf, h->device_id(), where);
     if (in_dim <= 0 || xf.size(-1) != in_dim)
         throw std::runtime_error(std::string(where) + ": last dim of x must equal in_dim " + std::to_string(in_dim));
     const int64_t tokens = xf.numel() / in_dim;
-    check_range(h, offset, out_dim * (in_dim / 32) * 18, where);
+    check_range(h, offset, out_dim * (in_dim / 32) * (q4 ? 18 : 34), where);
     auto out_shape = xf.sizes().vec();
     out_shape.back() = out_dim;
     torch::Tensor out = torch::empty(out_shape, fp16_on(h->device_id()));
-    check(gdsllm_dequant_gemm_q4_0(at_offset(h, offset), xf.data_ptr(), out.data_ptr(), out_dim, in_dim, tokens,
-                                   in_dim, out_dim, OnDevice(h->device_id()).stream()),
-          where);
+    const int rc = (q4 ? gdsllm_dequant_gemm_q4_0 : gdsllm_dequant_gemm_q8_0)(
+        at_offset(h, offset), xf.data_ptr(), out.data_ptr(), out_dim, in_dim, tokens, in_dim, out_dim,
+        OnDevice(h->device_id()).stream());
+    if (rc == GDSLLM_ERR_UNSUPPORTED) return std::nullopt;
+    check(rc, where);
+    return out;
+}
+
+// Prefill affine-Q4 projection: x [..., in_dim] -> [..., out_dim] on the MFMA
+// dequant-GEMM; None for shapes, groupings or alignments it does not serve.
+std::optional<torch::Tensor> fused_affine_q4_gemm(const Handle& h, torch::Tensor x, std::vector<int64_t> weight_shape,
+                                                  int64_t weight_offset, int64_t scale_offset, int64_t bias_offset,
+                                                  int64_t group_size) {
+    const char* where = "fused_affine_q4_gemm";
+    check_handle(h, where);
+    if (weight_shape.size() != 2) throw std::runtime_error(std::string(where) + ": weight_shape must be [out_dim, in_dim]");
+    const int64_t out_dim = weight_shape[0], in_dim = weight_shape[1];
+    torch::Tensor xf = x.contiguous();
+    check_x(xf, h->device_id(), where);
+    if (in_dim <= 0 || xf.size(-1) != in_dim)
+        throw std::runtime_error(std::string(where) + ": last dim of x must equal in_dim " + std::to_string(in_dim));
+    const int64_t tokens = xf.numel() / in_dim;
+    const auto p = affine_ptrs(h, out_dim, in_dim, weight_offset, scale_offset, bias_offset, group_size, where);
+    auto out_shape = xf.sizes().vec();
+    out_shape.back() = out_dim;
+    torch::Tensor out = torch::empty(out_shape, fp16_on(h->device_id()));
+    const int rc = gdsllm_dequant_gemm_affine_q4(p.w, p.s, p.b, xf.data_ptr(), out.data_ptr(), out_dim, in_dim,
+                                                 group_size, tokens, in_dim, out_dim, OnDevice(h->device_id()).stream());
+    if (rc == GDSLLM_ERR_UNSUPPORTED) return std::nullopt;
+    check(rc, where);
+    return out;
+}
+
+// Prefill routed-expert MLP over resident stacked experts (the prefill branch
+// of runtime/qwen_moe.py:475-492): x [T, hidden], top-k indices / weights
+// [T, k]; returns expert_output [T, hidden] fp16, or None for shapes the
+// grouped GEMM does not serve.
+std::optional<torch::Tensor> moe_prefill_affine_q4(torch::Tensor x, std::vector<AffineEntry> entries,
+                                                   torch::Tensor top_k_indices, torch::Tensor top_k_weights) {
+    const char* where = "moe_prefill_affine_q4";
+    if (entries.size() != 3) throw std::runtime_error(std::string(where) + ": expects gate, up, down");
+    gdsllm_affine_experts e[3];
+    for (int i = 0; i < 3; ++i) e[i] = experts_of(entries[i], where);
+    const int dev = std::get<0>(entries[0])->device_id();
+    torch::Tensor xf = x.contiguous();
+    check_x(xf, dev, where);
+    const int64_t H = e[0].in_dim;
+    if (xf.size(-1) != H) throw std::runtime_error(std::string(where) + ": last dim of x must equal hidden " + std::to_string(H));
+    const int64_t T = xf.numel() / H;
+    torch::Tensor idx = top_k_indices.to(torch::TensorOptions().dtype(torch::kInt32).device(torch::kCUDA, dev)).contiguous();
+    torch::Tensor wts = top_k_weights.to(torch::TensorOptions().dtype(torch::kFloat16).device(torch::kCUDA, dev)).contiguous();
+    if (T == 0 || idx.numel() % T != 0 || wts.numel() != idx.numel())
+        throw std::runtime_error(std::string(where) + ": indices and weights must be [tokens, k]");
+    const int64_t k = idx.numel() / T;
+    const size_t ws_bytes = gdsllm_moe_prefill_workspace_size(T, k, e[0].out_dim, H, e[0].num_experts);
+    torch::Tensor ws = torch::empty({static_cast<int64_t>(ws_bytes)}, torch::TensorOptions().dtype(torch::kUInt8).device(torch::kCUDA, dev));
+    torch::Tensor out = torch::empty({T, H}, fp16_on(dev));
+    const int rc = gdsllm_moe_prefill_affine_q4(&e[0], &e[1], &e[2], xf.data_ptr(), H, idx.data_ptr<int32_t>(),
+                                                wts.data_ptr(), T, k, out.data_ptr(), H, ws.data_ptr(), ws_bytes,
+                                                OnDevice(dev).stream());
+    if (rc == GDSLLM_ERR_UNSUPPORTED) return std::nullopt;
+    check(rc, where);
     return out;
 }
 
@@ -806,7 +869,14 @@ PYBIND11_MODULE(gds_io_ext, m) {
           "Decode MoE MLP after routing (top-k experts, shared expert, sigmoid-gated combine) in two launches.",
           py::arg("x"), py::arg("entries"), py::arg("top_k_indices"), py::arg("top_k_weights"),
           py::arg("shared_gate_weight"));
-    m.def("fused_dequant_gemm", &fused_dequant_gemm, "Prefill Q4_0 dequant-GEMM on MFMA: x [T, K] -> [T, M].",
+    m.def("fused_affine_q4_gemm", &fused_affine_q4_gemm,
+          "Prefill affine-Q4 dequant-GEMM on MFMA: x [..., K] -> [..., M] (None if not served).", py::arg("handle"),
+          py::arg("x"), py::arg("weight_shape"), py::arg("weight_offset"), py::arg("scale_offset"),
+          py::arg("bias_offset"), py::arg("group_size"));
+    m.def("moe_prefill_affine_q4", &moe_prefill_affine_q4,
+          "Prefill routed-expert MLP over stacked experts: x [T, H] -> expert_output [T, H] (None if not served).",
+          py::arg("x"), py::arg("entries"), py::arg("top_k_indices"), py::arg("top_k_weights"));
+    m.def("fused_dequant_gemm", &fused_dequant_gemm, "Prefill Q4_0/Q8_0 dequant-GEMM on MFMA: x [T, K] -> [T, M] (None if not served).",
           py::arg("handle"), py::arg("x"), py::arg("weight_shape"), py::arg("gguf_type"), py::arg("offset"));
     m.def("gemv_f16", &gemv_f16, "fp16-weight GEMV (router, shared-expert gate): x [..., K] -> [..., M].",
           py::arg("weight"), py::arg("x"));

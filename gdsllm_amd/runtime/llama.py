@@ -7,11 +7,11 @@ arguments and weight-metadata dicts ({"buffer", "shape", "gguf_type",
 the same contract:
   * decode with batch > 1 (x [B, 1, K], B <= 8) runs one batched fused GEMV
     instead of failing the reference's x.view(-1) size check;
-  * Q4_0 prefill runs the fused MFMA dequant-GEMM instead of dequant + GEMM;
+  * Q4_0 and Q8_0 prefill run the fused MFMA dequant-GEMM instead of
+    dequant + GEMM (the dequant route stays for shapes it does not serve);
   * per-column int8 weights (runtime/llama.py:162-165) go through
     gds_io_ext.int8_linear: a fused GEMV at decode, a bit-exact dequant and one
     GEMM at prefill, instead of an fp32 copy of the whole matrix per call.
-Q8_0 prefill keeps the reference's dequant -> F.linear route.
 
 The decode step's fused launches are exposed as the reference's own units:
 qkv_projections (the three dequant_linear calls of runtime/llama.py:212-214 in
@@ -46,8 +46,9 @@ def _fused_dequant_gemv(x: torch.Tensor, meta: dict) -> torch.Tensor:
     return out.unsqueeze(1)
 
 
-def _fused_dequant_gemm(x: torch.Tensor, meta: dict) -> torch.Tensor:
-    """Prefill Q4_0 projection on the MFMA dequant-GEMM: (B, S, K) -> (B, S, M)."""
+def _fused_dequant_gemm(x: torch.Tensor, meta: dict) -> Optional[torch.Tensor]:
+    """Prefill Q4_0 / Q8_0 projection on the MFMA dequant-GEMM: (B, S, K) ->
+    (B, S, M); None for a shape or alignment the kernels do not serve."""
     return ext().fused_dequant_gemm(meta["buffer"], x, meta["shape"], meta["gguf_type"], meta["offset"])
 
 
@@ -59,8 +60,9 @@ def dequant_linear(
     if isinstance(w, dict) and "gguf_type" in w:
         if x.shape[1] == 1 and x.shape[0] <= 8:
             return _fused_dequant_gemv(x, w)
-        if w["gguf_type"] == "q4_0" and w["shape"][1] % 64 == 0:
-            return _fused_dequant_gemm(x, w)
+        out = _fused_dequant_gemm(x, w)
+        if out is not None:
+            return out
         w = _dequant_gguf(w, scratch)
     elif w.dtype == torch.int8:
         # per-column int8: fused GEMV for up to 8 rows of x, else the bit-exact

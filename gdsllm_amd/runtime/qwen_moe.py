@@ -4,12 +4,15 @@ Mirrors runtime/qwen_moe.py:20-73 and :386-513 of the reference (same names,
 arguments and metadata dicts {"buffer", "shape", "quant_type",
 "weight_offset", "scale_offset", "bias_offset", "group_size"}).
 
-The decode MoE path changes shape, not contract: instead of syncing the
-selected expert ids to the host and running 3 GEMV launches per expert over
-per-expert buffers (runtime/qwen_moe.py:455-474), the stacked [E, N, K]
-expert tensors stay resident and one gather kernel pair reads the selected
-experts by index on the device (`moe_gather`).  The reference's per-expert
-route (expert_tensors from load_experts) is still accepted.
+The MoE path changes shape, not contract: instead of syncing the selected
+expert ids to the host and running 3 GEMV launches per expert over per-expert
+buffers (runtime/qwen_moe.py:455-474), the stacked [E, N, K] expert tensors
+stay resident; decode reads the selected experts by index on the device
+(`moe_gather`, `moe_step`), and a prefill chunk groups its tokens by expert on
+the device and runs one grouped MFMA GEMM per phase (`moe_prefill_affine_q4`,
+for the loop of runtime/qwen_moe.py:475-492).  The reference's per-expert
+route (expert_tensors from load_experts) is still accepted; its prefill
+projections run on the MFMA dequant-GEMM.
 """
 
 from __future__ import annotations
@@ -40,13 +43,32 @@ def _fused_affine_q4_gemv(x: torch.Tensor, meta: dict) -> torch.Tensor:
     return out.unsqueeze(1)
 
 
+def _fused_affine_q4_gemm(x: torch.Tensor, meta: dict) -> Optional[torch.Tensor]:
+    """Prefill affine-Q4 projection on the MFMA dequant-GEMM: (..., K) -> (..., M);
+    None for a shape, grouping or alignment the kernel does not serve."""
+    return ext().fused_affine_q4_gemm(
+        meta["buffer"], x, meta["shape"], meta["weight_offset"], meta["scale_offset"], meta["bias_offset"],
+        meta["group_size"],
+    )
+
+
+def _affine_linear(x: torch.Tensor, meta: dict, scratch: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """F.linear(x, dequant(meta)) for a prefill chunk: the fused GEMM, else the
+    reference's dequant -> F.linear (runtime/qwen_moe.py:72-73)."""
+    out = _fused_affine_q4_gemm(x, meta)
+    if out is not None:
+        return out
+    return F.linear(x, _dequant_affine_q4(meta, scratch))
+
+
 def affine_q4_linear(x: torch.Tensor, weights: Dict, name: str, scratch: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """runtime/qwen_moe.py:58-73: fused GEMV for decode, dequant + F.linear otherwise."""
+    """runtime/qwen_moe.py:58-73: fused GEMV for decode, the MFMA dequant-GEMM
+    (or dequant + F.linear) otherwise."""
     w = weights[f"{name}.weight"]
     if isinstance(w, dict) and w.get("quant_type") == "affine_q4":
         if x.shape[1] == 1 and x.shape[0] <= 8:
             return _fused_affine_q4_gemv(x, w)
-        w = _dequant_affine_q4(w, scratch)
+        return _affine_linear(x, w, scratch)
     return F.linear(x, w)
 
 
@@ -56,6 +78,8 @@ def _router_logits(x: torch.Tensor, weights: Dict, scratch: Optional[torch.Tenso
     router_w = weights["mlp.gate.weight"]
     if isinstance(router_w, dict):
         return affine_q4_linear(x, weights, "mlp.gate", scratch)
+    if x.numel() // x.shape[-1] > 8:
+        return F.linear(x, router_w)  # a prefill chunk: one library GEMM
     return ext().gemv_f16(router_w, x)
 
 
@@ -161,9 +185,17 @@ def moe_mlp_selective(
         fused = moe_step(x, weights, top_k_indices, top_k_weights)
         if fused is not None:
             return fused
+    expert_output = None
     if resident and n_tok == 1:
         expert_output = moe_gather(x, weights, top_k_indices, top_k_weights).view(1, hidden)
-    else:
+    elif resident:
+        # prefill over the resident pools: tokens grouped by expert on the
+        # device, one grouped MFMA GEMM per phase, no host sync
+        expert_output = ext().moe_prefill_affine_q4(
+            x_flat, [_entry(weights[f"{p}.weight"]) for p in _EXPERT_PROJ],
+            top_k_indices.reshape(n_tok, num_experts_per_token), top_k_weights.reshape(n_tok, num_experts_per_token),
+        )
+    if expert_output is None:
         def meta(proj: str, e: int) -> dict:
             if resident:
                 return _expert_meta(weights[f"mlp.switch_mlp.{proj}.weight"], e)
@@ -185,12 +217,9 @@ def moe_mlp_selective(
                     e = int(e_t.item())
                     mask = ids == e
                     xs = x_flat[mask]
-                    gw = _dequant_affine_q4(meta("gate_proj", e), scratch)
-                    gate = F.linear(xs, gw)
-                    uw = _dequant_affine_q4(meta("up_proj", e), scratch)
-                    up = F.linear(xs, uw)
-                    dw = _dequant_affine_q4(meta("down_proj", e), scratch)
-                    down = F.linear(F.silu(gate) * up, dw)
+                    gate = _affine_linear(xs, meta("gate_proj", e), scratch)
+                    up = _affine_linear(xs, meta("up_proj", e), scratch)
+                    down = _affine_linear(F.silu(gate) * up, meta("down_proj", e), scratch)
                     expert_output[mask] += ew[mask].unsqueeze(-1) * down
     expert_output = expert_output.view(batch, seq_len, hidden)
 

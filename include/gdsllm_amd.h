@@ -276,6 +276,56 @@ int gdsllm_dequant_gemm_q4_0(const void* weight, const void* x, void* y,
                              int64_t out_dim, int64_t in_dim, int64_t tokens,
                              int64_t ldx, int64_t ldy, void* stream);
 
+/* The same on Q8_0 weights.  Replaces dequant_gguf(..., "q8_0") -> F.linear
+ * (runtime/llama.py:160-166).  Needs in_dim % 256 == 0, 16-byte aligned
+ * weight and x rows (else GDSLLM_ERR_UNSUPPORTED: the caller keeps the
+ * dequant route).  W enters the matrix cores as the bit-exact dequantized
+ * fp16 value (runtime/gguf_dequant.cu:52-57).                               */
+int gdsllm_dequant_gemm_q8_0(const void* weight, const void* x, void* y,
+                             int64_t out_dim, int64_t in_dim, int64_t tokens,
+                             int64_t ldx, int64_t ldy, void* stream);
+
+/* The same on affine-Q4 weights (words [out_dim][in_dim/8], scales and biases
+ * [out_dim][in_dim/group_size]).  Replaces _dequant_affine_q4 -> F.linear
+ * (runtime/qwen_moe.py:69-73).  Needs in_dim % 256 == 0, group_size 32, 64
+ * or 128, 16-byte aligned words and x rows, scales/biases 4-byte aligned
+ * (16-byte for group_size 32), else GDSLLM_ERR_UNSUPPORTED.  Each weight is
+ * fp16(nib*scale + bias) rounded once; the reference rounds through fp32
+ * first (runtime/affine_q4_dequant.cu:50-58), which differs by one fp16 ulp
+ * of a weight only where nib*scale + bias is not exact in fp32.            */
+int gdsllm_dequant_gemm_affine_q4(const void* weight, const void* scales, const void* biases,
+                                  const void* x, void* y, int64_t out_dim, int64_t in_dim,
+                                  int64_t group_size, int64_t tokens, int64_t ldx, int64_t ldy,
+                                  void* stream);
+
+/* Bytes of device workspace gdsllm_moe_prefill_affine_q4 needs. */
+size_t gdsllm_moe_prefill_workspace_size(int64_t tokens, int64_t top_k, int64_t ffn_dim,
+                                         int64_t hidden, int64_t num_experts);
+
+/* Routed-expert MLP of a prefill chunk over stacked affine-Q4 experts
+ * (layout of gdsllm_moe_gather_affine_q4): the prefill branch of
+ * moe_mlp_selective (runtime/qwen_moe.py:475-492).  idx int32 [tokens][top_k]
+ * and routing_weights fp16 [tokens][top_k] on the device, x row t at
+ * x + t*ldx, expert_output row t at y + t*ldy (fp16 [hidden]):
+ *   y[t] = sum over j in order of fp16(w[t][j] * down_e(h)), each product and
+ *          partial sum rounded to fp16, e = idx[t][j],
+ *   h    = fp16(fp16(silu(fp16(gate_e . x_t))) * fp16(up_e . x_t)).
+ * Four launches and no host sync: the entries sorted by expert, one grouped
+ * MFMA GEMM for gate/up/SiLU over each expert's tokens, one for down, the
+ * combine.  Expert indices outside [0, num_experts) contribute nothing.  No
+ * counterpart kernel in the reference, which loops over the unique experts
+ * with dequant -> F.linear per projection.  Needs hidden and ffn multiples of
+ * 256, group_size 32, 64 or 128, gate and up with equal strides, at most 4096
+ * experts (else GDSLLM_ERR_UNSUPPORTED); workspace_bytes >=
+ * gdsllm_moe_prefill_workspace_size(tokens, top_k, ffn, hidden, experts).    */
+int gdsllm_moe_prefill_affine_q4(const gdsllm_affine_experts* gate,
+                                 const gdsllm_affine_experts* up,
+                                 const gdsllm_affine_experts* down,
+                                 const void* x, int64_t ldx, const int32_t* idx,
+                                 const void* routing_weights, int64_t tokens, int64_t top_k,
+                                 void* y, int64_t ldy, void* workspace, size_t workspace_bytes,
+                                 void* stream);
+
 /* ------------------------------------------------------ measurement helpers --
  * Not on the matvec path and with no counterpart in the reference: reference
  * kernels the benchmark measures the GEMV against on the same device.

@@ -200,6 +200,62 @@ def moe_gather(x, gate, up, down, idx, routing_weights):
     return acc, hs
 
 
+def moe_prefill(x, gate, up, down, idx, routing_weights):
+    """Prefill branch of moe_mlp_selective (runtime/qwen_moe.py:475-492).
+
+    x fp16 [T, H]; gate/up/down: callables e -> fp16 dequantized [out, in]
+    matrix of expert e (None for an index outside the pool, which then
+    contributes nothing); idx [T, k], routing_weights fp16 [T, k].  Follows the
+    reference loop: for each slot k, for each unique expert e of that slot,
+    the tokens routed to e get g = fp16(F.linear(x_sel, gate_e)),
+    u = fp16(F.linear(x_sel, up_e)), h = fp16(fp16(silu(g)) * u),
+    d = fp16(F.linear(h, down_e)), then expert_output[mask] =
+    fp16(expert_output[mask] + fp16(w * d)) (fp16 tensor ops: fp32 math, one
+    rounding each).  The products are float64 over the exact fp16 operands.
+    Returns (expert_output fp16 [T, H], {(t, j): (h, d)}).
+    """
+    x = np.asarray(x, dtype=np.float16)
+    idx = np.asarray(idx).reshape(x.shape[0], -1)
+    w = np.asarray(routing_weights, dtype=np.float16).reshape(idx.shape)
+    T, k = idx.shape
+    out = np.zeros(x.shape, dtype=np.float16)
+    inter = {}
+    for j in range(k):
+        ids = idx[:, j]
+        for e in np.unique(ids):
+            e = int(e)
+            wg, wu, wd = gate(e), up(e), down(e)
+            if wg is None:
+                continue
+            toks = np.nonzero(ids == e)[0]
+            xs = x[toks]
+            g = (xs.astype(np.float64) @ wg.astype(np.float64).T).astype(np.float16)
+            u = (xs.astype(np.float64) @ wu.astype(np.float64).T).astype(np.float16)
+            h = (silu_fp16(g).astype(np.float32) * u.astype(np.float32)).astype(np.float16)
+            d = (h.astype(np.float64) @ wd.astype(np.float64).T).astype(np.float16)
+            prod = (w[toks, j].astype(np.float32)[:, None] * d.astype(np.float32)).astype(np.float16)
+            out[toks] = (out[toks].astype(np.float32) + prod.astype(np.float32)).astype(np.float16)
+            for r, t in enumerate(toks):
+                inter[(int(t), j)] = (h[r], d[r])
+    return out, inter
+
+
+def moe_prefill_combine(d_rows, pos, routing_weights):
+    """The combine step of moe_prefill alone, from given per-entry down
+    outputs: out[t] = fold over j of fp16(out + fp16(w[t][j] * d_rows[pos[t][j]]))
+    starting from fp16 zeros, skipping pos < 0 (runtime/qwen_moe.py:490-492)."""
+    d_rows = np.asarray(d_rows, dtype=np.float16)
+    pos = np.asarray(pos).reshape(len(pos), -1) if np.asarray(pos).ndim == 2 else np.asarray(pos)
+    w = np.asarray(routing_weights, dtype=np.float16).reshape(pos.shape)
+    T, k = pos.shape
+    out = np.zeros((T, d_rows.shape[1]), dtype=np.float16)
+    for j in range(k):
+        ok = pos[:, j] >= 0
+        prod = (w[ok, j].astype(np.float32)[:, None] * d_rows[pos[ok, j]].astype(np.float32)).astype(np.float16)
+        out[ok] = (out[ok].astype(np.float32) + prod.astype(np.float32)).astype(np.float16)
+    return out
+
+
 def route_topk(logits, k: int):
     """moe_route (runtime/qwen_moe.py:408-412): torch.topk(logits, k) then
     F.softmax(top.float(), dim=-1).type_as(x), per row of fp16 logits [n, E].

@@ -130,6 +130,45 @@ def test_gemm_validation():
     assert g(None, None, None, 4, 64, 0, 64, 4, None) == 0
 
 
+def test_gemm_other_formats_validation():
+    q8 = capi().gdsllm_dequant_gemm_q8_0
+    assert q8(16, 16, 16, 4, 48, 2, 48, 4, None) == 1 and "multiple of 32" in _err()
+    assert q8(16, 16, 16, -4, 256, 2, 256, 4, None) == 1 and "negative" in _err()
+    assert q8(None, 16, 16, 4, 256, 2, 256, 4, None) == 1 and "null" in _err()
+    assert q8(16, 16, 16, 4, 96, 2, 96, 4, None) == 2 and "multiple of 256" in _err()
+    assert q8(16, 24, 16, 4, 256, 2, 256, 4, None) == 2 and "aligned" in _err()
+    assert q8(None, None, None, 4, 256, 0, 256, 4, None) == 0
+    a = capi().gdsllm_dequant_gemm_affine_q4
+    assert a(16, 16, 16, 16, 16, 4, 256, 12, 2, 256, 4, None) == 1 and "group_size" in _err()
+    assert a(16, 16, 16, 16, 16, 4, 256, 96, 2, 256, 4, None) == 1 and "group_size" in _err()
+    assert a(16, None, 16, 16, 16, 4, 256, 64, 2, 256, 4, None) == 1 and "null" in _err()
+    assert a(16, 16, 16, 16, 16, 4, 512, 256, 2, 512, 4, None) == 2 and "group_size" in _err()
+    assert a(16, 16, 16, 16, 16, 4, 192, 64, 2, 192, 4, None) == 2 and "multiple of 256" in _err()
+    assert a(16, 18, 16, 16, 16, 4, 256, 64, 2, 256, 4, None) == 2 and "aligned" in _err()
+    assert a(16, 20, 20, 16, 16, 4, 256, 32, 2, 256, 4, None) == 2 and "16-byte aligned" in _err()  # group 32
+
+
+def test_moe_prefill_validation():
+    lib = capi()
+    ws = lib.gdsllm_moe_prefill_workspace_size
+    assert ws(512, 10, 1024, 4096, 512) > 512 * 10 * (1024 + 4096) * 2
+    assert ws(-1, 10, 1024, 4096, 512) == 0
+    fn = lib.gdsllm_moe_prefill_affine_q4
+    gate, up, down = _experts(), _experts(), _experts(N=512, K=256)
+    need = ws(4, 2, 256, 512, 8)
+    args = lambda g, u, d, x=16, k=2, t=4, wsb=need: (ctypes.byref(g) if g else None, ctypes.byref(u), ctypes.byref(d),  # noqa: E731
+                                                      x, 512, 16, 16, t, k, 16, 512, 256, wsb, None)
+    assert fn(*args(None, up, down)) == 1 and "gate is null" in _err()
+    assert fn(*args(gate, up, _experts(N=512, K=512))) == 1 and "disagree" in _err()
+    assert fn(*args(gate, up, down, k=0)) == 1 and "top_k" in _err()
+    assert fn(*args(gate, up, down, t=0)) == 0  # nothing to compute
+    assert fn(*args(gate, up, down, x=None)) == 1 and "null" in _err()
+    assert fn(*args(gate, up, down, wsb=need - 1)) == 1 and "workspace" in _err()
+    assert fn(*args(gate, up, _experts(N=512, K=256, g=256))) == 1  # down grouping differs
+    odd = _experts(N=192, K=512)
+    assert fn(*args(odd, _experts(N=192, K=512), _experts(N=512, K=192, g=64))) == 2 and "multiples of 256" in _err()
+
+
 def _experts(w=16, s=16, b=16, E=8, N=256, K=512, g=64, ws=None):
     return AffineExperts(w, s, b, ws if ws is not None else N * K // 2, N * K // g * 2, N * K // g * 2, E, N, K, g)
 

@@ -1,0 +1,332 @@
+"""Parity of the MFMA prefill dequant-GEMM for Q8_0 and affine-Q4 weights (the
+Q4_0 cases live in test_gpu_moe_gemm.py), tile-width invariance, and the
+grouped-expert MoE prefill, against the oracle, through the C ABI.
+
+The dense GEMMs replace the reference's prefill route dequant -> F.linear
+(runtime/llama.py:160-166, runtime/qwen_moe.py:69-73); the MoE prefill
+replaces the per-expert loop of runtime/qwen_moe.py:475-492.
+"""
+
+import ctypes
+import functools
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import (affine_dequant_np, assert_gemv_close, capi, check, experts_struct, gen, oq, ptr, stream, syn,
+                     to_np)
+
+pytestmark = pytest.mark.gpu
+
+# (T, M, K): one stage pair, ragged token and row tiles, LLaMA-7B layer shapes
+# at a 512-token chunk (the Q8_0 layer of the benchmark's Q8_0 model)
+Q8_CASES = [(1, 128, 256), (7, 300, 256), (64, 128, 4096), (100, 260, 1024), (33, 11008, 4096),
+            (512, 4096, 4096), (512, 11008, 4096), (512, 4096, 11008)]
+
+
+@pytest.mark.parametrize("T,M,K", Q8_CASES, ids=[f"T{t}_{m}x{k}" for t, m, k in Q8_CASES])
+def test_dequant_gemm_q8_0(gpu, T, M, K):
+    w = syn.q8_0_weights(M, K, gen(5200 + M + K))
+    x = syn.activations(T, K, gen(5201 + T))
+    deq = oq.dequant_q8_0(to_np(w)).reshape(M, K)
+    wd, xd = w.to(gpu), x.to(gpu)
+    y = torch.empty(T, M, dtype=torch.float16, device=gpu)
+    check(capi().gdsllm_dequant_gemm_q8_0(ptr(wd), ptr(xd), ptr(y), M, K, T, K, M, stream()))
+    torch.cuda.synchronize()
+    rel, mx = assert_gemv_close(to_np(y), deq, to_np(x), f"q8_0 gemm T{T} {M}x{K}")
+    print(f"q8_0 gemm T{T} {M}x{K}: rel={rel:.2e} max={mx:.2e}")
+
+
+AFF_CASES = [(5, 200, 256, 64), (64, 1024, 4096, 64), (512, 4096, 1024, 64), (100, 260, 2048, 128),
+             (70, 384, 512, 32), (512, 1024, 4096, 128), (33, 512, 1024, 32)]
+
+
+@pytest.mark.parametrize("T,M,K,g", AFF_CASES, ids=[f"T{t}_{m}x{k}_g{g}" for t, m, k, g in AFF_CASES])
+def test_dequant_gemm_affine_q4(gpu, T, M, K, g):
+    words, scales, biases = syn.affine_q4_weights([M, K], g, gen(5300 + M + g))
+    x = syn.activations(T, K, gen(5301 + T))
+    deq = affine_dequant_np(words, scales, biases, g).reshape(M, K)
+    wd, sd, bd, xd = words.to(gpu), scales.to(gpu), biases.to(gpu), x.to(gpu)
+    y = torch.empty(T, M, dtype=torch.float16, device=gpu)
+    check(capi().gdsllm_dequant_gemm_affine_q4(ptr(wd), ptr(sd), ptr(bd), ptr(xd), ptr(y), M, K, g, T, K, M, stream()))
+    torch.cuda.synchronize()
+    rel, mx = assert_gemv_close(to_np(y), deq, to_np(x), f"affine gemm T{T} {M}x{K} g{g}")
+    print(f"affine gemm T{T} {M}x{K} g{g}: rel={rel:.2e} max={mx:.2e}")
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+def test_dequant_gemm_tile_width_keeps_bits(gpu, fmt):
+    """11008 rows at 512 tokens take the 128-token tile, 64 tokens the 64-token
+    tile: the same MFMA sequence per output, so the shared rows are equal bit
+    for bit (and within the GEMV tolerance of the oracle)."""
+    M, K = 11008, 4096
+    w = (syn.q4_0_weights if fmt == "q4_0" else syn.q8_0_weights)(M, K, gen(5400))
+    x = syn.activations(512, K, gen(5401))
+    wd, xd = w.to(gpu), x.to(gpu)
+    fn = capi().gdsllm_dequant_gemm_q4_0 if fmt == "q4_0" else capi().gdsllm_dequant_gemm_q8_0
+    y = torch.empty(512, M, dtype=torch.float16, device=gpu)
+    y64 = torch.empty(64, M, dtype=torch.float16, device=gpu)
+    check(fn(ptr(wd), ptr(xd), ptr(y), M, K, 512, K, M, stream()))
+    check(fn(ptr(wd), ptr(xd), ptr(y64), M, K, 64, K, M, stream()))
+    torch.cuda.synchronize()
+    assert torch.equal(y[:64].view(torch.int16), y64.view(torch.int16)), "tile width changed the result"
+    deq = (oq.dequant_q4_0 if fmt == "q4_0" else oq.dequant_q8_0)(to_np(w)).reshape(M, K)
+    assert_gemv_close(to_np(y)[448:], deq, to_np(x)[448:], f"{fmt} gemm last token tile")
+
+
+@pytest.mark.parametrize("fmt", ["q8_0", "affine"])
+def test_dequant_gemm_strided(gpu, fmt):
+    """x and y rows with leading dimensions wider than the rows; columns past
+    the rows are left alone."""
+    T, M, K, ldx, ldy, g = 70, 390, 512, 520, 397, 64
+    xfull = syn.activations(T, ldx, gen(5500))
+    x = xfull[:, :K]
+    xd = xfull.to(gpu)
+    y = torch.full((T, ldy), 7.0, dtype=torch.float16, device=gpu)
+    if fmt == "q8_0":
+        w = syn.q8_0_weights(M, K, gen(5501))
+        deq = oq.dequant_q8_0(to_np(w)).reshape(M, K)
+        wd = w.to(gpu)
+        check(capi().gdsllm_dequant_gemm_q8_0(ptr(wd), ptr(xd), ptr(y), M, K, T, ldx, ldy, stream()))
+    else:
+        words, scales, biases = syn.affine_q4_weights([M, K], g, gen(5502))
+        deq = affine_dequant_np(words, scales, biases, g).reshape(M, K)
+        wd, sd, bd = words.to(gpu), scales.to(gpu), biases.to(gpu)
+        check(capi().gdsllm_dequant_gemm_affine_q4(ptr(wd), ptr(sd), ptr(bd), ptr(xd), ptr(y), M, K, g, T, ldx, ldy,
+                                                   stream()))
+    torch.cuda.synchronize()
+    yh = to_np(y)
+    assert_gemv_close(yh[:, :M].copy(), deq, to_np(x).copy(), f"{fmt} gemm strided")
+    assert (yh[:, M:] == 7.0).all(), "padding columns of y were written"
+
+
+def test_dequant_gemm_unsupported_shapes(gpu):
+    """Shapes off the MFMA kernels' grid are refused as unsupported (the caller
+    keeps the dequant route), before any launch."""
+    y = torch.empty(64, dtype=torch.float16, device=gpu)
+    assert capi().gdsllm_dequant_gemm_q8_0(ptr(y), ptr(y), ptr(y), 4, 96, 2, 96, 4, stream()) == 2
+    assert b"multiple of 256" in capi().gdsllm_last_error()
+    assert capi().gdsllm_dequant_gemm_affine_q4(ptr(y), ptr(y), ptr(y), ptr(y), ptr(y), 4, 256, 256, 2, 256, 4,
+                                                stream()) == 2
+    assert b"group_size" in capi().gdsllm_last_error()
+
+
+# ------------------------------------------------------------ MoE prefill --
+
+
+def _prefill_layout(T, k, F, H, E):
+    """Byte offsets of the library's MoE-prefill workspace regions (tok, pos,
+    tiles, ntiles, h, d), 256-byte aligned, in the order the library lays them out."""
+    up = lambda v: (v + 255) & ~255  # noqa: E731
+    n = T * k
+    max_tiles = n // 32 + min(E, n) + 1
+    o, out = 0, {}
+    for name, size in (("tok", 4 * n), ("pos", 4 * n), ("tiles", 16 * max_tiles), ("ntiles", 16), ("h", 2 * n * F),
+                       ("d", 2 * n * H)):
+        out[name] = o
+        o = up(o + size)
+    out["total"] = o
+    return out
+
+
+def _moe_prefill(gate, up, down, xd, idx_d, w_d, g, T, k):
+    gs, us, ds = (experts_struct(*p, g) for p in (gate, up, down))
+    E, F, H = gs.num_experts, gs.out_dim, gs.in_dim
+    ws_bytes = capi().gdsllm_moe_prefill_workspace_size(T, k, F, H, E)
+    L = _prefill_layout(T, k, F, H, E)
+    assert ws_bytes == L["total"]
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=xd.device)
+    y = torch.full((T, H), 3.0, dtype=torch.float16, device=xd.device)
+    check(capi().gdsllm_moe_prefill_affine_q4(ctypes.byref(gs), ctypes.byref(us), ctypes.byref(ds), ptr(xd), H,
+                                              ptr(idx_d), ptr(w_d), T, k, ptr(y), H, ptr(ws), ws_bytes, stream()))
+    torch.cuda.synchronize()
+    n = T * k
+    part = lambda name, dt, count: ws[L[name]:L[name] + count * dt.itemsize].view(dt)  # noqa: E731
+    tok = to_np(part("tok", torch.int32, n))
+    pos = to_np(part("pos", torch.int32, n)).reshape(T, k)
+    ntiles = int(to_np(part("ntiles", torch.int32, 1))[0])
+    tiles = to_np(part("tiles", torch.int32, 4 * ntiles)).reshape(ntiles, 4)
+    hbuf = to_np(part("h", torch.float16, n * F)).reshape(n, F)
+    dbuf = to_np(part("d", torch.float16, n * H)).reshape(n, H)
+    return y, tok, pos, tiles, hbuf, dbuf
+
+
+def _check_sort(idx, tok, pos, tiles, E, BT=32):
+    """Every in-range entry (t, j) has a position p with tok[p] == t; positions
+    are a permutation of 0 .. n_valid-1; the tiles cover each expert's positions
+    in runs of at most BT."""
+    T, k = idx.shape
+    valid = (idx >= 0) & (idx < E)
+    assert (pos[~valid] == -1).all()
+    pv = pos[valid]
+    assert sorted(pv.tolist()) == list(range(int(valid.sum())))
+    for t, j in zip(*np.nonzero(valid)):
+        assert tok[pos[t, j]] == t
+    owner = np.full(int(valid.sum()), -1)
+    owner[pv] = idx[valid]
+    covered = np.zeros(len(owner), bool)
+    for e, p0, cnt, _ in tiles:
+        assert 1 <= cnt <= BT and (owner[p0:p0 + cnt] == e).all()
+        assert not covered[p0:p0 + cnt].any()
+        covered[p0:p0 + cnt] = True
+    assert covered.all()
+
+
+def _dq_fn(pool, g):
+    @functools.lru_cache(maxsize=None)
+    def f(e):
+        if e < 0 or e >= pool[0].shape[0]:
+            return None
+        w, s, b = (t[e].cpu() for t in pool)
+        return affine_dequant_np(w, s, b, g).reshape(w.shape[0], -1)
+    return lambda e: f(int(e))
+
+
+def _check_moe_prefill(y, tok, pos, hbuf, dbuf, gate, up, down, x, idx, wts, g, E, sample=None):
+    T, k = idx.shape
+    gf, uf, dn = _dq_fn(gate, g), _dq_fn(up, g), _dq_fn(down, g)
+    toks = range(T) if sample is None else sample
+    xn = to_np(x)
+    # (1) phase 2: each down row against the oracle product of the kernel's own h
+    for t in toks:
+        for j in range(k):
+            e = int(idx[t, j])
+            if gf(e) is None:
+                continue
+            p = pos[t, j]
+            assert_gemv_close(dbuf[p][None, :], dn(e), hbuf[p][None, :], f"down t{t} j{j}")
+    # (2) the combine, replayed from the kernel's down rows: bit for bit
+    want = oq.moe_prefill_combine(dbuf, pos, wts)
+    assert np.array_equal(to_np(y).view(np.uint16), want.view(np.uint16)), "combine differs from the fp16 fold"
+    # (3) h and end to end against the all-oracle prefill on the sampled tokens
+    sel = np.asarray(list(toks))
+    ref, inter = oq.moe_prefill(xn[sel], gf, uf, dn, idx[sel], wts[sel])
+    hk = np.stack([hbuf[pos[t, j]] for t in sel for j in range(k) if gf(int(idx[t, j])) is not None]).astype(np.float64)
+    hr = np.stack([inter[(r, j)][0] for r in range(len(sel)) for j in range(k) if (r, j) in inter]).astype(np.float64)
+    relh = float(np.linalg.norm(hk - hr) / np.linalg.norm(hr))
+    got = to_np(y)[sel].astype(np.float64)
+    rel = float(np.linalg.norm(got - ref.astype(np.float64)) / np.linalg.norm(ref.astype(np.float64)))
+    print(f"moe prefill: h rel L2 {relh:.2e}, expert_output rel L2 {rel:.2e}")
+    assert relh <= oq.GEMV_REL_L2, f"h rel L2 {relh:.3e}"
+    assert np.isfinite(got).all() and rel <= oq.GEMV_REL_L2, f"expert_output rel L2 {rel:.3e}"
+
+
+PREFILL_CASES = [(16, 1024, 512, 64, 4, 37), (64, 2048, 1024, 64, 10, 100), (8, 512, 256, 32, 3, 9),
+                 (32, 1024, 256, 128, 8, 65), (4, 1024, 512, 64, 2, 300)]
+
+
+@pytest.mark.parametrize("E,H,F,g,k,T", PREFILL_CASES, ids=[f"E{e}_H{h}_F{f}_g{g}_k{k}_T{t}" for e, h, f, g, k, t in PREFILL_CASES])
+def test_moe_prefill(gpu, E, H, F, g, k, T):
+    gg = gen(5600 + E + T)
+    gate = syn.affine_q4_weights([E, F, H], g, gg)
+    up = syn.affine_q4_weights([E, F, H], g, gg)
+    down = syn.affine_q4_weights([E, H, F], g, gg)
+    x = syn.activations(T, H, gen(5601 + T))
+    idx = np.stack([np.random.default_rng(5602 + t).choice(E, k, replace=False) for t in range(T)]).astype(np.int32)
+    wts = torch.softmax(torch.randn(T, k, generator=gen(5603)), -1).to(torch.float16)
+    dev = [tuple(t.to(gpu) for t in p) for p in (gate, up, down)]
+    y, tok, pos, tiles, hbuf, dbuf = _moe_prefill(*dev, x.to(gpu), torch.from_numpy(idx).to(gpu), wts.to(gpu), g, T, k)
+    _check_sort(idx, tok, pos, tiles, E)
+    _check_moe_prefill(y, tok, pos, hbuf, dbuf, gate, up, down, x, idx, to_np(wts), g, E)
+    # a second run gives the same bits (positions inside an expert may differ)
+    y2 = _moe_prefill(*dev, x.to(gpu), torch.from_numpy(idx).to(gpu), wts.to(gpu), g, T, k)[0]
+    assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
+
+
+def test_moe_prefill_out_of_range_experts(gpu):
+    E, H, F, g, k, T = 6, 512, 256, 64, 3, 11
+    gg = gen(5700)
+    pools = [syn.affine_q4_weights(s, g, gg) for s in ([E, F, H], [E, F, H], [E, H, F])]
+    x = syn.activations(T, H, gen(5701))
+    idx = np.stack([np.random.default_rng(5702 + t).choice(E, k, replace=False) for t in range(T)]).astype(np.int32)
+    idx[0, 1], idx[3, 0], idx[7, 2] = -1, E, 1 << 20
+    wts = torch.softmax(torch.randn(T, k, generator=gen(5703)), -1).to(torch.float16)
+    dev = [tuple(t.to(gpu) for t in p) for p in pools]
+    y, tok, pos, tiles, hbuf, dbuf = _moe_prefill(*dev, x.to(gpu), torch.from_numpy(idx).to(gpu), wts.to(gpu), g, T, k)
+    _check_sort(idx, tok, pos, tiles, E)
+    _check_moe_prefill(y, tok, pos, hbuf, dbuf, *pools, x, idx, to_np(wts), g, E)
+
+
+def test_moe_prefill_cfg2_pool_512_tokens(gpu):
+    """The 512-expert pool of the MoE configuration (3.6 GB, generated on the
+    device) with a 512-token chunk at top-10: the sort and the combine are
+    checked for every token, the GEMMs and the end result on 8 sampled tokens
+    (the oracle only dequantizes the experts those tokens pick)."""
+    E, H, F, g, k, T = 512, 4096, 1024, 64, 10, 512
+    gd = torch.Generator(device=gpu).manual_seed(5800)
+    dev = [syn.affine_q4_weights(s, g, gd) for s in ([E, F, H], [E, F, H], [E, H, F])]
+    x = syn.activations(T, H, gen(5801))
+    idx = np.stack([np.random.default_rng(5802 + t).choice(E, k, replace=False) for t in range(T)]).astype(np.int32)
+    wts = torch.softmax(torch.randn(T, k, generator=gen(5803)), -1).to(torch.float16)
+    y, tok, pos, tiles, hbuf, dbuf = _moe_prefill(*dev, x.to(gpu), torch.from_numpy(idx).to(gpu), wts.to(gpu), g, T, k)
+    _check_sort(idx, tok, pos, tiles, E)
+    sample = sorted(np.random.default_rng(5804).choice(T, 8, replace=False).tolist())
+
+    class Lazy:
+        """pool[e] on the CPU, only for the experts the sample touches"""
+        def __init__(self, t):
+            self.t, self.shape = t, t.shape
+
+        def __getitem__(self, e):
+            return self.t[e].cpu()
+
+    pools = [tuple(Lazy(t) for t in p) for p in dev]
+    _check_moe_prefill(y, tok, pos, hbuf, dbuf, *pools, x, idx, to_np(wts), g, E, sample=sample)
+    del dev
+    torch.cuda.empty_cache()
+
+
+def test_runtime_moe_prefill_matches_per_expert_route(gpu, tmp_path):
+    """moe_mlp_selective on a prefill chunk: the resident stacked experts (one
+    grouped GEMM per phase) and the reference's per-expert buffers from
+    load_experts (the MFMA GEMM per projection) against the oracle."""
+    from gdsllm_amd.runtime import qwen_moe as qm
+    from gdsllm_amd.runtime.torch_bridge import ModelWeights
+    from gdsllm_amd.synthetic_model import write_moe_layer
+
+    E, H, F, g, k, T = 8, 2048, 512, 64, 4, 40
+    d = str(tmp_path / "moe")
+    raw = write_moe_layer(d, experts=E, hidden=H, ffn=F, group=g, seed=5900)
+    mw = ModelWeights(d)
+    part, _h = mw.load_layer_partial(0)
+    full, _hf = mw.load_layer(0)
+    x = syn.activations(T, H, gen(5901))
+    xd = x.to(gpu).view(1, T, H)
+    idx = np.stack([np.random.default_rng(5902 + t).choice(E, k, replace=False) for t in range(T)]).astype(np.int64)
+    wts = torch.softmax(torch.randn(T, k, generator=gen(5903)), -1).to(torch.float16)
+    it, wt = torch.from_numpy(idx).to(gpu).view(1, T, k), wts.to(gpu).view(1, T, k)
+    y_res = qm.moe_mlp_selective(xd, full, None, it, wt, k)
+    experts, _eh = mw.load_experts(0, sorted(set(idx.reshape(-1).tolist())))
+    y_exp = qm.moe_mlp_selective(xd, part, experts, it, wt, k)
+    torch.cuda.synchronize()
+
+    def fn(proj):
+        def f(e):
+            w, s, b = (t[e] for t in raw[f"mlp.switch_mlp.{proj}"])
+            return affine_dequant_np(w, s, b, g).reshape(w.shape[0], -1)
+        return f
+
+    ref, _ = oq.moe_prefill(to_np(x), fn("gate_proj"), fn("up_proj"), fn("down_proj"), idx, to_np(wts))
+    ref = np.clip(ref, np.float16(-65504), np.float16(65504)).astype(np.float64)
+    for name, y in (("resident", y_res), ("per-expert", y_exp)):
+        got = to_np(y).reshape(T, H).astype(np.float64)
+        rel = float(np.linalg.norm(got - ref) / np.linalg.norm(ref))
+        print(f"runtime moe prefill {name}: rel L2 {rel:.2e}")
+        assert np.isfinite(got).all() and rel <= oq.GEMV_REL_L2, f"{name}: rel L2 {rel:.3e}"
+
+
+def test_runtime_q8_0_prefill_projection(gpu):
+    """dequant_linear on a Q8_0 weight with a prefill chunk takes the MFMA GEMM."""
+    from gdsllm_amd.runtime import ext
+    from gdsllm_amd.runtime import llama
+
+    M, K, T = 1024, 4096, 48
+    w = syn.q8_0_weights(M, K, gen(6000))
+    handle = ext().GdsBufferHandle.from_tensor(w.reshape(-1).to(gpu))
+    meta = {"buffer": handle, "shape": [M, K], "gguf_type": "q8_0", "offset": 0}
+    x = syn.activations(T, K, gen(6001))
+    y = llama.dequant_linear(x.to(gpu).view(2, T // 2, K), {"p.weight": meta}, "p")
+    torch.cuda.synchronize()
+    assert y.shape == (2, T // 2, M)
+    assert_gemv_close(to_np(y).reshape(T, M), oq.dequant_q8_0(to_np(w)).reshape(M, K), to_np(x), "q8_0 dequant_linear")

@@ -353,6 +353,56 @@ def test_moe_gather_composition():
     assert np.allclose(yc, ya, rtol=0, atol=0)
 
 
+def test_moe_prefill_matches_token_by_token_loop():
+    """The prefill oracle groups tokens by expert per slot; an independent loop
+    over tokens (one token at a time, slots in order, the same fp16 steps
+    written out by hand with Fraction-free float64 products) must give the same
+    bits, and one token with one slot of weight 1 equals the decode oracle's h
+    and down product rounded to fp16."""
+    rng = np.random.default_rng(11)
+    H, F, E, T, k = 64, 32, 5, 9, 3
+    mats = {e: [rng.normal(0, 0.1, size=s).astype(np.float16) for s in ((F, H), (F, H), (H, F))] for e in range(E)}
+    gate = lambda e: mats[e][0] if e in mats else None  # noqa: E731
+    up = lambda e: mats[e][1] if e in mats else None  # noqa: E731
+    down = lambda e: mats[e][2] if e in mats else None  # noqa: E731
+    x = rng.normal(size=(T, H)).astype(np.float16)
+    idx = np.stack([rng.choice(E, k, replace=False) for _ in range(T)])
+    idx[2, 1] = -1   # an index outside the pool contributes nothing
+    idx[5, 0] = E
+    w = (rng.random((T, k)) / k).astype(np.float16)
+    out, inter = oq.moe_prefill(x, gate, up, down, idx, w)
+    for t in range(T):
+        acc = np.float16(0)
+        for j in range(k):
+            e = int(idx[t, j])
+            if e not in mats:
+                assert (t, j) not in inter
+                continue
+            xt = x[t].astype(np.float64)
+            g = (mats[e][0].astype(np.float64) @ xt).astype(np.float16)
+            u = (mats[e][1].astype(np.float64) @ xt).astype(np.float16)
+            gf = g.astype(np.float32)
+            h = ((gf / (np.float32(1) + np.exp(-gf))).astype(np.float16).astype(np.float32) * u.astype(np.float32)).astype(np.float16)
+            d = (mats[e][2].astype(np.float64) @ h.astype(np.float64)).astype(np.float16)
+            assert np.array_equal(inter[(t, j)][0], h) and np.array_equal(inter[(t, j)][1], d)
+            acc = (np.float32(acc) + (np.float32(w[t, j]) * d.astype(np.float32)).astype(np.float16).astype(np.float32)).astype(np.float16)
+        assert np.array_equal(out[t].view(np.uint16), np.asarray(acc, dtype=np.float16).view(np.uint16)), t
+    # one slot, weight 1: the decode oracle's float64 sum rounds to the same value
+    y1, hs = oq.moe_gather(x[0], gate, up, down, idx[0, :1], [1.0])
+    o1, _ = oq.moe_prefill(x[:1], gate, up, down, idx[:1, :1], np.ones((1, 1), np.float16))
+    assert np.array_equal(o1[0], y1.astype(np.float16))
+    # the combine alone, replayed from the intermediates and positions
+    pos = np.full((T, k), -1)
+    rows = []
+    for (t, j), (_h, d) in sorted(inter.items()):
+        pos[t, j] = len(rows)
+        rows.append(d)
+    assert np.array_equal(oq.moe_prefill_combine(np.stack(rows), pos, w).view(np.uint16), out.view(np.uint16))
+    # a planted mistake (slots summed in reverse order) changes some bits
+    rev = oq.moe_prefill_combine(np.stack(rows), pos[:, ::-1].copy(), w[:, ::-1].copy())
+    assert not np.array_equal(rev.view(np.uint16), out.view(np.uint16))
+
+
 def test_affine_double_rounding_follows_reference():
     """Cases where rounding nib*s+b straight to fp16 differs from the reference's
     fp32-then-fp16 exist; the oracle gives the reference's value (checked with

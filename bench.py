@@ -218,14 +218,27 @@ def bench_decode_sweep(args, dev):
     return ms_fused, ms_unfused, (layers, lm_head)
 
 
+_EAGER = False  # --profile-case: launch eagerly instead of replaying graphs
+
+
 def _replay_ms(capture, reps: int, warm: int = 3) -> float:
     """Captures `capture()` (launches on the current stream) into a HIP graph
     once, replays it `warm` times untimed, then `reps` times between HIP
-    events on the launch stream; returns ms per replay."""
+    events on the launch stream; returns ms per replay.  With _EAGER set,
+    `capture()` itself runs once untimed and `reps` times timed, so a profiler
+    sees plain kernel dispatches."""
     import torch
 
     capture()
     torch.cuda.synchronize()
+    if _EAGER:
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            capture()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / reps
     graph = _capture(capture)
     for _ in range(warm):
         graph.replay()
@@ -639,7 +652,7 @@ def bench_prefill_formats(dev, tokens: int = 512, reps: int = 20):
     return out
 
 
-def bench_moe_prefill(dev, tokens: int = 512, reps: int = 5):
+def bench_moe_prefill(dev, tokens: int = 512, reps: int = 5, reference: bool = True):
     """Routed-expert MLP of a 512-token prefill chunk over the resident
     512-expert affine-Q4 pool (hidden 4096, ffn 1024, group 64, top-10, random
     distinct picks per token): the grouped MFMA path (4 launches, no host
@@ -685,6 +698,11 @@ def bench_moe_prefill(dev, tokens: int = 512, reps: int = 5):
     per_expert = 3 * (Fd * H // 2 + 2 * 2 * Fd * H // g)
     wbytes = len(used) * per_expert
     flops = 2 * tokens * k * 3 * Fd * H
+    res = {"us_per_chunk": round(ms * 1e3, 1), "tokens": tokens, "top_k": k, "experts_used": len(used),
+           "weight_bytes": wbytes, "weight_GB_s": round(wbytes / (ms * 1e-3) / 1e9, 1),
+           "TFLOP_s": round(flops / (ms * 1e-3) / 1e12, 1), "launches": 4, "host_syncs": 0}
+    if not reference:
+        return res
 
     # the reference's route, eagerly (it syncs to the host for every expert id)
     gd = torch.empty(Fd, H, dtype=torch.float16, device=dev)
@@ -719,11 +737,9 @@ def bench_moe_prefill(dev, tokens: int = 512, reps: int = 5):
     torch.cuda.synchronize()
     ref_ms = (time.perf_counter() - t0) * 1e3
     rel = float(torch.linalg.vector_norm((y.float() - ref.float())) / torch.linalg.vector_norm(ref.float()))
-    return {"us_per_chunk": round(ms * 1e3, 1), "tokens": tokens, "top_k": k, "experts_used": len(used),
-            "weight_bytes": wbytes, "weight_GB_s": round(wbytes / (ms * 1e-3) / 1e9, 1),
-            "TFLOP_s": round(flops / (ms * 1e-3) / 1e12, 1), "launches": 4, "host_syncs": 0,
-            "reference_route_ms": round(ref_ms, 2), "speedup_vs_reference_route": round(ref_ms / ms, 1),
-            "rel_l2_vs_reference_route": rel}
+    res.update({"reference_route_ms": round(ref_ms, 2), "speedup_vs_reference_route": round(ref_ms / ms, 1),
+                "rel_l2_vs_reference_route": rel})
+    return res
 
 
 def bench_load(dev, layers: int = 2, reps: int = 3, tokens: int = 512, emb_reps: int = 20):
@@ -864,25 +880,46 @@ def cpu_baseline(weights_dev, x_dev, y_gpu, seconds: float):
 
 def profile_case(case: str, reps: int, dev) -> int:
     """One workload launched `reps` times eagerly (no graph), for a profiler's
-    kernel trace or counters; prints one JSON line and returns 0."""
+    kernel trace or counters; prints one JSON line and returns 0.
+      gemm:M,K,T / gemm_q8:M,K,T / gemm_aff:M,K,T   Q4_0 / Q8_0 / affine-Q4 g64
+                                                    prefill dequant-GEMM
+      gemv:M,K,B                                    Q4_0 fused GEMV
+      moe                                           top-10 gather, `reps` calls
+      moe_step                                      the decode MoE step, 8-launch
+                                                    and 4-launch forms, `reps` calls each
+      moe_prefill                                   grouped MoE prefill, 512 tokens"""
     import torch
 
     from gdsllm_amd import capi, check
     from gdsllm_amd import synthetic as syn
 
+    global _EAGER
+    _EAGER = True
     kind, _, spec = case.partition(":")
     st = torch.cuda.current_stream().cuda_stream
     gen = torch.Generator(device=dev).manual_seed(1020)
-    if kind in ("gemm", "gemv"):
+    lib = capi()
+    if kind in ("gemm", "gemv", "gemm_q8", "gemm_aff"):
         m, k, t = (int(v) for v in spec.split(","))
-        w = syn.q4_0_weights(m, k, gen)
         x = syn.activations(t, k, gen)
         y = torch.empty(t, m, dtype=torch.float16, device=dev)
-        fn = capi().gdsllm_dequant_gemm_q4_0 if kind == "gemm" else capi().gdsllm_fused_q4_0_gemv
-        launch = lambda: check(fn(w.data_ptr(), x.data_ptr(), y.data_ptr(), m, k, t, k, m, st))  # noqa: E731
-    elif kind == "moe":
-        res = bench_moe(dev, calls=reps, reps=1, decode_step=False)
-        print(json.dumps({"profile_case": case, "calls": reps, "us_per_call": res["us_per_call"]}), flush=True)
+        if kind == "gemm_aff":
+            aw, asc, ab = syn.affine_q4_weights([m, k], 64, gen)
+            launch = lambda: check(lib.gdsllm_dequant_gemm_affine_q4(  # noqa: E731
+                aw.data_ptr(), asc.data_ptr(), ab.data_ptr(), x.data_ptr(), y.data_ptr(), m, k, 64, t, k, m, st))
+        else:
+            w = syn.q8_0_weights(m, k, gen) if kind == "gemm_q8" else syn.q4_0_weights(m, k, gen)
+            fn = {"gemm": lib.gdsllm_dequant_gemm_q4_0, "gemm_q8": lib.gdsllm_dequant_gemm_q8_0,
+                  "gemv": lib.gdsllm_fused_q4_0_gemv}[kind]
+            launch = lambda: check(fn(w.data_ptr(), x.data_ptr(), y.data_ptr(), m, k, t, k, m, st))  # noqa: E731
+    elif kind in ("moe", "moe_step"):
+        res = bench_moe(dev, calls=reps, reps=1, decode_step=kind == "moe_step")
+        res = res.get("decode_step", res)
+        print(json.dumps({"profile_case": case, "calls": reps, "result": res}), flush=True)
+        return 0
+    elif kind == "moe_prefill":
+        res = bench_moe_prefill(dev, reps=reps, reference=False)
+        print(json.dumps({"profile_case": case, "chunks": reps, "result": res}), flush=True)
         return 0
     else:
         print(f"bench.py: unknown --profile-case {case!r}", file=sys.stderr)

@@ -176,14 +176,19 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
-// One fp16 row dot x (both 16-byte aligned, K % 8 == 0) by one wave, summed
-// in the order of gemv_f16's vector path: lane l takes 8 weights of every
-// 512-column chunk, chunks in order, v_dot2 into fp32, then a wave sum.  The
-// same inputs give the same bits as gdsllm_gemv_f16.
-__device__ __forceinline__ float f16_row_dot(const uint16_t* __restrict__ w, const uint16_t* __restrict__ x, int K,
-                                             int lane) {
+// Row dot products of fp16 weights (gemv_f16 and everything that must give
+// its bits) in one fixed order: the row's 512-column chunks are dealt to four
+// parts, chunk c to part c % 4; within a part lane l takes 8 weights of each
+// of its chunks, in chunk order, with v_dot2 into fp32, then the part is
+// summed over the wave (group_sum<64>); the row is ((p0 + p1) + p2) + p3.
+// gemv_f16 runs the four parts on four waves of a workgroup.
+
+// This lane's sum over the chunks of part `part` of row w (K % 8 == 0, w and
+// x 16-byte aligned).
+__device__ __forceinline__ float f16_part_lane(const uint16_t* __restrict__ w, const uint16_t* __restrict__ x, int K,
+                                               int part, int lane) {
     float acc = 0.f;
-    for (int c = 8 * lane; c < K; c += 512) {
+    for (int c = 8 * lane + 512 * part; c < K; c += 2048) {
         const uint4 wv = *reinterpret_cast<const uint4*>(w + c);
         const uint4 xv = *reinterpret_cast<const uint4*>(x + c);
         acc = dot2(wv.x, xv.x, acc);
@@ -191,7 +196,17 @@ __device__ __forceinline__ float f16_row_dot(const uint16_t* __restrict__ w, con
         acc = dot2(wv.z, xv.z, acc);
         acc = dot2(wv.w, xv.w, acc);
     }
-    return group_sum<64>(acc);
+    return acc;
+}
+
+// One fp16 row dot x by one wave, the four parts in turn: the same inputs give
+// the same bits as gdsllm_gemv_f16.
+__device__ __forceinline__ float f16_row_dot(const uint16_t* __restrict__ w, const uint16_t* __restrict__ x, int K,
+                                             int lane) {
+    float p[4];
+#pragma unroll
+    for (int part = 0; part < 4; ++part) p[part] = group_sum<64>(f16_part_lane(w, x, K, part, lane));
+    return ((p[0] + p[1]) + p[2]) + p[3];
 }
 
 // 16 bytes per lane from global memory straight into LDS (global_load_lds_dwordx4,

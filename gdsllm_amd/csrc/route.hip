@@ -8,7 +8,8 @@
 // (runtime/qwen_moe.py:496-513).  These kernels keep all of it on the device:
 //  * gemv_f16: y = fp16(sum_k w[r][k] * x[k]) for fp16 weights (the router
 //    and the shared-expert gate; the converter stores unquantized tensors as
-//    fp16, tools/convert_qwen_moe.py:177-189), fp32 accumulation;
+//    fp16, tools/convert_qwen_moe.py:177-189), fp32 accumulation, each row in
+//    the fixed four-part order of f16_row_dot (common.h);
 //  * route_topk: the k largest logits per token in descending order (ties:
 //    lower expert index first; NaN above every number, as torch.topk), and
 //    fp16(softmax_fp32(those logits));
@@ -27,16 +28,90 @@ constexpr int kMaxBatch = 8;
 constexpr int kMaxExperts = 4096;  // 64 pick words per lane
 constexpr int kMaxTopK = 64;       // one pick per lane
 
-// One wave per row, rows dealt round-robin over the grid's waves.  Vector
-// path: each lane takes 8 consecutive weights of every 512-column chunk as one
-// 16-byte load (the row length is a multiple of 8 and every row start is
-// 16-byte aligned); the NCH loads of a row (NCH = 0: a loop over the row) are
-// all issued before the first dot product, so a wave has its whole row in
-// flight.  Scalar path: one element per lane per 64 columns.
-template <bool VEC, int NCH>
+// Vector path (K % 8 == 0, rows and x 16-byte aligned): a 4-wave workgroup
+// per row, rows dealt round-robin over the grid; wave w computes part w of
+// the row (chunks w, w+4, ... of 512 columns: all its NJ loads in flight
+// before the first dot product), the four wave sums meet in LDS and wave 0
+// adds them in part order.  The sums are f16_row_dot's, bit for bit.
+template <int NJ>
+__device__ __forceinline__ void f16_row_parts(const uint16_t* __restrict__ wr, const uint16_t* __restrict__ X, int K,
+                                              int nb, int64_t ldx, int wave, int lane, float (*part)[kMaxBatch]) {
+    if constexpr (NJ == 0) {  // rows past 16 chunks: a loop over the part's chunks
+        float acc[kMaxBatch];
+#pragma unroll
+        for (int b = 0; b < kMaxBatch; ++b) acc[b] = 0.f;
+        for (int c = 8 * lane + 512 * wave; c < K; c += 2048) {
+            const uint4 w = load_nt16(wr + c);
+#pragma unroll
+            for (int b = 0; b < kMaxBatch; ++b) {
+                if (b < nb) {
+                    const uint4 xv = *reinterpret_cast<const uint4*>(X + b * ldx + c);
+                    acc[b] = dot2(w.x, xv.x, acc[b]);
+                    acc[b] = dot2(w.y, xv.y, acc[b]);
+                    acc[b] = dot2(w.z, xv.z, acc[b]);
+                    acc[b] = dot2(w.w, xv.w, acc[b]);
+                }
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < kMaxBatch; ++b) {
+            if (b < nb) {
+                const float s = group_sum<64>(acc[b]);
+                if (lane == 0) part[wave][b] = s;
+            }
+        }
+        return;
+    }
+    constexpr int NW = NJ > 0 ? NJ : 1;
+    uint4 w[NW];
+#pragma unroll
+    for (int j = 0; j < NW; ++j) {
+        const int c = 8 * lane + 512 * (wave + 4 * j);
+        w[j] = c < K ? load_nt16(wr + c) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int b = 0; b < kMaxBatch; ++b) {
+        if (b < nb) {
+            float acc = 0.f;
+#pragma unroll
+            for (int j = 0; j < NW; ++j) {
+                const int c = 8 * lane + 512 * (wave + 4 * j);
+                if (c < K) {
+                    const uint4 xv = *reinterpret_cast<const uint4*>(X + b * ldx + c);
+                    acc = dot2(w[j].x, xv.x, acc);
+                    acc = dot2(w[j].y, xv.y, acc);
+                    acc = dot2(w[j].z, xv.z, acc);
+                    acc = dot2(w[j].w, xv.w, acc);
+                }
+            }
+            const float s = group_sum<64>(acc);
+            if (lane == 0) part[wave][b] = s;
+        }
+    }
+}
+
+// Rows blockIdx.x, += gridDim.x: y[b][r] = fp16(((p0 + p1) + p2) + p3).
+template <int NJ>
 __global__ __launch_bounds__(kF16Waves * 64) void gemv_f16(const uint16_t* __restrict__ W,
                                                            const uint16_t* __restrict__ X, uint16_t* __restrict__ Y,
                                                            int M, int K, int nb, int64_t ldx, int64_t ldy) {
+    __shared__ float part[4][kMaxBatch];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int r = blockIdx.x; r < M; r += gridDim.x) {
+        f16_row_parts<NJ>(W + static_cast<int64_t>(r) * K, X, K, nb, ldx, wave, lane, part);
+        __syncthreads();
+        if (wave == 0 && lane < nb)
+            Y[lane * ldy + r] = f2h_bits(((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane]);
+        __syncthreads();
+    }
+}
+
+// Scalar path (rows or x off the 16-byte grid, or K % 8 != 0): one wave per
+// row, one element per lane per 64 columns.
+__global__ __launch_bounds__(kF16Waves * 64) void gemv_f16_scalar(const uint16_t* __restrict__ W,
+                                                                  const uint16_t* __restrict__ X,
+                                                                  uint16_t* __restrict__ Y, int M, int K, int nb,
+                                                                  int64_t ldx, int64_t ldy) {
     const int lane = threadIdx.x & 63;
     const int wpb = static_cast<int>(blockDim.x) >> 6;
     const int nwaves = static_cast<int>(gridDim.x) * wpb;
@@ -45,50 +120,11 @@ __global__ __launch_bounds__(kF16Waves * 64) void gemv_f16(const uint16_t* __res
         float acc[kMaxBatch];
 #pragma unroll
         for (int b = 0; b < kMaxBatch; ++b) acc[b] = 0.f;
-        if constexpr (VEC && NCH > 0) {
-            uint4 w[NCH];
+        for (int c = lane; c < K; c += 64) {
+            const float w = h2f(wr[c]);
 #pragma unroll
-            for (int i = 0; i < NCH; ++i) {
-                const int c = 8 * lane + 512 * i;
-                w[i] = c < K ? load_nt16(wr + c) : make_uint4(0, 0, 0, 0);
-            }
-#pragma unroll
-            for (int b = 0; b < kMaxBatch; ++b) {
-                if (b < nb) {
-#pragma unroll
-                    for (int i = 0; i < NCH; ++i) {
-                        const int c = 8 * lane + 512 * i;
-                        if (c < K) {
-                            const uint4 xv = *reinterpret_cast<const uint4*>(X + b * ldx + c);
-                            acc[b] = dot2(w[i].x, xv.x, acc[b]);
-                            acc[b] = dot2(w[i].y, xv.y, acc[b]);
-                            acc[b] = dot2(w[i].z, xv.z, acc[b]);
-                            acc[b] = dot2(w[i].w, xv.w, acc[b]);
-                        }
-                    }
-                }
-            }
-        } else if constexpr (VEC) {
-            for (int c = 8 * lane; c < K; c += 512) {
-                const uint4 w = load_nt16(wr + c);
-#pragma unroll
-                for (int b = 0; b < kMaxBatch; ++b) {
-                    if (b < nb) {
-                        const uint4 xv = *reinterpret_cast<const uint4*>(X + b * ldx + c);
-                        acc[b] = dot2(w.x, xv.x, acc[b]);
-                        acc[b] = dot2(w.y, xv.y, acc[b]);
-                        acc[b] = dot2(w.z, xv.z, acc[b]);
-                        acc[b] = dot2(w.w, xv.w, acc[b]);
-                    }
-                }
-            }
-        } else {
-            for (int c = lane; c < K; c += 64) {
-                const float w = h2f(wr[c]);
-#pragma unroll
-                for (int b = 0; b < kMaxBatch; ++b)
-                    if (b < nb) acc[b] = fmaf(w, h2f(X[b * ldx + c]), acc[b]);
-            }
+            for (int b = 0; b < kMaxBatch; ++b)
+                if (b < nb) acc[b] = fmaf(w, h2f(X[b * ldx + c]), acc[b]);
         }
 #pragma unroll
         for (int b = 0; b < kMaxBatch; ++b) {
@@ -132,15 +168,13 @@ __device__ __forceinline__ uint32_t wave_max(uint32_t v) {
     return max(max(r0, r1), max(r2, r3));
 }
 
-// One wave per token.  NPL pick words per lane live in registers (logit
-// lane + 64*j), NPL * 64 >= E; k rounds of a wave-wide max take the next pick
-// and its owner clears it.  The softmax of the picks is in fp32, summed in
-// pick order: exp(l - max) / sum, rounded to fp16.
+// Top-k of one token by one wave.  NPL pick words per lane live in registers
+// (logit lane + 64*j), NPL * 64 >= E; k rounds of a wave-wide max take the
+// next pick and its owner clears it.  The softmax of the picks is in fp32,
+// summed in pick order: exp(l - max) / sum, rounded to fp16.
 template <int NPL>
-__global__ __launch_bounds__(64) void route_topk(const uint16_t* __restrict__ logits, int E, int64_t ld, int k,
-                                                int32_t* __restrict__ idx, uint16_t* __restrict__ wts) {
-    const int lane = threadIdx.x;
-    const uint16_t* L = logits + static_cast<int64_t>(blockIdx.x) * ld;
+__device__ __forceinline__ void topk_wave(const uint16_t* __restrict__ L, int E, int k, int32_t* __restrict__ idx,
+                                          uint16_t* __restrict__ wts, int lane) {
     // all loads first (unconditional, past E re-reading logit 0): a load under
     // a branch would be waited for before the next one is issued
     uint32_t h[NPL], word[NPL];
@@ -176,9 +210,17 @@ __global__ __launch_bounds__(64) void route_topk(const uint16_t* __restrict__ lo
     for (int i = 0; i < k; ++i)
         sum = fp32_rounded(sum + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_ex), i)));
     if (lane < k) {
-        idx[static_cast<int64_t>(blockIdx.x) * k + lane] = my_idx;
-        wts[static_cast<int64_t>(blockIdx.x) * k + lane] = f2h_bits(fp32_rounded(my_ex / sum));
+        idx[lane] = my_idx;
+        wts[lane] = f2h_bits(fp32_rounded(my_ex / sum));
     }
+}
+
+// One wave per token.
+template <int NPL>
+__global__ __launch_bounds__(64) void route_topk(const uint16_t* __restrict__ logits, int E, int64_t ld, int k,
+                                                int32_t* __restrict__ idx, uint16_t* __restrict__ wts) {
+    const int64_t t = blockIdx.x;
+    topk_wave<NPL>(logits + t * ld, E, k, idx + t * k, wts + t * k, static_cast<int>(threadIdx.x));
 }
 
 // y = clamp(e + fp16(fp16(sigmoid(g)) * s), -65504, 65504) elementwise, g per token.
@@ -223,25 +265,20 @@ extern "C" int gdsllm_gemv_f16(const void* weight, const void* x, void* y, int64
     const auto* xp = static_cast<const uint16_t*>(x);
     auto* yp = static_cast<uint16_t*>(y);
     const hipStream_t st = as_stream(stream);
-    if (vec && K <= 16 * 512) {
-        // one-wave workgroups, so even a few hundred rows reach every CU
-        const int grid = std::min(M, 32 * cu_count());
-        const int nch = (K + 511) / 512;
+    if (vec) {
+        // a 4-wave workgroup per row (one row each while the grid fits)
+        const int grid = std::min(M, 16 * cu_count());
+        const int nj = ((K + 511) / 512 + 3) / 4;
         auto launch = [&](auto kern) {
-            hipLaunchKernelGGL(kern, dim3(grid), dim3(64), 0, st, w, xp, yp, M, K, B, ldx, ldy);
+            hipLaunchKernelGGL(kern, dim3(grid), dim3(kF16Waves * 64), 0, st, w, xp, yp, M, K, B, ldx, ldy);
         };
-        if (nch <= 2) launch(gemv_f16<true, 2>);
-        else if (nch <= 4) launch(gemv_f16<true, 4>);
-        else if (nch <= 8) launch(gemv_f16<true, 8>);
-        else launch(gemv_f16<true, 16>);
+        if (nj <= 1) launch(gemv_f16<1>);
+        else if (nj <= 2) launch(gemv_f16<2>);
+        else if (nj <= 4) launch(gemv_f16<4>);
+        else launch(gemv_f16<0>);
     } else {
         const int grid = std::min((M + kF16Waves - 1) / kF16Waves, 8 * cu_count());
-        if (vec)
-            hipLaunchKernelGGL((gemv_f16<true, 0>), dim3(grid), dim3(kF16Waves * 64), 0, st, w, xp, yp, M, K, B, ldx,
-                               ldy);
-        else
-            hipLaunchKernelGGL((gemv_f16<false, 0>), dim3(grid), dim3(kF16Waves * 64), 0, st, w, xp, yp, M, K, B,
-                               ldx, ldy);
+        hipLaunchKernelGGL(gemv_f16_scalar, dim3(grid), dim3(kF16Waves * 64), 0, st, w, xp, yp, M, K, B, ldx, ldy);
     }
     if (int rc = check_hip(hipGetLastError(), "gemv_f16 launch")) return rc;
     return ok();

@@ -12,7 +12,8 @@ from helpers import assert_gemv_close, capi, check, gen, on_gpu, oq, ptr, stream
 
 pytestmark = pytest.mark.gpu
 
-F16_CASES = [(512, 4096, 1), (512, 4096, 3), (512, 2048, 8), (1, 4096, 1), (100, 1000, 2), (37, 100, 1), (9, 20, 4)]
+F16_CASES = [(512, 4096, 1), (512, 4096, 3), (512, 2048, 8), (1, 4096, 1), (100, 1000, 2), (37, 100, 1), (9, 20, 4),
+             (60, 1024, 1), (48, 8192, 2), (16, 12288, 3), (2048, 4096, 1)]
 
 
 @pytest.mark.parametrize("M,K,B", F16_CASES, ids=[f"{m}x{k}_b{b}" for m, k, b in F16_CASES])

@@ -744,7 +744,11 @@ template <int LR, int CPL, int NB, class Rows>
 __global__ __launch_bounds__(kThreads) void affine_rows(Rows rows, const uint16_t* __restrict__ X, int K, int gsize,
                                                         int64_t ldx, int x_al16) {
     constexpr int RPG = 64 / LR;  // rows per load group
-    constexpr int G = 4;          // load groups per stage
+    // load groups per stage: gate/up pairs take one pair (gate row n, up row
+    // n) per stage, loaded after the previous stage is computed; plain rows
+    // take 4 rows per stage with the next stage requested before the compute
+    constexpr bool kPairs = IsGateUp<Rows>::value;
+    constexpr int G = kPairs ? 2 : 4;
     constexpr int RPS = G * RPG;  // rows per stage
     static_assert(!IsGateUp<Rows>::value || (LR == 64 && NB == 1), "gate/up pairs need one row per load group");
     const int lane = threadIdx.x & 63;
@@ -800,6 +804,12 @@ __global__ __launch_bounds__(kThreads) void affine_rows(Rows rows, const uint16_
             const int c = li + LR * i;
             load_xchunk_raw(xr[b][i], X + b * ldx + 32 * c, x_al16 != 0, c < CPR);
         }
+    // Gate/up pairs: the expert indices (lane_idx) and x in before any weight
+    // is requested.  Waiting for them here, once, lets every later read of
+    // lane_idx go without a wait; otherwise the compiler, unsure how many
+    // (conditional) weight loads follow it, drains all of them before each
+    // load group.  It also keeps x from queueing behind the weights.
+    if constexpr (kPairs) wait_vmcnt<0>();
     issue(gw);
     XChunk xc[NB][CPL];
     bool x_nonfinite = false;
@@ -851,7 +861,7 @@ __global__ __launch_bounds__(kThreads) void affine_rows(Rows rows, const uint16_
                 cb[j][i] = bv[j][i];
             }
         }
-        if (t + 1 < T) issue(st + TW);
+        if (!kPairs && t + 1 < T) issue(st + TW);
         float acc[NB][G];
 #pragma unroll
         for (int b = 0; b < NB; ++b)
@@ -869,21 +879,30 @@ __global__ __launch_bounds__(kThreads) void affine_rows(Rows rows, const uint16_
                                                  h2f(cb[j][i]), nu);
                 }
         }
-        const int j = reduce4_index<LR>(lane);
-        const int row = st * RPS + j * RPG + sub;
-        const bool writer = (li % (LR / 4)) == 0 && row < rows.M;
+        if constexpr (kPairs) {
+            // one row per half-wave (LR = 64): lanes 0-31 the gate row, 32-63 the up row
+            const bool b1 = lane & 32;
+            float v = b1 ? acc[0][1] : acc[0][0];
+            v += __shfl_xor(b1 ? acc[0][0] : acc[0][1], 32);
+            v += __shfl_xor(v, 16);
+            v = lanes_sum<16>(v);
+            const int row = st * RPS + (b1 ? 1 : 0);
+            if ((lane & 31) == 0 && row < rows.M) rows.store(0, row, v);
+            const float up = __shfl_xor(v, 32);
+            if (lane == 0 && row < rows.M) {
+                const int k = row / (2 * rows.F);
+                const int n = (row - k * 2 * rows.F) >> 1;
+                rows.h[k * rows.F + n] = silu_mul_h(v, up);
+            }
+            if (t + 1 < T) issue(st + TW);
+        } else {
+            const int j = reduce4_index<LR>(lane);
+            const int row = st * RPS + j * RPG + sub;
+            const bool writer = (li % (LR / 4)) == 0 && row < rows.M;
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            const float v = reduce4<LR>(acc[b], lane);
-            if (writer) rows.store(b, row, v);
-            if constexpr (IsGateUp<Rows>::value) {
-                // lanes 0 / 32 hold gate rows n, n+1; lanes 16 / 48 the matching up rows
-                const float other = __shfl_xor(v, 16);
-                if ((lane & 31) == 0 && row < rows.M) {
-                    const int k = row / (2 * rows.F);
-                    const int n = (row - k * 2 * rows.F) >> 1;
-                    rows.h[k * rows.F + n] = silu_mul_h(v, other);
-                }
+            for (int b = 0; b < NB; ++b) {
+                const float v = reduce4<LR>(acc[b], lane);
+                if (writer) rows.store(b, row, v);
             }
         }
     }
@@ -929,25 +948,29 @@ __global__ __launch_bounds__(NT) void moe_down_rows(gdsllm_affine_experts down, 
     // Request order: expert indices and routing weights, then this thread's
     // first h items, then (once the indices are in) the first stage's weights;
     // loads retire in order, so each consumer waits only for what it needs.
+    // Every load here is unconditional (indices clamped to valid addresses,
+    // what is out of range discarded afterwards): a load under a branch leaves
+    // the compiler unsure how many loads follow it, and it then waits for all
+    // of them before the first use, i.e. for the weights before h is prepared.
     int eraw[SLOTS];
     uint32_t wraw[SLOTS];
 #pragma unroll
     for (int i = 0; i < SLOTS; ++i) {
         const int k = i * EPI + sub;
-        eraw[i] = k < top_k ? idx[k] : (k == top_k && nsh ? 0 : -1);
-        wraw[i] = k < top_k ? rw[k] : 0u;
+        const int kc = k < top_k ? k : 0;
+        eraw[i] = idx[kc];
+        wraw[i] = rw[kc];
     }
     const uint32_t graw = nsh ? gl[0] : 0u;
-    constexpr int kEarly = 2;
+    constexpr int kEarly = NT >= 1024 ? 2 : 3;
     const int items = (top_k + nsh) * CPR * 4;
     uint4 hraw[kEarly];
 #pragma unroll
     for (int u = 0; u < kEarly; ++u) {
-        const int it = u * NT + threadIdx.x;
-        if (it < items) {
-            const int wq = it & 3, c = (it >> 2) % CPR, k = (it >> 2) / CPR;
-            hraw[u] = *reinterpret_cast<const uint4*>(hbuf + k * F + 32 * c + 8 * wq);
-        }
+        const int it0 = u * NT + threadIdx.x;
+        const int it = it0 < items ? it0 : 0;
+        const int wq = it & 3, c = (it >> 2) % CPR, k = (it >> 2) / CPR;
+        hraw[u] = *reinterpret_cast<const uint4*>(hbuf + k * F + 32 * c + 8 * wq);
     }
 
     // expert slot of each lane: k, routing weight, this lane's chunk of row 0
@@ -960,7 +983,7 @@ __global__ __launch_bounds__(NT) void moe_down_rows(gdsllm_affine_experts down, 
 #pragma unroll
     for (int i = 0; i < SLOTS; ++i) {
         const int k = i * EPI + sub;
-        const int e = eraw[i];
+        const int e = k < top_k ? eraw[i] : (k == top_k && nsh ? 0 : -1);
         shs[i] = SH && k == top_k;
         const gdsllm_affine_experts& p = shs[i] ? sdown : down;
         const bool valid = e >= 0 && e < p.num_experts;
@@ -973,20 +996,22 @@ __global__ __launch_bounds__(NT) void moe_down_rows(gdsllm_affine_experts down, 
     }
     uint4 wv[R][SLOTS];
     uint32_t sv[R][SLOTS], bv[R][SLOTS];  // raw bits: see affine_rows
+    // unconditional loads (see above): a slot without an expert reads expert
+    // 0 and a row past the end reads the last row, both discarded
     auto issue = [&](int st) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const int o = st * R + r;
+            const int o0 = st * R + r;
+            const int64_t o = o0 < H ? o0 : H - 1;
 #pragma unroll
-            for (int i = 0; i < SLOTS; ++i)
-                if (kk[i] >= 0 && o < H) {
-                    wv[r][i] = load_nt16(wrow[i] + static_cast<int64_t>(o) * (F / 2));
-                    sv[r][i] = srow[i][static_cast<int64_t>(o) * gpr];
-                    bv[r][i] = brow[i][static_cast<int64_t>(o) * gpr];
-                }
+            for (int i = 0; i < SLOTS; ++i) {
+                wv[r][i] = load_nt16(wrow[i] + o * (F / 2));
+                sv[r][i] = srow[i][o * gpr];
+                bv[r][i] = brow[i][o * gpr];
+            }
         }
     };
-    if (T > 0) issue(gw);
+    issue(gw);
     // prepared h records [top_k][CPR], one quarter (8 elements) per item
     bool h_nonfinite = false;
     {
@@ -1110,7 +1135,7 @@ __global__ __launch_bounds__(NT) void moe_down_rows(gdsllm_affine_experts down, 
 template <int LR, int CPL, int NB, class Rows>
 int launch_affine_rows(const Rows& rows, const uint16_t* x, int K, int gsize, int64_t ldx, hipStream_t stream) {
     const void* fn = reinterpret_cast<const void*>(&affine_rows<LR, CPL, NB, Rows>);
-    const int rps = 4 * (64 / LR);
+    const int rps = (IsGateUp<Rows>::value ? 2 : 4) * (64 / LR);  // rows per stage, as in affine_rows
     const int stages = (rows.M + rps - 1) / rps;
     const int need = (stages + kWaves - 1) / kWaves;
     const int cap = blocks_per_cu(fn, 0, kThreads) * cu_count();

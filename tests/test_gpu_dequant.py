@@ -58,6 +58,30 @@ def test_gguf_dequant_special_scales(gpu, fmt):
     assert np.array_equal(_bits(got), _bits(ref))
 
 
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+def test_gguf_dequant_nonfinite_scales(gpu, fmt):
+    """Infinite and NaN scales: +-inf where the reference's fp32 product is
+    infinite, NaN where it is NaN (inf * 0 at q = 8, any NaN d).  NaN payloads
+    differ between processors (x86, this GPU and CUDA each make their own
+    default NaN), so NaN outputs are compared as NaN and every other output
+    bit for bit.  Q8_0 codes include -128 and 127."""
+    make = syn.q4_0_weights if fmt == "q4_0" else syn.q8_0_weights
+    bb = 18 if fmt == "q4_0" else 34
+    raw = make(1, 32 * 8, gen(4)).view(-1, bb).clone()
+    specials = np.array([np.inf, -np.inf, np.nan, -np.nan, 1.0, -1.0, np.inf, 2.0], dtype=np.float16)
+    bits = specials.view(np.uint16).copy()
+    bits[7] = 0x7C01  # signaling NaN
+    raw[:, :2] = torch.from_numpy(bits.view(np.uint8).reshape(8, 2).copy())
+    raw[0, 2:] = 0x88 if fmt == "q4_0" else 0  # d*0: NaN for an infinite d
+    raw[6, 2:] = torch.tensor([0x80, 0x7F] * ((bb - 2) // 2), dtype=torch.uint8) if fmt == "q8_0" else 0x0F
+    got = _dequant_gguf(fmt, raw.reshape(-1), gpu)
+    ref = (oq.dequant_q4_0 if fmt == "q4_0" else oq.dequant_q8_0)(to_np(raw.reshape(-1)))
+    nan = np.isnan(ref)
+    assert nan.any() and np.isinf(ref).any()
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(_bits(got)[~nan], _bits(ref)[~nan])
+
+
 @pytest.mark.parametrize("rows,cols,g", [(1, 64, 64), (4, 1024, 64), (1024, 4096, 64), (3, 256, 128), (5, 96, 32),
                                          (2, 64, 8), (3, 48, 16)])
 def test_affine_dequant_bit_exact(gpu, rows, cols, g):

@@ -26,6 +26,7 @@
 //    the 16-lane DPP row; lane 0 of the row writes the fp16 result.
 
 #include <algorithm>
+#include <type_traits>
 #include <utility>
 
 #include "common.h"
@@ -708,17 +709,6 @@ __device__ __forceinline__ void rows_pair_impl(const uint8_t* buf, const XSlice<
     }
 }
 
-// The window's products, exact or offset-corrected as its x requires (a
-// wave-uniform branch).
-template <Fmt F, int NB, int R0, int NR = 2>
-__device__ __forceinline__ void rows_pair(const uint8_t* buf, const XSlice<NB>& xs, float (&acc)[NB][4],
-                                          const NibUnpack& nu, int lane) {
-    if (xs.exact)
-        rows_pair_impl<F, NB, R0, NR, true>(buf, xs, acc, nu, lane);
-    else
-        rows_pair_impl<F, NB, R0, NR, false>(buf, xs, acc, nu, lane);
-}
-
 // Rows of `target` times x (MODE 0: one matrix; 1: a group; 2: gate/up pairs); x must be 16-byte aligned
 // with ldx % 8 == 0.  Workgroups of kWaves waves; LDS (dynamic): the waves'
 // stage buffers, then raw x.  One buffer per wave: after rows 0-1 of a stage are consumed, the next
@@ -797,27 +787,37 @@ __global__ __launch_bounds__(kWaves * 64) void gguf_gemv_rows(const RowsTarget t
         // Lanes past the end of a partial window skip; rows past M compute on
         // filler bytes and are never stored.  In flight here: this stage only.
         // Each row is consumed as soon as the transfers that hold it retire.
+        // The window's product form is one wave-uniform branch around the whole
+        // stage, so each form is straight-line code the compiler schedules
+        // across rows.
         const bool active = lane < st.nsb * 4;
-        wait_vmcnt<C - kRowDone[0]>();
-        if (active) rows_pair<F, NB, 0, 1>(buf, xs, acc, nu, lane);
-        wait_vmcnt<C - kRowDone[1]>();
-        if (active) rows_pair<F, NB, 1, 1>(buf, xs, acc, nu, lane);
-        // refill slots of rows 0-1 once their reads have returned
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         const RowsStage nx = stage_at(t + 1);
-        if (next) {
-            rows_issue<F, 0, kEarly, PAIRED>(buf, nx, X, row_bytes, goff, true, lane);
-            wait_vmcnt<C - kRowDone[2] + kEarly>();
-            if (active) rows_pair<F, NB, 2, 1>(buf, xs, acc, nu, lane);
-            wait_vmcnt<kEarly>();
-        } else {
-            wait_vmcnt<C - kRowDone[2]>();
-            if (active) rows_pair<F, NB, 2, 1>(buf, xs, acc, nu, lane);
-            wait_vmcnt<0>();
-        }
-        if (active) rows_pair<F, NB, 3, 1>(buf, xs, acc, nu, lane);
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        if (next) rows_issue<F, kEarly, C, PAIRED>(buf, nx, X, row_bytes, goff, true, lane);
+        auto consume = [&](auto exact_c) {
+            constexpr bool EX = decltype(exact_c)::value;
+            wait_vmcnt<C - kRowDone[0]>();
+            if (active) rows_pair_impl<F, NB, 0, 1, EX>(buf, xs, acc, nu, lane);
+            wait_vmcnt<C - kRowDone[1]>();
+            if (active) rows_pair_impl<F, NB, 1, 1, EX>(buf, xs, acc, nu, lane);
+            // refill slots of rows 0-1 once their reads have returned
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            if (next) {
+                rows_issue<F, 0, kEarly, PAIRED>(buf, nx, X, row_bytes, goff, true, lane);
+                wait_vmcnt<C - kRowDone[2] + kEarly>();
+                if (active) rows_pair_impl<F, NB, 2, 1, EX>(buf, xs, acc, nu, lane);
+                wait_vmcnt<kEarly>();
+            } else {
+                wait_vmcnt<C - kRowDone[2]>();
+                if (active) rows_pair_impl<F, NB, 2, 1, EX>(buf, xs, acc, nu, lane);
+                wait_vmcnt<0>();
+            }
+            if (active) rows_pair_impl<F, NB, 3, 1, EX>(buf, xs, acc, nu, lane);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            if (next) rows_issue<F, kEarly, C, PAIRED>(buf, nx, X, row_bytes, goff, true, lane);
+        };
+        if (kRowsExact && xs.exact)
+            consume(std::true_type{});
+        else
+            consume(std::false_type{});
         if (win == NW - 1) {
             const int row = lane >> 4;
 #pragma unroll

@@ -445,6 +445,27 @@ def bench_moe(dev, calls: int = 64, reps: int = 20, decode_step: bool = True):
                                                    yf[i].data_ptr(), wsf.data_ptr(), wsf_bytes, s))
 
     ms3 = _replay_ms(step_fused, reps) / calls
+
+    # The same step with the routing folded in (gdsllm_moe_step_routed_affine_q4):
+    # router GEMV, then the gate/up launch whose waves take the top-k
+    # themselves, then down: 3 launches.
+    wsr_bytes = capi().gdsllm_moe_step_routed_workspace_size(k, Fd, E)
+    wsr = torch.empty(wsr_bytes, dtype=torch.uint8, device=dev)
+    ridx3 = torch.empty(calls, k, dtype=torch.int32, device=dev)
+    rw3 = torch.empty(calls, k, dtype=torch.float16, device=dev)
+    y3 = torch.empty(calls, H, dtype=torch.float16, device=dev)
+
+    def step_routed():
+        s = torch.cuda.current_stream().cuda_stream
+        for i in range(calls):
+            sg_, su_, sd_ = sh_one[i]
+            check(capi().gdsllm_moe_step_routed_affine_q4(router[i].data_ptr(), ctypes.byref(gate), ctypes.byref(up),
+                                                          ctypes.byref(down), ctypes.byref(sg_), ctypes.byref(su_),
+                                                          ctypes.byref(sd_), xs[i].data_ptr(), k,
+                                                          sgate[i].data_ptr(), y3[i].data_ptr(), ridx3[i].data_ptr(),
+                                                          rw3[i].data_ptr(), wsr.data_ptr(), wsr_bytes, s))
+
+    ms4 = _replay_ms(step_routed, reps) / calls
     torch.cuda.synchronize()
     nbytes2 = E * H * 2 + (k + 1) * per_expert + H * 2 + 2 * H * 2
     includes = ("fp16 router GEMV 512x4096, top-k+softmax, top-10 gather, shared expert (ffn 1024), "
@@ -454,7 +475,13 @@ def bench_moe(dev, calls: int = 64, reps: int = 20, decode_step: bool = True):
         "GB_s": round(nbytes2 / (ms3 * 1e-3) / 1e9, 1), "pct_of_hbm_peak": round(nbytes2 / (ms3 * 1e-3) / 1e9 / 80, 1),
         "launches": 4, "host_syncs": 0, "includes": includes,
         "separate_launches": {"us_per_token_layer": round(ms2 * 1e3, 3), "launches": 8},
-        "bit_identical_to_separate": bool(torch.equal(yf.view(torch.int16), yy.view(torch.int16)))}
+        "bit_identical_to_separate": bool(torch.equal(yf.view(torch.int16), yy.view(torch.int16))),
+        "routed": {"us_per_token_layer": round(ms4 * 1e3, 3), "launches": 3,
+                   "GB_s": round(nbytes2 / (ms4 * 1e-3) / 1e9, 1),
+                   "pct_of_hbm_peak": round(nbytes2 / (ms4 * 1e-3) / 1e9 / 80, 1),
+                   "bit_identical_to_fused": bool(torch.equal(y3.view(torch.int16), yf.view(torch.int16)) and
+                                                  torch.equal(ridx3, ridx) and
+                                                  torch.equal(rw3.view(torch.int16), rw.view(torch.int16)))}}
     return out
 
 

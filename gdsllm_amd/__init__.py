@@ -58,6 +58,8 @@ SIGNATURES = {
     "gdsllm_moe_gather_affine_q4_noalloc": (ctypes.c_int, [ctypes.POINTER(AffineExperts)] * 3 + [_c_vp, _c_vp, _c_vp, _c_i64, _c_vp, _c_vp]),
     "gdsllm_moe_step_affine_q4": (ctypes.c_int, [ctypes.POINTER(AffineExperts)] * 6 + [_c_vp, _c_vp, _c_vp, _c_i64, _c_vp, _c_vp, _c_vp, ctypes.c_size_t, _c_vp]),
     "gdsllm_moe_step_workspace_size": (ctypes.c_size_t, [_c_i64, _c_i64]),
+    "gdsllm_moe_step_routed_affine_q4": (ctypes.c_int, [_c_vp] + [ctypes.POINTER(AffineExperts)] * 6 + [_c_vp, _c_i64, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, ctypes.c_size_t, _c_vp]),
+    "gdsllm_moe_step_routed_workspace_size": (ctypes.c_size_t, [_c_i64, _c_i64, _c_i64]),
     "gdsllm_dequant_gemm_q4_0": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp]),
     "gdsllm_dequant_gemm_q8_0": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp]),
     "gdsllm_dequant_gemm_affine_q4": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp]),

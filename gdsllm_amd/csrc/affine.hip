@@ -28,6 +28,7 @@
 #include <mutex>
 
 #include "common.h"
+#include "topk.h"
 
 namespace gdsllm {
 namespace {
@@ -658,12 +659,22 @@ __device__ __forceinline__ int reduce4_index(int lane) {
 // [top_k][2][F], and h = fp16(fp16(silu(g)) * u) fp16 [top_k][F].
 // The shared expert of the fused decode step (one-expert descriptors) fills
 // slot shared_slot, after the routed slots.
+// With router logits (routed step), every wave takes the top-k itself from
+// the fp16 logits of all route_e experts (top_k = shared_slot picks, the
+// selection of route_topk, topk.h), and the grid's first wave also stores
+// the picks and their fp16 softmax weights for the down launch and the
+// caller.
 struct SharedSlot {
     gdsllm_affine_experts sgate, sup;
     int shared_slot;
     const uint16_t* gate_w;  // fp16 [K] shared-expert gate row
     uint16_t* logit;         // fp16 out: its logit on x
+    const uint16_t* route_logits;  // fp16 [route_e], or null: picks come from idx
+    int route_e;                   // experts routed over (<= kRouteMaxExperts, multiple of 8)
+    int32_t* route_idx;            // out: the top_k picks, descending
+    uint16_t* route_w;             // out: their fp16 softmax weights
 };
+constexpr int kRouteMaxExperts = 512;  // 8 logits per lane
 struct NoSharedSlot {};
 
 template <bool SH>
@@ -680,6 +691,33 @@ struct GateUpPairsT : std::conditional_t<SH, SharedSlot, NoSharedSlot> {
         if constexpr (SH)
             if (lane == this->shared_slot) return 0;
         return lane < M / (2 * F) ? idx[lane] : -1;
+    }
+    // lane_index of the routed step: the wave's own top-k of the router
+    // logits (lane l holds logits 8l .. 8l+7, one 16-byte load); the writer
+    // wave stores the picks and weights.
+    __device__ uint4 route_load(int lane) const {
+        return load_nt16(this->route_logits + 8 * (8 * lane < this->route_e ? lane : 0));
+    }
+    __device__ int route_lane(uint4 v, int lane, bool writer) const {
+        static_assert(SH, "routing is part of the fused step");
+        const int E = this->route_e, k = this->shared_slot;
+        const bool in = 8 * lane < E;
+        const uint32_t hv[4] = {v.x, v.y, v.z, v.w};
+        uint32_t word[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) word[j] = in ? pick_word((hv[j >> 1] >> (16 * (j & 1))) & 0xFFFFu, 8 * lane + j) : 0u;
+        int my_idx;
+        uint32_t my_key, top_key;
+        topk_select<8>(word, k, lane, my_idx, my_key, top_key);
+        if (writer) {
+            const uint16_t w = topk_weight(my_key, top_key, k, lane);
+            if (lane < k) {
+                this->route_idx[lane] = my_idx;
+                this->route_w[lane] = w;
+            }
+        }
+        if (lane == this->shared_slot) return 0;
+        return lane < k ? my_idx : -1;
     }
     __device__ const gdsllm_affine_experts& proj(int k, bool is_up) const {
         if constexpr (SH)
@@ -714,16 +752,14 @@ struct GateUpPairsT : std::conditional_t<SH, SharedSlot, NoSharedSlot> {
         const int rem = v - k * 2 * F;
         gu[(2 * k + (rem & 1)) * F + (rem >> 1)] = f2h_bits(val);
     }
-    // locate for one lane on its own (no wave-wide reads): the slow path
-    __device__ bool locate_lane(int v, const uint32_t*& w, const uint16_t*& s, const uint16_t*& b, int K,
-                                int gpr) const {
+    // locate for one lane on its own, its slot's expert e given (the
+    // lane_index of lane v / 2F): the slow path
+    __device__ bool locate_pair_lane(int v, int e, const uint32_t*& w, const uint16_t*& s, const uint16_t*& b, int K,
+                                     int gpr) const {
         const int k = v / (2 * F);
         const int rem = v - k * 2 * F;
         const int n = rem >> 1;
         const gdsllm_affine_experts& p = proj(k, rem & 1);
-        int e = k < M / (2 * F) ? idx[k] : -1;
-        if constexpr (SH)
-            if (k == this->shared_slot) e = 0;
         if (e < 0 || e >= p.num_experts) return false;
         w = reinterpret_cast<const uint32_t*>(static_cast<const char*>(p.weight) + e * p.weight_stride) +
             static_cast<int64_t>(n) * (K / 8);
@@ -758,15 +794,45 @@ __global__ __launch_bounds__(kThreads) void affine_rows(Rows rows, const uint16_
     const int TW = gridDim.x * kWaves;
     const int gw = blockIdx.x * kWaves + (threadIdx.x >> 6);
     const int T = gw < stages ? (stages - 1 - gw) / TW + 1 : 0;
-    if constexpr (std::is_same_v<Rows, GateUpPairsT<true>>) {
+    constexpr bool kRoutable = std::is_same_v<Rows, GateUpPairsT<true>>;
+    uint32_t xr[NB][CPL][16];
+    auto load_x = [&] {
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int i = 0; i < CPL; ++i) {
+                const int c = li + LR * i;
+                load_xchunk_raw(xr[b][i], X + b * ldx + 32 * c, x_al16 != 0, c < CPR);
+            }
+    };
+    int routed_idx = -1;
+    if constexpr (kRoutable) {
+        // x in flight through the routing and the gate logit
+        load_x();
+        if (rows.route_logits) {
+            // routed step: one wave of the workgroup takes the top-k (wave
+            // blockIdx % 4, so the routing waves of a CU's workgroups sit on
+            // different SIMDs) and hands the picks to the others through LDS;
+            // every wave of the workgroup is still here for the barrier
+            __shared__ int route_pick[64];
+            if ((threadIdx.x >> 6) == static_cast<int>(blockIdx.x & (kWaves - 1)))
+                route_pick[lane] = rows.route_lane(rows.route_load(lane), lane, blockIdx.x == 0);
+            __syncthreads();
+            routed_idx = route_pick[lane];
+        }
         // the shared-expert gate logit, by the grid's last wave (it has the
         // fewest stages), as gdsllm_gemv_f16 would compute it
         if (gw == TW - 1) {
             const float g = f16_row_dot(rows.gate_w, X, K, lane);
             if (lane == 0) *rows.logit = f2h_bits(g);
         }
+        if (T == 0) {
+            wait_vmcnt<0>();  // no load outlives its wave
+            return;
+        }
+    } else {
+        if (T == 0) return;
     }
-    if (T == 0) return;
     const NibUnpack nu;
 
     // Scale / bias bits stay raw until the compute: converting them here would
@@ -775,7 +841,8 @@ __global__ __launch_bounds__(kThreads) void affine_rows(Rows rows, const uint16_
     uint4 wv[G][CPL];
     uint32_t sv[G][CPL], bv[G][CPL];
     bool ok[G];
-    const int lane_idx = rows.lane_index(lane);
+    // the slot experts: idx[lane], or (routed step) the workgroup's top-k
+    int lane_idx = -1;
     auto issue = [&](int st) {
 #pragma unroll
         for (int j = 0; j < G; ++j) {
@@ -796,14 +863,11 @@ __global__ __launch_bounds__(kThreads) void affine_rows(Rows rows, const uint16_
         }
     };
     // x first, then the first stage's weights: preparing x waits only for x
-    uint32_t xr[NB][CPL][16];
-#pragma unroll
-    for (int b = 0; b < NB; ++b)
-#pragma unroll
-        for (int i = 0; i < CPL; ++i) {
-            const int c = li + LR * i;
-            load_xchunk_raw(xr[b][i], X + b * ldx + 32 * c, x_al16 != 0, c < CPR);
-        }
+    if constexpr (!kRoutable) load_x();
+    if constexpr (kRoutable)
+        lane_idx = rows.route_logits ? routed_idx : rows.lane_index(lane);
+    else
+        lane_idx = rows.lane_index(lane);
     // Gate/up pairs: the expert indices (lane_idx) and x in before any weight
     // is requested.  Waiting for them here, once, lets every later read of
     // lane_idx go without a wait; otherwise the compiler, unsure how many
@@ -828,11 +892,13 @@ __global__ __launch_bounds__(kThreads) void affine_rows(Rows rows, const uint16_
         for (int t = 0; t < T; ++t) {
             const int row = (gw + t * TW) * RPS + lane;
             if constexpr (IsGateUp<Rows>::value) {
+                // the slot's expert from the lane that holds it, read with every lane active
+                const int e = __shfl(lane_idx, (row / (2 * rows.F)) & 63);
                 if (lane < RPS && (lane & 1) == 0 && row + 1 < rows.M) {
                     const uint32_t *wg, *wu;
                     const uint16_t *sg, *bg, *su, *bu;
-                    const float g = rows.locate_lane(row, wg, sg, bg, K, gpr) ? affine_row_exact(wg, sg, bg, X, K, gsize) : 0.f;
-                    const float u = rows.locate_lane(row + 1, wu, su, bu, K, gpr) ? affine_row_exact(wu, su, bu, X, K, gsize) : 0.f;
+                    const float g = rows.locate_pair_lane(row, e, wg, sg, bg, K, gpr) ? affine_row_exact(wg, sg, bg, X, K, gsize) : 0.f;
+                    const float u = rows.locate_pair_lane(row + 1, e, wu, su, bu, K, gpr) ? affine_row_exact(wu, su, bu, X, K, gsize) : 0.f;
                     rows.store(0, row, g);
                     rows.store(0, row + 1, u);
                     const int k = row / (2 * rows.F);
@@ -1476,13 +1542,26 @@ extern "C" int gdsllm_moe_gather_affine_q4_noalloc(const gdsllm_affine_experts* 
                            kNoAllocScratchBytes, stream, /*fixed_ws=*/true);
 }
 
-extern "C" int gdsllm_moe_step_affine_q4(const gdsllm_affine_experts* gate, const gdsllm_affine_experts* up,
-                                         const gdsllm_affine_experts* down, const gdsllm_affine_experts* shared_gate,
-                                         const gdsllm_affine_experts* shared_up,
-                                         const gdsllm_affine_experts* shared_down, const void* x, const int32_t* idx,
-                                         const void* routing_weights, int64_t top_k, const void* shared_gate_weight,
-                                         void* y, void* workspace, size_t workspace_bytes, void* stream) {
-    const std::string n = "moe_step_affine_q4";
+namespace {
+// The routed step's extra inputs: the fp16 router logits of num_experts
+// experts and where the picks and their weights go.
+struct RouteArgs {
+    const uint16_t* logits;
+    int num_experts;
+    int32_t* idx_out;
+    uint16_t* w_out;
+};
+}  // namespace
+
+// The fused decode step (gate/up with the shared expert, then down with the
+// combine); route != null takes the picks from the router logits inside the
+// gate/up launch (idx / routing_weights then name where they are stored).
+static int moe_step_impl(const std::string& n, const gdsllm_affine_experts* gate, const gdsllm_affine_experts* up,
+                         const gdsllm_affine_experts* down, const gdsllm_affine_experts* shared_gate,
+                         const gdsllm_affine_experts* shared_up, const gdsllm_affine_experts* shared_down,
+                         const void* x, const int32_t* idx, const void* routing_weights, int64_t top_k,
+                         const void* shared_gate_weight, void* y, void* workspace, size_t workspace_bytes,
+                         void* stream, const RouteArgs* route, bool dry_run = false) {
     std::string err;
     if (check_experts(gate, "gate", err) || check_experts(up, "up", err) || check_experts(down, "down", err) ||
         check_experts(shared_gate, "shared_gate", err) || check_experts(shared_up, "shared_up", err) ||
@@ -1523,6 +1602,7 @@ extern "C" int gdsllm_moe_step_affine_q4(const gdsllm_affine_experts* gate, cons
     const size_t budget = lds_budget();
     if (static_cast<size_t>(nslot) * cpr_f * kRec > budget || static_cast<size_t>(cpr_h) * kRec > budget)
         return set_error(GDSLLM_ERR_UNSUPPORTED, n + ": hidden or (top_k+1)*ffn too large for LDS staging");
+    if (dry_run) return GDSLLM_OK;
     hipStream_t s = as_stream(stream);
     auto* gu = static_cast<uint16_t*>(workspace);
     uint16_t* h = gu + static_cast<int64_t>(nslot) * 2 * F;  // after the gate/up outputs of every slot
@@ -1542,6 +1622,12 @@ extern "C" int gdsllm_moe_step_affine_q4(const gdsllm_affine_experts* gate, cons
                                             gdsllm_moe_gather_workspace_size(top_k + 1, F));
     pairs.gate_w = static_cast<const uint16_t*>(shared_gate_weight);
     pairs.logit = glw;
+    if (route) {
+        pairs.route_logits = route->logits;
+        pairs.route_e = route->num_experts;
+        pairs.route_idx = route->idx_out;
+        pairs.route_w = route->w_out;
+    }
     const auto* xp = static_cast<const uint16_t*>(x);
     const int gs = static_cast<int>(gate->group_size);
     int rc;
@@ -1562,4 +1648,57 @@ extern "C" int gdsllm_moe_step_affine_q4(const gdsllm_affine_experts* gate, cons
         default: rc = dispatch_moe_down_slots<64>(slots, *down, idx, wp, h, tk, yp, s, shared_down, gl); break;
     }
     return rc ? rc : ok();
+}
+
+extern "C" int gdsllm_moe_step_affine_q4(const gdsllm_affine_experts* gate, const gdsllm_affine_experts* up,
+                                         const gdsllm_affine_experts* down, const gdsllm_affine_experts* shared_gate,
+                                         const gdsllm_affine_experts* shared_up,
+                                         const gdsllm_affine_experts* shared_down, const void* x, const int32_t* idx,
+                                         const void* routing_weights, int64_t top_k, const void* shared_gate_weight,
+                                         void* y, void* workspace, size_t workspace_bytes, void* stream) {
+    return moe_step_impl("moe_step_affine_q4", gate, up, down, shared_gate, shared_up, shared_down, x, idx,
+                         routing_weights, top_k, shared_gate_weight, y, workspace, workspace_bytes, stream, nullptr);
+}
+
+extern "C" size_t gdsllm_moe_step_routed_workspace_size(int64_t top_k, int64_t ffn_dim, int64_t num_experts) {
+    const size_t logits = num_experts > 0 ? static_cast<size_t>(num_experts) * 2 : 0;
+    return gdsllm_moe_step_workspace_size(top_k, ffn_dim) + (logits + 255) / 256 * 256;
+}
+
+extern "C" int gdsllm_moe_step_routed_affine_q4(const void* router_weight, const gdsllm_affine_experts* gate,
+                                                const gdsllm_affine_experts* up, const gdsllm_affine_experts* down,
+                                                const gdsllm_affine_experts* shared_gate,
+                                                const gdsllm_affine_experts* shared_up,
+                                                const gdsllm_affine_experts* shared_down, const void* x,
+                                                int64_t top_k, const void* shared_gate_weight, void* y,
+                                                int32_t* idx_out, void* weights_out, void* workspace,
+                                                size_t workspace_bytes, void* stream) {
+    const std::string n = "moe_step_routed_affine_q4";
+    if (!gate) return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": gate is null");
+    const int64_t E = gate->num_experts, H = gate->in_dim, F = gate->out_dim;
+    if (!router_weight || !idx_out || !weights_out || !workspace || !x)
+        return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": null pointer");
+    if (top_k < 1 || top_k > 63 || top_k > E)
+        return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": top_k must be in [1, min(63, num_experts)]");
+    if (E > kRouteMaxExperts || E % 8 != 0 || H % 8 != 0)
+        return set_error(GDSLLM_ERR_UNSUPPORTED,
+                         n + ": routing inside the step takes num_experts <= 512, a multiple of 8, and hidden % 8 == 0");
+    if (reinterpret_cast<uintptr_t>(router_weight) % 16 || reinterpret_cast<uintptr_t>(x) % 16 ||
+        reinterpret_cast<uintptr_t>(idx_out) % 4 || reinterpret_cast<uintptr_t>(weights_out) % 2)
+        return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": misaligned pointer");
+    const size_t step_ws = gdsllm_moe_step_workspace_size(top_k, F);
+    if (workspace_bytes < gdsllm_moe_step_routed_workspace_size(top_k, F, E))
+        return set_error(GDSLLM_ERR_INVALID_ARGUMENT,
+                         n + ": workspace too small (" + std::to_string(workspace_bytes) + " < " +
+                             std::to_string(gdsllm_moe_step_routed_workspace_size(top_k, F, E)) + ")");
+    auto* logits = reinterpret_cast<uint16_t*>(static_cast<uint8_t*>(workspace) + step_ws);
+    const RouteArgs ra{logits, static_cast<int>(E), idx_out, static_cast<uint16_t*>(weights_out)};
+    // every check of the step before the first launch
+    if (int rc = moe_step_impl(n, gate, up, down, shared_gate, shared_up, shared_down, x, idx_out, weights_out, top_k,
+                               shared_gate_weight, y, workspace, step_ws, stream, &ra, /*dry_run=*/true))
+        return rc;
+    // router logits: the fp16 GEMV that moe_route runs (gdsllm_gemv_f16), same bits
+    if (int rc = gdsllm_gemv_f16(router_weight, x, logits, E, H, 1, H, E, stream)) return rc;
+    return moe_step_impl(n, gate, up, down, shared_gate, shared_up, shared_down, x, idx_out, weights_out, top_k,
+                         shared_gate_weight, y, workspace, step_ws, stream, &ra);
 }

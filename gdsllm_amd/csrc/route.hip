@@ -19,6 +19,7 @@
 #include <algorithm>
 
 #include "common.h"
+#include "topk.h"
 
 namespace gdsllm {
 namespace {
@@ -136,42 +137,8 @@ __global__ __launch_bounds__(kF16Waves * 64) void gemv_f16_scalar(const uint16_t
     }
 }
 
-// Pick word of logit e: a 16-bit order key of the fp16 value above a 16-bit
-// inverted index, so the largest word is the largest logit and, among equal
-// logits, the lowest index.  The key is monotone in the value (negative
-// encodings inverted, positive ones offset above them), -0 and +0 share a key
-// (torch.topk sees them as equal) and every NaN ranks above +inf.  The
-// smallest key, -inf's, is 0x03FF, so a word of 0 never occurs: it marks a
-// logit already taken.
-__device__ __forceinline__ uint32_t pick_word(uint32_t h, int e) {
-    const uint32_t mag = h & 0x7FFFu;
-    uint32_t key = (h & 0x8000u) ? (~h & 0xFFFFu) : (h | 0x8000u);
-    key = mag == 0 ? 0x8000u : key;         // +-0
-    key = mag > 0x7C00u ? 0xFFFFu : key;    // NaN
-    return (key << 16) | (0xFFFFu - static_cast<uint32_t>(e));
-}
-
-template <int CTRL>
-__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
-    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, false));
-}
-// Maximum over the wave, returned wave-uniform: DPP within each 16-lane row
-// (quad xor 1, quad xor 2, half-row mirror, row mirror), then the four row
-// maxima through readlane.
-__device__ __forceinline__ uint32_t wave_max(uint32_t v) {
-    v = max(v, dpp_u32<0xB1>(v));
-    v = max(v, dpp_u32<0x4E>(v));
-    v = max(v, dpp_u32<0x141>(v));
-    v = max(v, dpp_u32<0x140>(v));
-    const uint32_t r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16);
-    const uint32_t r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
-    return max(max(r0, r1), max(r2, r3));
-}
-
 // Top-k of one token by one wave.  NPL pick words per lane live in registers
-// (logit lane + 64*j), NPL * 64 >= E; k rounds of a wave-wide max take the
-// next pick and its owner clears it.  The softmax of the picks is in fp32,
-// summed in pick order: exp(l - max) / sum, rounded to fp16.
+// (logit lane + 64*j), NPL * 64 >= E (topk.h).
 template <int NPL>
 __device__ __forceinline__ void topk_wave(const uint16_t* __restrict__ L, int E, int k, int32_t* __restrict__ idx,
                                           uint16_t* __restrict__ wts, int lane) {
@@ -182,36 +149,13 @@ __device__ __forceinline__ void topk_wave(const uint16_t* __restrict__ L, int E,
     for (int j = 0; j < NPL; ++j) h[j] = L[lane + 64 * j < E ? lane + 64 * j : 0];
 #pragma unroll
     for (int j = 0; j < NPL; ++j) word[j] = lane + 64 * j < E ? pick_word(h[j], lane + 64 * j) : 0u;
-    // Each round's pick is wave-uniform and lane i keeps pick i; only the
-    // selection is serial.  Afterwards each lane decodes its pick's value
-    // (+-0 -> +0, NaN -> NaN, both softmax-neutral) and takes exp(l - max)
-    // itself, and the exponentials are summed in pick order.
-    int my_idx = 0;
-    uint32_t my_key = 0, top_key = 0;
-    for (int i = 0; i < k; ++i) {
-        uint32_t best = 0;
-#pragma unroll
-        for (int j = 0; j < NPL; ++j) best = word[j] > best ? word[j] : best;
-        best = wave_max(best);
-#pragma unroll
-        for (int j = 0; j < NPL; ++j) word[j] = word[j] == best ? 0u : word[j];
-        if (i == 0) top_key = best >> 16;
-        if (lane == i) {
-            my_idx = static_cast<int>(0xFFFFu - (best & 0xFFFFu));
-            my_key = best >> 16;
-        }
-    }
-    auto key_value = [](uint32_t key) {
-        return key == 0xFFFFu ? __builtin_nanf("") : h2f((key & 0x8000u) ? (key & 0x7FFFu) : (~key & 0xFFFFu));
-    };
-    const float m = key_value(top_key);
-    const float my_ex = lane < k ? expf(fp32_rounded(key_value(my_key) - m)) : 0.f;
-    float sum = 0.f;
-    for (int i = 0; i < k; ++i)
-        sum = fp32_rounded(sum + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_ex), i)));
+    int my_idx;
+    uint32_t my_key, top_key;
+    topk_select<NPL>(word, k, lane, my_idx, my_key, top_key);
+    const uint16_t w = topk_weight(my_key, top_key, k, lane);
     if (lane < k) {
         idx[lane] = my_idx;
-        wts[lane] = f2h_bits(fp32_rounded(my_ex / sum));
+        wts[lane] = w;
     }
 }
 

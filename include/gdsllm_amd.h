@@ -234,6 +234,25 @@ int gdsllm_moe_step_affine_q4(const gdsllm_affine_experts* gate, const gdsllm_af
                               const void* x, const int32_t* idx, const void* routing_weights, int64_t top_k,
                               const void* shared_gate_weight, void* y, void* workspace, size_t workspace_bytes,
                               void* stream);
+/* The same step with the routing of qwen_moe.py:386-416 folded in, in three
+ * launches: the fp16 router GEMV (gdsllm_gemv_f16 on router_weight
+ * [num_experts][H], logits into the workspace), then the gate/up launch, each
+ * of whose waves takes the top_k picks of those logits itself (the selection
+ * and fp16 softmax of gdsllm_moe_route_topk, bit for bit), then the down launch.
+ * idx_out (int32 [top_k]) and weights_out (fp16 [top_k]) receive the picks in
+ * descending order and their weights, as moe_route returns them.  No
+ * counterpart in the reference (moe_route followed by moe_mlp_selective).
+ * num_experts = gate->num_experts <= 512 and a multiple of 8, router_weight
+ * and x on the 16-byte grid (else GDSLLM_ERR_UNSUPPORTED or
+ * GDSLLM_ERR_INVALID_ARGUMENT); workspace_bytes >=
+ * gdsllm_moe_step_routed_workspace_size(top_k, F, num_experts).             */
+size_t gdsllm_moe_step_routed_workspace_size(int64_t top_k, int64_t ffn_dim, int64_t num_experts);
+int gdsllm_moe_step_routed_affine_q4(const void* router_weight, const gdsllm_affine_experts* gate,
+                                     const gdsllm_affine_experts* up, const gdsllm_affine_experts* down,
+                                     const gdsllm_affine_experts* shared_gate, const gdsllm_affine_experts* shared_up,
+                                     const gdsllm_affine_experts* shared_down, const void* x, int64_t top_k,
+                                     const void* shared_gate_weight, void* y, int32_t* idx_out, void* weights_out,
+                                     void* workspace, size_t workspace_bytes, void* stream);
 
 /* --------------------------------------- on-device MoE routing, epilogue --
  * The reference routes on the host side of a sync (F.linear, torch.topk,

@@ -223,6 +223,37 @@ def test_moe_step_validation():
     assert call(k=32, wsb=lib.gdsllm_moe_step_workspace_size(32, F)) == 2  # 33 slots, 4 per lane group: > 8
 
 
+def test_moe_step_routed_validation():
+    """The routed step checks the router arguments and every step argument
+    before it launches anything: each call below fails validation."""
+    lib = capi()
+    H, F, E = 2048, 512, 64
+    gate, up, down = _experts(E=E, N=F, K=H), _experts(E=E, N=F, K=H), _experts(E=E, N=H, K=F)
+    sg, su, sd = _experts(E=1, N=F, K=H), _experts(E=1, N=F, K=H), _experts(E=1, N=H, K=F)
+    ws = lib.gdsllm_moe_step_routed_workspace_size(4, F, E)
+    assert ws >= lib.gdsllm_moe_step_workspace_size(4, F) + 2 * E
+
+    def call(router=16, g=gate, u=up, d=down, a=sg, b=su, c=sd, k=4, wsb=ws, sgw=16, x=16, idx=16, w=16):
+        return lib.gdsllm_moe_step_routed_affine_q4(router, *(ctypes.byref(e) for e in (g, u, d, a, b, c)), x, k, sgw,
+                                                    16, idx, w, 16, wsb, None)
+
+    assert call(router=None) == 1 and "null" in _err()
+    assert call(idx=None) == 1 and "null" in _err()
+    assert call(k=0) == 1 and "top_k" in _err()
+    assert call(k=65) == 1 and "top_k" in _err()
+    assert call(router=8) == 1 and "misaligned" in _err()
+    assert call(idx=18) == 1 and "misaligned" in _err()
+    assert call(wsb=ws - 256) == 1 and "workspace" in _err()
+    odd = dict(g=_experts(E=60, N=F, K=H), u=_experts(E=60, N=F, K=H), d=_experts(E=60, N=H, K=F))
+    assert call(**odd, wsb=lib.gdsllm_moe_step_routed_workspace_size(4, F, 60)) == 2 and "512" in _err()
+    big = dict(g=_experts(E=1024, N=F, K=H), u=_experts(E=1024, N=F, K=H), d=_experts(E=1024, N=H, K=F))
+    assert call(**big, wsb=lib.gdsllm_moe_step_routed_workspace_size(4, F, 1024)) == 2
+    # step checks, before the router GEMV is launched
+    assert call(d=_experts(E=E, N=F, K=H)) == 1 and "disagree" in _err()
+    assert call(sgw=None) == 1 and "null" in _err()
+    assert call(k=32, wsb=lib.gdsllm_moe_step_routed_workspace_size(32, F, E)) == 2  # 33 slots: separate launches
+
+
 @pytest.mark.parametrize("name", ["gdsllm_embed_q4_0", "gdsllm_embed_q8_0"])
 def test_embed_validation(name):
     fn = getattr(capi(), name)

@@ -146,3 +146,58 @@ def test_moe_step_two_calls_share_nothing(gpu):
         outs.append((y, _separate(routed, shared, x, idx, w, sgw, g, gpu)))
     for y, want in outs:
         np.testing.assert_array_equal(to_np(y).view(np.uint16), to_np(want).view(np.uint16))
+
+
+def _routed_step(router, routed, shared, x, sgw, g, top_k, gpu):
+    structs = [experts_struct(*p, g) for p in routed + shared]
+    E, F = structs[0].num_experts, structs[0].out_dim
+    ws_bytes = capi().gdsllm_moe_step_routed_workspace_size(top_k, F, E)
+    ws = torch.full((ws_bytes,), 0xFF, dtype=torch.uint8, device=gpu)
+    y = torch.empty(structs[2].out_dim, dtype=torch.float16, device=gpu)
+    idx = torch.full((top_k,), -7, dtype=torch.int32, device=gpu)
+    w = torch.full((top_k,), float("nan"), dtype=torch.float16, device=gpu)
+    check(capi().gdsllm_moe_step_routed_affine_q4(ptr(router), *(ctypes.byref(s) for s in structs), ptr(x), top_k,
+                                                  ptr(sgw), ptr(y), ptr(idx), ptr(w), ptr(ws), ws_bytes, stream()))
+    torch.cuda.synchronize()
+    return y, idx, w
+
+
+# (E, H, F, top_k, ties): the cfg2 layer (512 experts, top-10), small pools,
+# and routers whose top logits tie (equal rows: the lower expert index first)
+ROUTED_CASES = [(512, 4096, 1024, 10, False), (64, 2048, 512, 4, False), (8, 2048, 512, 1, False),
+                (128, 4096, 512, 8, True), (512, 2048, 512, 31, True)]
+
+
+@pytest.mark.parametrize("E,H,F,k,ties", ROUTED_CASES)
+def test_moe_step_routed_matches_route_then_step(gpu, E, H, F, k, ties):
+    """The routed step (router GEMV, then the gate/up launch taking the top-k
+    itself, then down) gives the picks and weights of gemv_f16 +
+    moe_route_topk and the output of the fused step on them, bit for bit."""
+    g = 64
+    gg = gen(9700 + E + H + F + k)
+    routed = [_dev(syn.affine_q4_weights(s, g, gg), gpu) for s in ([E, F, H], [E, F, H], [E, H, F])]
+    shared = [_dev(_shared_stacked(syn.affine_q4_weights(s, g, gg)), gpu) for s in ([F, H], [F, H], [H, F])]
+    x = syn.activations(1, H, gen(9800 + k)).to(gpu)
+    router = (torch.randn(E, H, generator=gen(9900 + k)) * 0.02).to(torch.float16)
+    if ties:
+        hot = _gate_row(x.cpu(), 8.0)
+        for e in (E - 1, 5, 2, E // 2):  # equal top logits at four experts
+            router[e] = hot
+    router = router.to(gpu)
+    sgw = (torch.randn(H, generator=gen(9950 + k)) * 0.02).to(torch.float16).to(gpu)
+
+    y, idx, w = _routed_step(router, routed, shared, x, sgw, g, k, gpu)
+
+    logits = torch.empty(E, dtype=torch.float16, device=gpu)
+    check(capi().gdsllm_gemv_f16(ptr(router), ptr(x), ptr(logits), E, H, 1, H, E, stream()))
+    ridx = torch.empty(k, dtype=torch.int32, device=gpu)
+    rw = torch.empty(k, dtype=torch.float16, device=gpu)
+    check(capi().gdsllm_moe_route_topk(ptr(logits), E, 1, E, k, ptr(ridx), ptr(rw), stream()))
+    torch.cuda.synchronize()
+    want = _step(routed, shared, x, ridx, rw, sgw, g, k, gpu)
+    assert torch.equal(idx, ridx), f"picks {idx.tolist()} != {ridx.tolist()}"
+    assert torch.equal(w.view(torch.int16), rw.view(torch.int16))
+    if ties:
+        top = sorted((E - 1, 5, 2, E // 2))[:min(k, 4)]
+        assert idx[:len(top)].tolist() == top, "equal logits must come out lowest index first"
+    np.testing.assert_array_equal(to_np(y).view(np.uint16), to_np(want).view(np.uint16))

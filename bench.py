@@ -590,6 +590,24 @@ def bench_prefill(dev, layers, lm_head, tokens: int = 512, reps: int = 3):
     ms = _replay_ms(run, reps, warm=1)
     flops = 2 * tokens * (N_LAYERS * sum(m * k for m, k in LAYER_SHAPES) + LM_HEAD[0] * LM_HEAD[1])
 
+    # The same chunk with each layer's gate and up projections and the SiLU in
+    # one launch (gdsllm_dequant_gemm_gate_up_silu_q4_0) writing h, the down
+    # projection's input: 6 launches per layer, the MLP's real data flow.
+    h = torch.empty(tokens, 11008, dtype=torch.float16, device=dev)
+
+    def run_fused_mlp():
+        st = torch.cuda.current_stream().cuda_stream
+        for lw in layers:
+            for w, (m, k) in zip(lw[:4], LAYER_SHAPES[:4]):
+                gemm(w, m, k)
+            check(capi().gdsllm_dequant_gemm_gate_up_silu_q4_0(lw[4].data_ptr(), lw[5].data_ptr(), xs[4096].data_ptr(),
+                                                                h.data_ptr(), 11008, 4096, tokens, 4096, 11008, st))
+            check(capi().gdsllm_dequant_gemm_q4_0(lw[6].data_ptr(), h.data_ptr(), ys[4096].data_ptr(), 4096, 11008,
+                                                  tokens, 11008, 4096, st))
+        gemm(lm_head, *LM_HEAD)
+
+    ms_fused = _replay_ms(run_fused_mlp, reps, warm=1)
+
     # Per shape: the fused kernel against the reference's route, the bit-exact
     # dequant into an fp16 scratch matrix followed by the vendor GEMM
     # (hipBLASLt through torch.mm), runtime/llama.py:160-166.
@@ -621,9 +639,39 @@ def bench_prefill(dev, layers, lm_head, tokens: int = 512, reps: int = 3):
                                  "dequant_then_hipblaslt_us": round(r_us, 2), "dequant_us": round(d_us, 2),
                                  "hipblaslt_fp16_gemm_us": round(mm_us, 2), "fused_faster": bool(f_us < r_us)}
         del wdq, yr
+    # The MLP input of a layer: gate and up projections and h = silu(g) * u.
+    # Fused: one launch.  The reference's route: both projections as dequant +
+    # vendor GEMM, then torch's F.silu and product on the fp16 outputs.
+    m, k = LAYER_SHAPES[4]
+    wg_, wu_ = layers[0][4], layers[0][5]
+    wdq = torch.empty(m, k, dtype=torch.float16, device=dev)
+    g_, u_ = (torch.empty(tokens, m, dtype=torch.float16, device=dev) for _ in range(2))
+
+    def gate_up_fused():
+        check(lib.gdsllm_dequant_gemm_gate_up_silu_q4_0(wg_.data_ptr(), wu_.data_ptr(), xs[k].data_ptr(), h.data_ptr(),
+                                                        m, k, tokens, k, m, torch.cuda.current_stream().cuda_stream))
+
+    def gate_up_route():
+        for w, out in ((wg_, g_), (wu_, u_)):
+            check(lib.gdsllm_dequant_q4_0(w.data_ptr(), wdq.data_ptr(), m * k // 32,
+                                          torch.cuda.current_stream().cuda_stream))
+            torch.mm(xs[k], wdq.t(), out=out)
+        torch.nn.functional.silu(g_).mul_(u_)
+
+    f_us, r_us = (_replay_ms(fn, 20) * 1e3 for fn in (gate_up_fused, gate_up_route))
+    fl = 2 * 2 * tokens * m * k
+    per_shape[f"gate_up_silu_{m}x{k}"] = {"fused_us": round(f_us, 2), "fused_TFLOP_s": round(fl / (f_us * 1e-6) / 1e12, 1),
+                                          "dequant_then_hipblaslt_silu_us": round(r_us, 2),
+                                          "fused_faster": bool(f_us < r_us)}
+    del wdq, g_, u_
     return {"ms_per_chunk": round(ms, 3), "tokens": tokens, "tok_s": round(tokens / (ms * 1e-3), 1),
             "TFLOP_s": round(flops / (ms * 1e-3) / 1e12, 1), "flop_per_chunk": flops,
-            "pct_of_fp16_dense_peak": round(flops / (ms * 1e-3) / 1e12 / 25, 1), "per_shape": per_shape}
+            "pct_of_fp16_dense_peak": round(flops / (ms * 1e-3) / 1e12 / 25, 1), "launches_per_layer": 7,
+            "fused_gate_up_silu": {"ms_per_chunk": round(ms_fused, 3), "tok_s": round(tokens / (ms_fused * 1e-3), 1),
+                                   "TFLOP_s": round(flops / (ms_fused * 1e-3) / 1e12, 1),
+                                   "pct_of_fp16_dense_peak": round(flops / (ms_fused * 1e-3) / 1e12 / 25, 1),
+                                   "launches_per_layer": 6, "writes": "h = silu(gate x) * (up x), as the MLP uses it"},
+            "per_shape": per_shape}
 
 
 def bench_prefill_formats(dev, tokens: int = 512, reps: int = 20):

@@ -63,6 +63,8 @@ SIGNATURES = {
     "gdsllm_dequant_gemm_q4_0": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp]),
     "gdsllm_dequant_gemm_q8_0": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp]),
     "gdsllm_dequant_gemm_affine_q4": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp]),
+    "gdsllm_dequant_gemm_gate_up_silu_q4_0": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp]),
+    "gdsllm_dequant_gemm_gate_up_silu_q8_0": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp]),
     "gdsllm_moe_prefill_workspace_size": (ctypes.c_size_t, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64]),
     "gdsllm_moe_prefill_affine_q4": (ctypes.c_int, [ctypes.POINTER(AffineExperts)] * 3 + [_c_vp, _c_i64, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, ctypes.c_size_t, _c_vp]),
     "gdsllm_gemv_f16": (ctypes.c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp]),

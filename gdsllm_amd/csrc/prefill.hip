@@ -50,6 +50,10 @@
 //  * kGather  the tile list of the MoE prefill: tile (expert e, position p0,
 //             count n) multiplies the X rows tok[p0 .. p0+n-1] by expert e's
 //             matrix (stacked pool, e * stride) into Y rows p0 .. p0+n-1.
+//  * kDenseDual kDense with the gate/up split of kDualSilu: workgroup rows
+//             0..63 from the gate matrix and 64..127 from the up matrix at the
+//             same 64 output rows, h written instead of g and u (the prefill
+//             form of the decode gate_up_silu, runtime/llama.py:253-256).
 //  * kDualSilu  kGather with rows 0..63 of the workgroup taken from the gate
 //             pool and rows 64..127 from the up pool at the same 64 output
 //             rows; the epilogue writes h = fp16(fp16(silu(g)) * u) with
@@ -64,7 +68,7 @@ namespace gdsllm {
 namespace {
 
 enum class WF { Q4_0, Q8_0, AFF32, AFF64, AFF128 };
-enum Mode { kDense = 0, kGather = 1, kDualSilu = 2 };
+enum Mode { kDense = 0, kGather = 1, kDualSilu = 2, kDenseDual = 3 };
 
 constexpr int kWaves = 8;
 constexpr int kBM = 128;     // weight rows per workgroup
@@ -156,9 +160,9 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_sk(GemmArgs a) {
     constexpr int NX = BT / 32;         // X transfers per wave per stage
     constexpr int SPS = Fm::SPS, XR = R::XR, RW = R::RW, CW = Fm::kCW;
     constexpr int kXSlot = R::kXSlot;
-    constexpr bool kGath = MODE != kDense;
-    constexpr bool kDual = MODE == kDualSilu;
-    static_assert(!kDual || Fm::kAff, "dual gate/up tiles are built for the affine pools");
+    constexpr bool kGath = MODE == kGather || MODE == kDualSilu;
+    constexpr bool kDual = MODE == kDualSilu || MODE == kDenseDual;
+    static_assert(MODE != kDualSilu || Fm::kAff, "the gathered dual tiles are built for the affine pools");
 
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int tid = threadIdx.x;
@@ -190,7 +194,7 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_sk(GemmArgs a) {
         const int nwg = gridDim.x, b = blockIdx.x;
         const int per = nwg >> 3, rem = nwg & 7, xcd = b & 7;
         const int q = xcd * per + (xcd < rem ? xcd : rem) + (b >> 3);
-        m0 = (q % a.mtiles) * kBM;
+        m0 = (q % a.mtiles) * (kDual ? 64 : kBM);
         t0 = (q / a.mtiles) * BT;
         nt = min(BT, a.T - t0);
     }
@@ -631,6 +635,33 @@ int dense_gemm_auto(const GemmArgs& a, hipStream_t stream) {
     return tiles128 >= cu_count() ? dense_gemm<F, 128>(a, stream) : dense_gemm<F, 64>(a, stream);
 }
 
+// Gate/up/SiLU over token chunks: 64 output rows per workgroup (gate rows in
+// one half, up rows in the other), the 128-token tile when it fills every CU.
+template <WF F, int BT>
+int dense_dual_gemm(GemmArgs a, hipStream_t stream) {
+    const int64_t mtiles = (a.M + 63) / 64;
+    a.mtiles = static_cast<int>(mtiles);
+    const int64_t tchunk = std::max<int64_t>(1, (int64_t(1) << 30) / mtiles) * BT;
+    const int T = a.T;
+    const uint16_t* x0 = a.x;
+    uint16_t* y0 = a.y;
+    for (int64_t t = 0; t < T; t += tchunk) {
+        const int tc = static_cast<int>(std::min<int64_t>(T - t, tchunk));
+        a.x = x0 + t * a.ldx;
+        a.y = y0 + t * a.ldy;
+        a.T = tc;
+        const unsigned nwg = static_cast<unsigned>(mtiles * ((tc + BT - 1) / BT));
+        if (int rc = launch_sk<F, BT, kDenseDual>(a, nwg, stream)) return rc;
+    }
+    return GDSLLM_OK;
+}
+
+template <WF F>
+int dense_dual_gemm_auto(const GemmArgs& a, hipStream_t stream) {
+    const int64_t tiles128 = (a.M + 63) / 64 * ((a.T + 127) / 128);
+    return tiles128 >= cu_count() ? dense_dual_gemm<F, 128>(a, stream) : dense_dual_gemm<F, 64>(a, stream);
+}
+
 // ------------------------------------------------------------ MoE prefill --
 //
 // moe_sort (one workgroup): the T*k routed (token, slot) entries sorted by
@@ -1000,4 +1031,44 @@ extern "C" int gdsllm_moe_prefill_affine_q4(const gdsllm_affine_experts* gate, c
         default: rc = moe_prefill_run<WF::AFF128>(*gate, *up, *down, x, ldx, idx, routing_weights, tokens, top_k, y, ldy, ws, s); break;
     }
     return rc == GDSLLM_OK ? ok() : rc;
+}
+
+namespace {
+template <WF F>
+int gate_up_silu_entry(const std::string& n, const void* gate, const void* up, const void* x, void* h,
+                       int64_t ffn_dim, int64_t in_dim, int64_t tokens, int64_t ldx, int64_t ldh, void* stream) {
+    bool empty;
+    if (int rc = check_dense(n, gate, x, h, ffn_dim, in_dim, tokens, ldx, ldh, empty)) return rc;
+    if (empty) return ok();
+    if (!up) return set_error(GDSLLM_ERR_INVALID_ARGUMENT, n + ": null pointer");
+    if (reinterpret_cast<uintptr_t>(up) % 16)
+        return set_error(GDSLLM_ERR_UNSUPPORTED, n + ": weight and x rows must be 16-byte aligned (ldx % 8 == 0)");
+    if (in_dim % 256 != 0) return off_grid(n, in_dim);
+    GemmArgs a{};
+    a.w = static_cast<const uint8_t*>(gate);
+    a.w2 = static_cast<const uint8_t*>(up);
+    a.x = static_cast<const uint16_t*>(x);
+    a.y = static_cast<uint16_t*>(h);
+    a.M = static_cast<int>(ffn_dim);
+    a.K = static_cast<int>(in_dim);
+    a.T = static_cast<int>(tokens);
+    a.ldx = ldx;
+    a.ldy = ldh;
+    const int rc = dense_dual_gemm_auto<F>(a, as_stream(stream));
+    return rc == GDSLLM_OK ? ok() : rc;
+}
+}  // namespace
+
+extern "C" int gdsllm_dequant_gemm_gate_up_silu_q4_0(const void* gate_weight, const void* up_weight, const void* x,
+                                                     void* h, int64_t ffn_dim, int64_t in_dim, int64_t tokens,
+                                                     int64_t ldx, int64_t ldh, void* stream) {
+    return gate_up_silu_entry<WF::Q4_0>("dequant_gemm_gate_up_silu_q4_0", gate_weight, up_weight, x, h, ffn_dim,
+                                        in_dim, tokens, ldx, ldh, stream);
+}
+
+extern "C" int gdsllm_dequant_gemm_gate_up_silu_q8_0(const void* gate_weight, const void* up_weight, const void* x,
+                                                     void* h, int64_t ffn_dim, int64_t in_dim, int64_t tokens,
+                                                     int64_t ldx, int64_t ldh, void* stream) {
+    return gate_up_silu_entry<WF::Q8_0>("dequant_gemm_gate_up_silu_q8_0", gate_weight, up_weight, x, h, ffn_dim,
+                                        in_dim, tokens, ldx, ldh, stream);
 }

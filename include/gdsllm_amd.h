@@ -316,6 +316,20 @@ int gdsllm_dequant_gemm_affine_q4(const void* weight, const void* scales, const 
                                   const void* x, void* y, int64_t out_dim, int64_t in_dim,
                                   int64_t group_size, int64_t tokens, int64_t ldx, int64_t ldy,
                                   void* stream);
+/* The MLP input of a prefill chunk in one launch: h[t][r] =
+ * fp16(fp16(silu(g)) * u) with g = fp16(sum_k x[t][k] * gate[r][k]) and u
+ * likewise for up (GGUF Q4_0 / Q8_0 [ffn_dim][in_dim], the bits
+ * gdsllm_dequant_gemm_* gives for each), torch's fp16 SiLU and product.
+ * Replaces the reference's two prefill projections and its elementwise SiLU
+ * (runtime/llama.py:253-256 over dequant_linear, llama.py:160-166); the
+ * prefill form of gdsllm_fused_*_gate_up_silu.  in_dim % 256 == 0, weights
+ * and x on the 16-byte grid, ldx % 8 == 0 (else GDSLLM_ERR_UNSUPPORTED).     */
+int gdsllm_dequant_gemm_gate_up_silu_q4_0(const void* gate_weight, const void* up_weight, const void* x,
+                                          void* h, int64_t ffn_dim, int64_t in_dim, int64_t tokens,
+                                          int64_t ldx, int64_t ldh, void* stream);
+int gdsllm_dequant_gemm_gate_up_silu_q8_0(const void* gate_weight, const void* up_weight, const void* x,
+                                          void* h, int64_t ffn_dim, int64_t in_dim, int64_t tokens,
+                                          int64_t ldx, int64_t ldh, void* stream);
 
 /* Bytes of device workspace gdsllm_moe_prefill_affine_q4 needs. */
 size_t gdsllm_moe_prefill_workspace_size(int64_t tokens, int64_t top_k, int64_t ffn_dim,

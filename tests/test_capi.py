@@ -223,6 +223,19 @@ def test_moe_step_validation():
     assert call(k=32, wsb=lib.gdsllm_moe_step_workspace_size(32, F)) == 2  # 33 slots, 4 per lane group: > 8
 
 
+@pytest.mark.parametrize("name", ["gdsllm_dequant_gemm_gate_up_silu_q4_0", "gdsllm_dequant_gemm_gate_up_silu_q8_0"])
+def test_gate_up_silu_gemm_validation(name):
+    """Every call fails validation before any launch."""
+    fn = getattr(capi(), name)
+    assert fn(16, 16, 16, 16, 64, 100, 8, 100, 64, None) == 1 and "multiple of 32" in _err()
+    assert fn(16, 16, 16, 16, -1, 256, 8, 256, 64, None) == 1 and "negative" in _err()
+    assert fn(16, 16, 16, 16, 0, 256, 8, 256, 64, None) == 0  # empty: nothing to do
+    assert fn(16, None, 16, 16, 64, 256, 8, 256, 64, None) == 1 and "null" in _err()
+    assert fn(16, 24, 16, 16, 64, 256, 8, 256, 64, None) == 2 and "aligned" in _err()
+    assert fn(16, 16, 16, 16, 64, 96, 8, 96, 64, None) == 2 and "256" in _err()
+    assert fn(16, 16, 16, 16, 64, 256, 8, 200, 64, None) == 1 and "ldx" in _err()
+
+
 def test_moe_step_routed_validation():
     """The routed step checks the router arguments and every step argument
     before it launches anything: each call below fails validation."""

@@ -330,3 +330,48 @@ def test_runtime_q8_0_prefill_projection(gpu):
     torch.cuda.synchronize()
     assert y.shape == (2, T // 2, M)
     assert_gemv_close(to_np(y).reshape(T, M), oq.dequant_q8_0(to_np(w)).reshape(M, K), to_np(x), "q8_0 dequant_linear")
+
+
+# (fmt, T, F, K): the 7B gate/up shape at a 512-token chunk (128-token tiles)
+# and at 64 tokens (64-token tiles), ragged rows and tokens, a short K
+GATE_UP_CASES = [("q4_0", 512, 11008, 4096), ("q4_0", 64, 11008, 4096), ("q4_0", 7, 300, 256),
+                 ("q4_0", 100, 1000, 512), ("q8_0", 512, 11008, 4096), ("q8_0", 33, 260, 1024)]
+
+
+@pytest.mark.parametrize("fmt,T,F,K", GATE_UP_CASES, ids=[f"{f}_T{t}_{m}x{k}" for f, t, m, k in GATE_UP_CASES])
+def test_dequant_gemm_gate_up_silu(gpu, fmt, T, F, K):
+    """h = fp16(fp16(silu(g)) * u) for a prefill chunk in one launch.  (1)
+    Against g and u from the dense GEMM: within one fp16 ulp of silu times |u|
+    plus one ulp of h (the room the device's expf leaves against numpy's).
+    (2) End to end against the oracle's g and u: relative L2 of h."""
+    make = syn.q4_0_weights if fmt == "q4_0" else syn.q8_0_weights
+    dq = oq.dequant_q4_0 if fmt == "q4_0" else oq.dequant_q8_0
+    gemm = capi().gdsllm_dequant_gemm_q4_0 if fmt == "q4_0" else capi().gdsllm_dequant_gemm_q8_0
+    fused = (capi().gdsllm_dequant_gemm_gate_up_silu_q4_0 if fmt == "q4_0"
+             else capi().gdsllm_dequant_gemm_gate_up_silu_q8_0)
+    wg, wu = make(F, K, gen(5600 + F)), make(F, K, gen(5601 + K))
+    x = syn.activations(T, K, gen(5602 + T))
+    wgd, wud, xd = wg.to(gpu), wu.to(gpu), x.to(gpu)
+    h = torch.full((T, F), float("nan"), dtype=torch.float16, device=gpu)
+    check(fused(ptr(wgd), ptr(wud), ptr(xd), ptr(h), F, K, T, K, F, stream()))
+    g = torch.empty(T, F, dtype=torch.float16, device=gpu)
+    u = torch.empty(T, F, dtype=torch.float16, device=gpu)
+    check(gemm(ptr(wgd), ptr(xd), ptr(g), F, K, T, K, F, stream()))
+    check(gemm(ptr(wud), ptr(xd), ptr(u), F, K, T, K, F, stream()))
+    torch.cuda.synchronize()
+    hk = to_np(h).astype(np.float64)
+    assert np.all(np.isfinite(hk)), "h not written everywhere"
+    gn, un = to_np(g), to_np(u)
+    sg = oq.silu_fp16(gn)
+    href = (sg.astype(np.float32) * un.astype(np.float32)).astype(np.float16)
+    bound = oq.fp16_ulp(sg) * np.abs(un.astype(np.float64)) + oq.fp16_ulp(href)
+    bad = np.abs(hk - href.astype(np.float64)) > bound
+    assert not bad.any(), f"{int(bad.sum())} of {bad.size} h values off; first at {np.argwhere(bad)[0]}"
+    rows = np.arange(T) if T <= 64 else np.random.default_rng(T).choice(T, 64, replace=False)
+    xr = to_np(x)[rows]
+    gq = oq.gemv(dq(to_np(wg)).reshape(F, K), xr).astype(np.float16)
+    uq = oq.gemv(dq(to_np(wu)).reshape(F, K), xr).astype(np.float16)
+    h_oracle = (oq.silu_fp16(gq).astype(np.float32) * uq.astype(np.float32)).astype(np.float64)
+    rel = float(np.linalg.norm(hk[rows] - h_oracle) / np.linalg.norm(h_oracle))
+    print(f"gate_up_silu {fmt} T{T} {F}x{K}: rel L2 {rel:.2e}")
+    assert rel <= oq.GEMV_REL_L2, f"h end-to-end rel L2 {rel:.3e}"

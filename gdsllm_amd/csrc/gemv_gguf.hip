@@ -714,9 +714,9 @@ __device__ __forceinline__ void rows_pair_impl(const uint8_t* buf, const XSlice<
 // stage buffers, then raw x.  One buffer per wave: after rows 0-1 of a stage are consumed, the next
 // stage's transfers that land in their slots only (kEarly) are issued, the
 // rest after rows 2-3.
-template <Fmt F, int NB, int MODE>
-__global__ __launch_bounds__(kWaves * 64) void gguf_gemv_rows(const RowsTarget target, const uint16_t* __restrict__ X,
-                                                              int K, int64_t ldx) {
+template <Fmt F, int NB, int MODE, int WV = kWaves>
+__global__ __launch_bounds__(WV * 64) void gguf_gemv_rows(const RowsTarget target, const uint16_t* __restrict__ X,
+                                                          int K, int64_t ldx) {
     constexpr bool PAIRED = MODE == 2;
     using L = Layout<F>;
     constexpr int C = L::kSbChunks;                        // transfers per stage
@@ -731,13 +731,13 @@ __global__ __launch_bounds__(kWaves * 64) void gguf_gemv_rows(const RowsTarget t
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     uint8_t* buf = lds + wave * stage_bytes<F>();
-    uint8_t* xp = lds + kWaves * stage_bytes<F>();
+    uint8_t* xp = lds + WV * stage_bytes<F>();
     TargetRegs tg;
     tg.load<MODE>(target);
     const int RG = (tg.m + (PAIRED ? 1 : kRowsPerStage - 1)) / (PAIRED ? 2 : kRowsPerStage);
     const int NW = (S + kSbPerWindow - 1) / kSbPerWindow;
-    const int total_waves = tg.blocks * kWaves;
-    const int gw = (blockIdx.x - tg.first_block) * kWaves + wave;
+    const int total_waves = tg.blocks * WV;
+    const int gw = (blockIdx.x - tg.first_block) * WV + wave;
     const int my_rgs = gw < RG ? (RG - 1 - gw) / total_waves + 1 : 0;
     const int T = my_rgs * NW;
     const NibUnpack nu;
@@ -760,7 +760,7 @@ __global__ __launch_bounds__(kWaves * 64) void gguf_gemv_rows(const RowsTarget t
     // starts next to running ones leave ahead of their weight requests
     // (11008x4096 at batch 1: 7.006 against 7.038 us per call).
     __builtin_amdgcn_s_setprio(3);
-    rows_xraw_issue<NB>(xp, X, ldx, K, NW, wave, kWaves, lane);
+    rows_xraw_issue<NB>(xp, X, ldx, K, NW, wave, WV, lane);
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_s_setprio(0);
     rows_issue<F, 0, C, PAIRED>(buf, stage_at(0), X, row_bytes, goff, T > 0, lane);
@@ -1776,22 +1776,43 @@ int launch_staged(const void* w, const uint16_t* x, uint16_t* y, int M, int K, i
 // each.  Returns false when no geometry fits (the caller takes another kernel).
 // Sets tg.gb_end: workgroups per matrix, as many as its row groups need while
 // all fit at once, else the resident count shared in proportion to row groups.
+// Resident workgroups of the row-span kernel with WV waves (0: the LDS does
+// not fit), and sets the dynamic LDS size.
+template <Fmt F, int NB, int MODE, int WV>
+int rows_resident(int NW) {
+    const size_t lds = rows_lds_bytes<F, NB>(NW, WV);
+    if (lds > static_cast<size_t>(max_lds_bytes())) return 0;
+    const void* fn = reinterpret_cast<const void*>(&gguf_gemv_rows<F, NB, MODE, WV>);
+    if (prepare_lds(fn, lds) != GDSLLM_OK) return 0;
+    return blocks_per_cu(fn, lds, WV * 64) * cu_count();
+}
+
 template <Fmt F, int NB, int MODE>
-bool plan_rows(RowsTarget& tg, int K, int& grid) {
+bool plan_rows(RowsTarget& tg, int K, int& grid, int& wv) {
     constexpr bool PAIRED = MODE == 2;
     const int NW = ((K >> 8) + kSbPerWindow - 1) / kSbPerWindow;
-    const size_t lds = rows_lds_bytes<F, NB>(NW, kWaves);
-    if (lds > static_cast<size_t>(max_lds_bytes())) return false;
-    const void* fn = reinterpret_cast<const void*>(&gguf_gemv_rows<F, NB, MODE>);
-    if (prepare_lds(fn, lds) != GDSLLM_OK) return false;
-    const int resident = blocks_per_cu(fn, lds, kWaves * 64) * cu_count();
     const int parts = PAIRED ? 1 : tg.n;
-    int need[kMaxGroup], total = 0, rg_all = 0;
+    int rg_all = 0;
+    for (int i = 0; i < parts; ++i)
+        rg_all += PAIRED ? (tg.m[0] + 1) / 2 : (tg.m[i] + kRowsPerStage - 1) / kRowsPerStage;
+    // 4-wave workgroups, unless 8-wave ones keep more row groups in flight
+    // (single matrices whose x fills so much LDS that one 4-wave workgroup
+    // fits per CU: the 8192 x 28672 down projection of a 70B layer)
+    wv = kWaves;
+    int resident = rows_resident<F, NB, MODE, kWaves>(NW);
+    if constexpr (MODE == 0) {
+        const int r8 = rows_resident<F, NB, MODE, 8>(NW);
+        if (std::min(r8 * 8, rg_all) > std::min(resident * kWaves, rg_all)) {
+            wv = 8;
+            resident = r8;
+        }
+    }
+    if (resident == 0) return false;
+    int need[kMaxGroup], total = 0;
     for (int i = 0; i < parts; ++i) {
         const int rg = PAIRED ? (tg.m[0] + 1) / 2 : (tg.m[i] + kRowsPerStage - 1) / kRowsPerStage;
-        need[i] = (rg + kWaves - 1) / kWaves;
+        need[i] = (rg + wv - 1) / wv;
         total += need[i];
-        rg_all += rg;
     }
     grid = 0;
     for (int i = 0; i < parts; ++i) {
@@ -1809,9 +1830,15 @@ bool plan_rows(RowsTarget& tg, int K, int& grid) {
 }
 
 template <Fmt F, int NB, int MODE>
-int launch_rows(const RowsTarget& tg, const uint16_t* x, int K, int64_t ldx, int grid, hipStream_t stream) {
+int launch_rows(const RowsTarget& tg, const uint16_t* x, int K, int64_t ldx, int grid, int wv, hipStream_t stream) {
     const int NW = ((K >> 8) + kSbPerWindow - 1) / kSbPerWindow;
-    const size_t lds = rows_lds_bytes<F, NB>(NW, kWaves);
+    const size_t lds = rows_lds_bytes<F, NB>(NW, wv);
+    if constexpr (MODE == 0) {
+        if (wv == 8) {
+            hipLaunchKernelGGL((gguf_gemv_rows<F, NB, MODE, 8>), dim3(grid), dim3(8 * 64), lds, stream, tg, x, K, ldx);
+            return check_hip(hipGetLastError(), "gguf_gemv launch");
+        }
+    }
     hipLaunchKernelGGL((gguf_gemv_rows<F, NB, MODE>), dim3(grid), dim3(kWaves * 64), lds, stream, tg, x, K, ldx);
     return check_hip(hipGetLastError(), "gguf_gemv launch");
 }
@@ -1827,13 +1854,13 @@ int try_rows(RowsTarget tg, const void* x, int K, int64_t batch, int64_t ldx, hi
     const bool x_al16 = reinterpret_cast<uintptr_t>(x) % 16 == 0 && (ldx % 8 == 0 || batch == 1);
     if (batch > 2 || K % 256 != 0 || K > (1 << 20) || !w_al16 || !x_al16) return -1;
     const auto* xp = static_cast<const uint16_t*>(x);
-    int grid = 0;
+    int grid = 0, wv = kWaves;
     if (batch == 1) {
-        if (!plan_rows<F, 1, MODE>(tg, K, grid)) return -1;
-        return launch_rows<F, 1, MODE>(tg, xp, K, ldx, grid, s);
+        if (!plan_rows<F, 1, MODE>(tg, K, grid, wv)) return -1;
+        return launch_rows<F, 1, MODE>(tg, xp, K, ldx, grid, wv, s);
     }
-    if (!plan_rows<F, 2, MODE>(tg, K, grid)) return -1;
-    return launch_rows<F, 2, MODE>(tg, xp, K, ldx, grid, s);
+    if (!plan_rows<F, 2, MODE>(tg, K, grid, wv)) return -1;
+    return launch_rows<F, 2, MODE>(tg, xp, K, ldx, grid, wv, s);
 }
 
 RowsTarget single_target(const void* w, void* y, int M, int64_t ldy) {

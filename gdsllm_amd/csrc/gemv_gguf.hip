@@ -714,7 +714,14 @@ __device__ __forceinline__ void rows_pair_impl(const uint8_t* buf, const XSlice<
 // stage buffers, then raw x.  One buffer per wave: after rows 0-1 of a stage are consumed, the next
 // stage's transfers that land in their slots only (kEarly) are issued, the
 // rest after rows 2-3.
-template <Fmt F, int NB, int MODE, int WV = kWaves>
+//
+// SW (split windows, MODE 0, in_dim over NW >= 2 windows of 4096): wave w
+// takes window w % NW of row-group slot w / NW (WV = NW x slots), so the NW
+// stages of a row group stream at once from NW waves instead of one after
+// another from one.  Each stage's four row sums go to a partial area after
+// x, [stage t][wave][batch row][4]; after a workgroup barrier the window-0
+// waves add the NW partials of each row in window order and store y.
+template <Fmt F, int NB, int MODE, int WV = kWaves, bool SW = false>
 __global__ __launch_bounds__(WV * 64) void gguf_gemv_rows(const RowsTarget target, const uint16_t* __restrict__ X,
                                                           int K, int64_t ldx) {
     constexpr bool PAIRED = MODE == 2;
@@ -736,12 +743,22 @@ __global__ __launch_bounds__(WV * 64) void gguf_gemv_rows(const RowsTarget targe
     tg.load<MODE>(target);
     const int RG = (tg.m + (PAIRED ? 1 : kRowsPerStage - 1)) / (PAIRED ? 2 : kRowsPerStage);
     const int NW = (S + kSbPerWindow - 1) / kSbPerWindow;
-    const int total_waves = tg.blocks * WV;
-    const int gw = (blockIdx.x - tg.first_block) * WV + wave;
-    const int my_rgs = gw < RG ? (RG - 1 - gw) / total_waves + 1 : 0;
-    const int T = my_rgs * NW;
+    static_assert(!SW || MODE == 0, "split windows serve one matrix");
+    // plain: wave gw takes row groups gw, gw + total_waves, ..., each window
+    // in turn; SW: wave (slot, my_win) takes window my_win of row groups
+    // rg0, rg0 + total_slots, ...
+    const int R = SW ? WV / NW : 1;  // row-group slots per workgroup
+    const int my_win = SW ? wave % NW : 0;
+    const int total_waves = tg.blocks * WV, total_slots = tg.blocks * R;
+    const int gw = SW ? (blockIdx.x - tg.first_block) * R + wave / NW : (blockIdx.x - tg.first_block) * WV + wave;
+    const int my_rgs = gw < RG ? (RG - 1 - gw) / (SW ? total_slots : total_waves) + 1 : 0;
+    const int T = SW ? my_rgs : my_rgs * NW;
     const NibUnpack nu;
-    auto stage_at = [&](int t) { return rows_stage<F, PAIRED>(tg, gw + (t / NW) * total_waves, t % NW, S, row_bytes); };
+    auto stage_at = [&](int t) {
+        if constexpr (SW) return rows_stage<F, PAIRED>(tg, gw + t * total_slots, my_win, S, row_bytes);
+        else return rows_stage<F, PAIRED>(tg, gw + (t / NW) * total_waves, t % NW, S, row_bytes);
+    };
+    const uint32_t part0 = lds_addr(xp + rows_xraw_bytes(NB, NW));  // SW: the partial row sums
 
     uint32_t goff[C];
 #pragma unroll
@@ -768,8 +785,8 @@ __global__ __launch_bounds__(WV * 64) void gguf_gemv_rows(const RowsTarget targe
     lds_barrier();  // every wave's share of x has landed
 
     XSlice<NB> xs;
-    if (T > 0) load_slice<F, NB>(xs, xp, NW, 0, K, lane);
-    int xwin = 0;
+    if (T > 0) load_slice<F, NB>(xs, xp, NW, my_win, K, lane);
+    int xwin = my_win;
     float acc[NB][4];
 #pragma unroll
     for (int b = 0; b < NB; ++b)
@@ -777,7 +794,7 @@ __global__ __launch_bounds__(WV * 64) void gguf_gemv_rows(const RowsTarget targe
         for (int r = 0; r < 4; ++r) acc[b][r] = 0.f;
 
     for (int t = 0; t < T; ++t) {
-        const int win = t % NW;
+        const int win = SW ? my_win : t % NW;
         const RowsStage st = stage_at(t);
         const bool next = t + 1 < T;
         if (win != xwin) {
@@ -818,7 +835,19 @@ __global__ __launch_bounds__(WV * 64) void gguf_gemv_rows(const RowsTarget targe
             consume(std::true_type{});
         else
             consume(std::false_type{});
-        if (win == NW - 1) {
+        if constexpr (SW) {
+            // this window's four row sums; written with raw LDS stores (a
+            // compiler-visible one would wait for the transfers in flight)
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const float v = reduce_rows4(acc[b]);
+                if ((lane & 15) == 0)
+                    lds_write4_raw(part0 + 4u * (((t * WV + wave) * NB + b) * 4 + (lane >> 4)),
+                                   __builtin_bit_cast(uint32_t, v));
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[b][r] = 0.f;
+            }
+        } else if (win == NW - 1) {
             const int row = lane >> 4;
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
@@ -840,6 +869,24 @@ __global__ __launch_bounds__(WV * 64) void gguf_gemv_rows(const RowsTarget targe
     // no transfer into this workgroup's LDS may outlive it (a wave with no
     // stage issued dummy ones; every other transfer was waited for above)
     if (T == 0) wait_vmcnt<0>();
+    if constexpr (SW) {
+        lds_barrier();  // every wave's partials are in
+        if (my_win == 0 && lane < 4 * NB) {
+            const int b = lane >> 2, r = lane & 3;
+            for (int t = 0; t < T; ++t) {
+                const RowsStage st = stage_at(t);
+                float v = 0.f;
+                for (int w = 0; w < NW; ++w) {
+                    uint32_t bits;
+                    asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)"
+                                 : "=v"(bits)
+                                 : "v"(part0 + 4u * (((t * WV + wave + w) * NB + b) * 4 + r)));
+                    v += __builtin_bit_cast(float, bits);
+                }
+                if (r < st.nrows) st.y[b * st.ldy + st.r0 + r] = f2h_bits(v);
+            }
+        }
+    }
 }
 
 // ---- MFMA batched GEMV (batch 3..16) ---------------------------------------------
@@ -1787,9 +1834,74 @@ int rows_resident(int NW) {
     return blocks_per_cu(fn, lds, WV * 64) * cu_count();
 }
 
+// Split-window plan (MODE 0, NW in 2..4): WV = NW x (1 or 2) row-group
+// slots.  Dynamic LDS: the waves' stage buffers, raw x, then the partial row
+// sums, tmax stages x WV waves x NB x 4 floats.
+template <Fmt F, int NB, int WV>
+size_t rows_sw_lds(int NW, int tmax) {
+    return rows_lds_bytes<F, NB>(NW, WV) + static_cast<size_t>(tmax) * WV * NB * 4 * sizeof(float);
+}
+
+template <Fmt F, int NB, int WV>
+int rows_sw_resident(int NW, int tmax) {
+    const size_t lds = rows_sw_lds<F, NB, WV>(NW, tmax);
+    if (lds > static_cast<size_t>(max_lds_bytes())) return 0;
+    const void* fn = reinterpret_cast<const void*>(&gguf_gemv_rows<F, NB, 0, WV, true>);
+    if (prepare_lds(fn, lds) != GDSLLM_OK) return 0;
+    return blocks_per_cu(fn, lds, WV * 64) * cu_count();
+}
+
+// Workgroups of WV = NW * R waves for RG row groups, all resident at once
+// (0 if they do not fit); sets tmax, the row groups per slot.
+template <Fmt F, int NB, int WV>
+int rows_sw_grid(int RG, int NW, int& tmax) {
+    if (WV % NW != 0) return 0;
+    const int R = WV / NW;
+    const int need = (RG + R - 1) / R;
+    int grid = std::min(need, rows_sw_resident<F, NB, WV>(NW, 1));
+    if (grid <= 0) return 0;
+    tmax = (RG + grid * R - 1) / (grid * R);
+    if (rows_sw_resident<F, NB, WV>(NW, tmax) < grid) return 0;
+    return grid;
+}
+
+// Split windows where they put more stages in flight than the plain plan's
+// `plain_waves`: sets grid and wv (the wave count, which says which
+// instantiation launches), tmax for the LDS size.
+template <Fmt F, int NB>
+bool plan_split_windows(int RG, int NW, int plain_waves, int& grid, int& wv, int& tmax) {
+    if (NW < 2 || NW > 4) return false;
+    int best = plain_waves, bg = 0, bw = 0, bt = 0;
+    auto consider = [&](int w, int g, int t) {
+        if (g > 0 && std::min(g * w, RG * NW) > best) {
+            best = std::min(g * w, RG * NW);
+            bg = g, bw = w, bt = t;
+        }
+    };
+    int t = 0;
+    switch (NW) {
+        case 2:
+            consider(2, rows_sw_grid<F, NB, 2>(RG, NW, t), t);
+            consider(4, rows_sw_grid<F, NB, 4>(RG, NW, t), t);
+            break;
+        case 3:
+            consider(3, rows_sw_grid<F, NB, 3>(RG, NW, t), t);
+            consider(6, rows_sw_grid<F, NB, 6>(RG, NW, t), t);
+            break;
+        default:
+            consider(4, rows_sw_grid<F, NB, 4>(RG, NW, t), t);
+            consider(8, rows_sw_grid<F, NB, 8>(RG, NW, t), t);
+            break;
+    }
+    if (bg == 0) return false;
+    grid = bg, wv = bw, tmax = bt;
+    return true;
+}
+
 template <Fmt F, int NB, int MODE>
-bool plan_rows(RowsTarget& tg, int K, int& grid, int& wv) {
+bool plan_rows(RowsTarget& tg, int K, int& grid, int& wv, int& tmax) {
     constexpr bool PAIRED = MODE == 2;
+    tmax = 0;
     const int NW = ((K >> 8) + kSbPerWindow - 1) / kSbPerWindow;
     const int parts = PAIRED ? 1 : tg.n;
     int rg_all = 0;
@@ -1826,14 +1938,46 @@ bool plan_rows(RowsTarget& tg, int K, int& grid, int& wv) {
         tg.gb_end[i] = grid;
     }
     for (int i = parts; i < kMaxGroup; ++i) tg.gb_end[i] = grid;
+    if constexpr (MODE == 0) {
+        // one matrix over several windows of x, too few row groups to give
+        // every CU a workgroup: split the windows over waves, which spreads
+        // the stages over more CUs (tmax > 0 marks the plan).  Where every CU
+        // already has a workgroup the split measured slower (4096 x 11008:
+        // 9.5 against 8.4 us; more workgroups re-read x from L2 and wait at
+        // one more barrier); 1024 x 8192: 4.95 against 5.84 us.
+        int g2 = 0, w2 = 0, t2 = 0;
+        if (grid > 0 && grid < cu_count() &&
+            plan_split_windows<F, NB>(rg_all, NW, std::min(grid * wv, rg_all), g2, w2, t2) && g2 > grid) {
+            grid = g2, wv = w2, tmax = t2;
+            for (int i = 0; i < kMaxGroup; ++i) tg.gb_end[i] = grid;
+        }
+    }
     return grid > 0;
 }
 
 template <Fmt F, int NB, int MODE>
-int launch_rows(const RowsTarget& tg, const uint16_t* x, int K, int64_t ldx, int grid, int wv, hipStream_t stream) {
+int launch_rows(const RowsTarget& tg, const uint16_t* x, int K, int64_t ldx, int grid, int wv, int tmax,
+                hipStream_t stream) {
     const int NW = ((K >> 8) + kSbPerWindow - 1) / kSbPerWindow;
     const size_t lds = rows_lds_bytes<F, NB>(NW, wv);
     if constexpr (MODE == 0) {
+        if (tmax > 0) {
+            auto go = [&](auto wv_c) {
+                constexpr int W = decltype(wv_c)::value;
+                const size_t sw_lds = rows_sw_lds<F, NB, W>(NW, tmax);
+                hipLaunchKernelGGL((gguf_gemv_rows<F, NB, 0, W, true>), dim3(grid), dim3(W * 64), sw_lds, stream, tg,
+                                   x, K, ldx);
+                return check_hip(hipGetLastError(), "gguf_gemv launch");
+            };
+            switch (wv) {
+                case 2: return go(std::integral_constant<int, 2>{});
+                case 3: return go(std::integral_constant<int, 3>{});
+                case 4: return go(std::integral_constant<int, 4>{});
+                case 6: return go(std::integral_constant<int, 6>{});
+                case 8: return go(std::integral_constant<int, 8>{});
+                default: return set_error(GDSLLM_ERR_UNSUPPORTED, "gguf_gemv: no split-window kernel for this wave count");
+            }
+        }
         if (wv == 8) {
             hipLaunchKernelGGL((gguf_gemv_rows<F, NB, MODE, 8>), dim3(grid), dim3(8 * 64), lds, stream, tg, x, K, ldx);
             return check_hip(hipGetLastError(), "gguf_gemv launch");
@@ -1854,13 +1998,13 @@ int try_rows(RowsTarget tg, const void* x, int K, int64_t batch, int64_t ldx, hi
     const bool x_al16 = reinterpret_cast<uintptr_t>(x) % 16 == 0 && (ldx % 8 == 0 || batch == 1);
     if (batch > 2 || K % 256 != 0 || K > (1 << 20) || !w_al16 || !x_al16) return -1;
     const auto* xp = static_cast<const uint16_t*>(x);
-    int grid = 0, wv = kWaves;
+    int grid = 0, wv = kWaves, tmax = 0;
     if (batch == 1) {
-        if (!plan_rows<F, 1, MODE>(tg, K, grid, wv)) return -1;
-        return launch_rows<F, 1, MODE>(tg, xp, K, ldx, grid, wv, s);
+        if (!plan_rows<F, 1, MODE>(tg, K, grid, wv, tmax)) return -1;
+        return launch_rows<F, 1, MODE>(tg, xp, K, ldx, grid, wv, tmax, s);
     }
-    if (!plan_rows<F, 2, MODE>(tg, K, grid, wv)) return -1;
-    return launch_rows<F, 2, MODE>(tg, xp, K, ldx, grid, wv, s);
+    if (!plan_rows<F, 2, MODE>(tg, K, grid, wv, tmax)) return -1;
+    return launch_rows<F, 2, MODE>(tg, xp, K, ldx, grid, wv, tmax, s);
 }
 
 RowsTarget single_target(const void* w, void* y, int M, int64_t ldy) {

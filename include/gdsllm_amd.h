@@ -131,7 +131,10 @@ int gdsllm_fused_int8_gemv(const void* weight, const void* scale, const void* x,
 
 /* n (1..4) GEMVs sharing x and in_dim in one launch: ys[i] receives
  * fp16[batch][out_dims[i]] (row-contiguous) = W_i x.  Same numerics as
- * gdsllm_fused_q4_0_gemv / gdsllm_fused_q8_0_gemv on each matrix; shapes the
+ * gdsllm_fused_q4_0_gemv / gdsllm_fused_q8_0_gemv on each matrix (the same
+ * bits, except where the single GEMV of a matrix too short to give every
+ * compute unit a workgroup, with in_dim over 2-4 windows of 4096, adds its
+ * window sums in another order: equal to fp32 rounding); shapes the
  * single-launch kernel does not serve fall back to one launch per matrix.    */
 int gdsllm_fused_q4_0_gemv_group(int n, const void* const* weights, void* const* ys,
                                  const int64_t* out_dims, const void* x, int64_t in_dim,

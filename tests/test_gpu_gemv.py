@@ -208,6 +208,37 @@ def test_gemv_group(gpu, fmt, Ms, K, B):
         assert np.array_equal(y, to_np(gguf_gemv(fmt, wd[i], xd, M, K))), f"group[{i}] differs from the single GEMV"
 
 
+# Fewer row groups than compute units and in_dim over 2-4 windows of 4096:
+# the single-matrix launch splits the windows over waves (2 windows; 3 with a
+# ragged last one; 4), and a group of two matrices keeps them in one wave.
+SPLIT_SHAPES = [(1024, 8192), (200, 11008), (37, 16384), (513, 12288), (4, 8192)]
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("B", [1, 2])
+@pytest.mark.parametrize("M,K", SPLIT_SHAPES, ids=[f"{m}x{k}" for m, k in SPLIT_SHAPES])
+def test_gemv_split_windows(gpu, fmt, B, M, K):
+    """Window sums added in window order after the stages: within the GEMV
+    tolerance of the oracle, and within fp32 reassociation of the unsplit
+    kernel (the same products; one fp16 ulp plus 2^-16 of ||w_r * x||)."""
+    import ctypes
+
+    w, x, deq = _gguf_case(fmt, M, K, B, 6500 + M + K + B)
+    wd, xd = w.to(gpu), x.to(gpu)
+    y = gguf_gemv(fmt, wd, xd, M, K)
+    assert_gemv_close(to_np(y), deq, to_np(x), f"{fmt} split {M}x{K} B{B}")
+    ys = [torch.empty(B, M, dtype=torch.float16, device=gpu) for _ in range(2)]
+    fn = capi().gdsllm_fused_q4_0_gemv_group if fmt == "q4_0" else capi().gdsllm_fused_q8_0_gemv_group
+    check(fn(2, (ctypes.c_void_p * 2)(ptr(wd), ptr(wd)), (ctypes.c_void_p * 2)(*[ptr(t) for t in ys]),
+             (ctypes.c_int64 * 2)(M, M), ptr(xd), K, B, K, stream()))
+    torch.cuda.synchronize()
+    a, b = to_np(y).astype(np.float64), to_np(ys[0]).astype(np.float64)
+    norms = oq.row_norms(deq, to_np(x))
+    bound = oq.fp16_ulp(np.maximum(np.abs(a), np.abs(b))) + norms * 2.0 ** -16
+    bad = np.abs(a - b) > bound
+    assert not bad.any(), f"{int(bad.sum())} outputs apart beyond reassociation, first at {np.argwhere(bad)[0]}"
+
+
 GATE_UP_CASES = [(300, 1024, 1), (11008, 4096, 1), (7, 256, 2), (1025, 2048, 2), (4096, 11008, 1), (16001, 1024, 1)]
 
 

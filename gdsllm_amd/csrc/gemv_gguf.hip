@@ -2046,16 +2046,22 @@ int gemv(const char* name, const void* w, const void* x, void* y, int64_t out_di
     const auto* xp = static_cast<const uint16_t*>(x);
     auto* yp = static_cast<uint16_t*>(y);
     const bool fast = (K % 256 == 0) && (reinterpret_cast<uintptr_t>(w) % 16 == 0);
-    int rc = try_rows<F, 0>(single_target(w, y, M, ldy), x, K, batch, ldx, s);
+    const bool x_al16 = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (ldx % 8 == 0);
+    // Q4_0 at batch 2 whose two rows of x would fill more than 64 KiB of the
+    // row-span kernel's LDS (8192 x 28672: 112 KiB, one 4-wave workgroup per
+    // CU, 37.0 us) goes to the code kernel (30.5 us); below that the row-span
+    // kernel is faster (11008 x 4096: 9.3 against 13.7 us)
+    const bool b2_codes = F == Fmt::Q4_0 && batch == 2 && fast && x_al16 && K <= (1 << 20) &&
+                          rows_xraw_bytes(2, ((K >> 8) + kSbPerWindow - 1) / kSbPerWindow) > 65536;
+    int rc = b2_codes ? -1 : try_rows<F, 0>(single_target(w, y, M, ldy), x, K, batch, ldx, s);
     if (rc != -1) return rc == GDSLLM_OK ? ok() : rc;
     rc = GDSLLM_OK;
-    const bool x_al16 = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (ldx % 8 == 0);
     if (F == Fmt::Q4_0 && fast && batch >= 3 && x_al16 && (use_q4_xreg(M, K) || use_q4_xreg_few(M, K, batch)) &&
         2 * (7 * ldx + K) < (int64_t{1} << 31)) {
         const int rc2 = launch_q4_xreg<bx::Tall>(w, xp, yp, M, K, batch, ldx, ldy, s);
         return rc2 == GDSLLM_OK ? ok() : rc2;
     }
-    if (F == Fmt::Q4_0 && fast && batch >= 3 && K <= (1 << 20) && x_al16) {
+    if (F == Fmt::Q4_0 && fast && (batch >= 3 || b2_codes) && K <= (1 << 20) && x_al16) {
         const int rc2 = q4_codes_rows(M) == 32 ? launch_q4_codes<32>(w, xp, yp, M, K, batch, ldx, ldy, s)
                                                : launch_q4_codes<16>(w, xp, yp, M, K, batch, ldx, ldy, s);
         return rc2 == GDSLLM_OK ? ok() : rc2;

@@ -820,11 +820,19 @@ __global__ __launch_bounds__(kThreads) void affine_rows(Rows rows, const uint16_
             __syncthreads();
             routed_idx = route_pick[lane];
         }
-        // the shared-expert gate logit, by the grid's last wave (it has the
-        // fewest stages), as gdsllm_gemv_f16 would compute it
-        if (gw == TW - 1) {
-            const float g = f16_row_dot(rows.gate_w, X, K, lane);
-            if (lane == 0) *rows.logit = f2h_bits(g);
+        // the shared-expert gate logit, by the grid's last workgroup (its
+        // waves have the fewest stages): wave j takes part j of the row dot
+        // and wave 0 adds the parts in order, as gdsllm_gemv_f16 does (one
+        // wave taking all four parts made itself the launch's last wave)
+        if (blockIdx.x == gridDim.x - 1) {
+            __shared__ float logit_part[kWaves];
+            static_assert(kWaves == 4, "one part of the row dot per wave");
+            const int part = threadIdx.x >> 6;
+            const float p = group_sum<64>(f16_part_lane(rows.gate_w, X, K, part, lane));
+            if (lane == 0) logit_part[part] = p;
+            __syncthreads();
+            if (threadIdx.x == 0)
+                *rows.logit = f2h_bits(((logit_part[0] + logit_part[1]) + logit_part[2]) + logit_part[3]);
         }
         if (T == 0) {
             wait_vmcnt<0>();  // no load outlives its wave

@@ -330,7 +330,7 @@ def test_extension_module_surface():
                               "output"],
         "fused_affine_q4_gemv": ["handle", "x", "weight_shape", "weight_offset", "scale_offset", "bias_offset",
                                  "group_size"],
-        # extensions of this build
+        # extensions of this library
         "embed_gguf": ["handle", "token_ids", "shape", "gguf_type", "offset"],
         "dequant_int8": ["weight", "scale", "output"],
         "int8_linear": ["weight", "scale", "x"],

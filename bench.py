@@ -1057,7 +1057,7 @@ def main() -> int:
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU only: the library has no multi-GPU path "
-              "(the GEMV would shard by output rows; see the design notes).", file=sys.stderr)
+              "(the GEMV would shard by output rows, one row range per GPU).", file=sys.stderr)
         return 2
     if args.steps < 1 or args.warmup < 0 or args.copies < 1 or args.chunk < 1:
         print("bench.py: --steps >= 1, --warmup >= 0, --copies >= 1, --chunk >= 1", file=sys.stderr)

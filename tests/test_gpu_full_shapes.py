@@ -2,7 +2,9 @@
 geometry and the kernel chosen differ from the smaller test shapes:
 
 * the LLaMA-70B layer projections (q/o 8192x8192, k/v 1024x8192, gate/up
-  28672x8192, down 8192x28672) at batch 1, 2, 4 and 8;
+  28672x8192, down 8192x28672) at batch 1, 2, 4 and 8, and the layer's
+  decode-step fusions at batch 1 and 2 (q/k/v in one grouped launch,
+  gate/up/SiLU in one launch);
 * the LLaMA-7B lm_head 32000x4096 as the batch-1 GEMV and as the 512-token
   prefill GEMM, and the 512-token GEMMs of gate/up 11008x4096 and down
   4096x11008.
@@ -84,3 +86,40 @@ def test_q4_0_prefill_gemm_512_tokens(gpu, M, K):
     check(capi().gdsllm_dequant_gemm_q4_0(ptr(w), ptr(xd), ptr(y), M, K, T, K, M, stream()))
     torch.cuda.synchronize()
     _check_rows(y, w, x, _sample_rows(M, seed), K, f"prefill T{T} {M}x{K}")
+
+
+@pytest.mark.parametrize("B", [1, 2])
+def test_q4_0_70b_qkv_group_and_gate_up_silu(gpu, B):
+    """The fused 70B layer of the benchmark: q, k, v (8192, 1024, 1024 rows x
+    8192) in one grouped launch and h = silu(gate x) * (up x) for 28672 x 8192
+    in one launch, against the oracle on sampled rows (h from the oracle's
+    fp16 g and u with torch's fp16 SiLU and product)."""
+    import ctypes
+
+    seed = 3300 + B
+    Ms = (8192, 1024, 1024)
+    ws = [_weights(M, 8192, seed + i, gpu) for i, M in enumerate(Ms)]
+    x = syn.activations(B, 8192, torch.Generator().manual_seed(seed + 5))
+    xd = x.to(gpu)
+    ys = [torch.empty(B, M, dtype=torch.float16, device=gpu) for M in Ms]
+    check(capi().gdsllm_fused_q4_0_gemv_group(3, (ctypes.c_void_p * 3)(*[ptr(w) for w in ws]),
+                                              (ctypes.c_void_p * 3)(*[ptr(y) for y in ys]),
+                                              (ctypes.c_int64 * 3)(*Ms), ptr(xd), 8192, B, 8192, stream()))
+    F = 28672
+    wg, wu = _weights(F, 8192, seed + 6, gpu), _weights(F, 8192, seed + 7, gpu)
+    h = torch.empty(B, F, dtype=torch.float16, device=gpu)
+    check(capi().gdsllm_fused_q4_0_gate_up_silu(ptr(wg), ptr(wu), ptr(xd), ptr(h), F, 8192, B, 8192, F, stream()))
+    torch.cuda.synchronize()
+    for i, (w, y, M) in enumerate(zip(ws, ys, Ms)):
+        _check_rows(y, w, x, _sample_rows(M, seed + i), 8192, f"70B qkv group[{i}] {M}x8192 B={B}")
+    rows = _sample_rows(F, seed + 8)
+    hn = to_np(h).astype(np.float64)[:, rows]
+    assert np.isfinite(hn).all(), "non-finite h"
+    idx = torch.as_tensor(rows, device=gpu)
+    gq = oq.gemv(oq.dequant_q4_0(to_np(wg[idx])).reshape(len(rows), 8192), to_np(x)).astype(np.float16)
+    uq = oq.gemv(oq.dequant_q4_0(to_np(wu[idx])).reshape(len(rows), 8192), to_np(x)).astype(np.float16)
+    h_ref = (oq.silu_fp16(gq).astype(np.float32) * uq.astype(np.float32)).astype(np.float64)
+    rel = float(np.linalg.norm(hn - h_ref) / np.linalg.norm(h_ref))
+    print(f"70B gate_up_silu 28672x8192 B={B}: rel L2 {rel:.2e}")
+    assert rel <= oq.GEMV_REL_L2, f"h rel L2 {rel:.3e}"
+

@@ -264,9 +264,13 @@ def _gemv_call(fmt: str, w, x, y, m: int, k: int, b: int) -> None:
 
 def bench_q8_layer(dev, layers_rotated: int = 3, reps: int = 50):
     """Q8_0 LLaMA-7B decoder layer at batch 1: 7 GEMVs per layer, rotating over
-    `layers_rotated` distinct layers (3 x 215 MB > the 256 MB Infinity Cache)."""
+    `layers_rotated` distinct layers (3 x 215 MB > the 256 MB Infinity Cache);
+    also with the decode-step fusions (4 launches per layer)."""
+    import ctypes
+
     import torch
 
+    from gdsllm_amd import capi, check
     from gdsllm_amd import synthetic as syn
 
     gen = torch.Generator(device=dev).manual_seed(1001)
@@ -281,9 +285,33 @@ def bench_q8_layer(dev, layers_rotated: int = 3, reps: int = 50):
 
     ms = _replay_ms(run, reps) / layers_rotated
     nbytes = sum(m * (k // 32) * 34 + 2 * k + 2 * m for m, k in LAYER_SHAPES)
+
+    # q/k/v in one grouped launch, o, gate/up/SiLU writing h, down on h
+    lib = capi()
+    h = torch.empty(1, 11008, dtype=torch.float16, device=dev)
+    yq, yk, yv = (torch.empty(1, 4096, dtype=torch.float16, device=dev) for _ in range(3))
+    dims = (ctypes.c_int64 * 3)(4096, 4096, 4096)
+    outs = (ctypes.c_void_p * 3)(yq.data_ptr(), yk.data_ptr(), yv.data_ptr())
+    groups = [(ctypes.c_void_p * 3)(lw[0].data_ptr(), lw[1].data_ptr(), lw[2].data_ptr()) for lw in layers]
+
+    def run_fused():
+        st = torch.cuda.current_stream().cuda_stream
+        for lw, grp in zip(layers, groups):
+            check(lib.gdsllm_fused_q8_0_gemv_group(3, grp, outs, dims, xs[4096].data_ptr(), 4096, 1, 4096, st))
+            _gemv_call("q8_0", lw[3], xs[4096], ys[4096], 4096, 4096, 1)
+            check(lib.gdsllm_fused_q8_0_gate_up_silu(lw[4].data_ptr(), lw[5].data_ptr(), xs[4096].data_ptr(),
+                                                     h.data_ptr(), 11008, 4096, 1, 4096, 11008, st))
+            _gemv_call("q8_0", lw[6], h, ys[4096], 4096, 11008, 1)
+
+    msf = _replay_ms(run_fused, reps) / layers_rotated
+    fbytes = sum(m * (k // 32) * 34 for m, k in LAYER_SHAPES) + 2 * (4096 + 3 * 4096 + 2 * 4096 + 4096 + 11008 +
+                                                                    11008 + 4096)
     return {"us_per_layer": round(ms * 1e3, 3), "bytes_per_layer": nbytes,
             "GB_s": round(nbytes / (ms * 1e-3) / 1e9, 1), "pct_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / 80, 1),
-            "layers_rotated": layers_rotated}
+            "layers_rotated": layers_rotated,
+            "fused_4_launches": {"us_per_layer": round(msf * 1e3, 3), "bytes_per_layer": fbytes,
+                                 "GB_s": round(fbytes / (msf * 1e-3) / 1e9, 1),
+                                 "pct_of_hbm_peak": round(fbytes / (msf * 1e-3) / 1e9 / 80, 1)}}
 
 
 def bench_int8_layer(dev, layers_rotated: int = 2, reps: int = 50, ref_reps: int = 5):

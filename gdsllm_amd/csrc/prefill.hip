@@ -51,9 +51,9 @@
 //             count n) multiplies the X rows tok[p0 .. p0+n-1] by expert e's
 //             matrix (stacked pool, e * stride) into Y rows p0 .. p0+n-1.
 //  * kDenseDual kDense with the gate/up split of kDualSilu: workgroup rows
-//             0..63 from the gate matrix and 64..127 from the up matrix at the
-//             same 64 output rows, h written instead of g and u (the prefill
-//             form of the decode gate_up_silu, runtime/llama.py:253-256).
+//             0..BM/2-1 from the gate matrix and BM/2..BM-1 from the up matrix
+//             at the same BM/2 output rows, h written instead of g and u (the
+//             prefill form of the decode gate_up_silu, runtime/llama.py:253-256).
 //  * kDualSilu  kGather with rows 0..63 of the workgroup taken from the gate
 //             pool and rows 64..127 from the up pool at the same 64 output
 //             rows; the epilogue writes h = fp16(fp16(silu(g)) * u) with
@@ -71,7 +71,7 @@ enum class WF { Q4_0, Q8_0, AFF32, AFF64, AFF128 };
 enum Mode { kDense = 0, kGather = 1, kDualSilu = 2, kDenseDual = 3 };
 
 constexpr int kWaves = 8;
-constexpr int kBM = 128;     // weight rows per workgroup
+constexpr int kBM = 128;     // weight rows per workgroup (256 for the dense GGUF tile below)
 constexpr int kStageK = 128; // k values per stage
 
 constexpr bool is_affine(WF f) { return f == WF::AFF32 || f == WF::AFF64 || f == WF::AFF128; }
@@ -79,35 +79,39 @@ constexpr int aff_group(WF f) { return f == WF::AFF32 ? 32 : f == WF::AFF64 ? 64
 
 // W slot geometry per format.
 //   SPS      stages per slot
-//   kSlot    bytes of one slot (128 rows)
+//   kSlot    bytes of one slot (BM rows; BM = 256 for GGUF only)
 //   kReal    transfers that carry data per slot; kCW per wave (dummies past kReal)
 //   GGUF: a 144-byte window per row (9 chunks): Q4_0 two stages (8 blocks of
 //   18 bytes); Q8_0 one stage (4 blocks of 34 = 136 bytes, starting 0 or 8
 //   bytes into the window).  Affine: 128 bytes of words per row (two stages),
 //   then the rows' scales and biases for those 256 k values (SB bytes each).
-template <WF F>
+template <WF F, int BM = kBM>
 struct Fmt {
     static constexpr bool kAff = is_affine(F);
+    static_assert(BM == kBM || (BM == 2 * kBM && !kAff), "256-row slots hold GGUF windows only");
     static constexpr int G = kAff ? aff_group(F) : 32;
     static constexpr int SPS = F == WF::Q8_0 ? 1 : 2;
     static constexpr int SB = kAff ? 512 / G : 0;                          // scale bytes per row per slot
     static constexpr bool kS16 = SB == 16;                                 // scales move in 16-byte transfers
     static constexpr int kST = kAff ? (kS16 ? 2 : SB * kBM / 256) : 0;     // transfers for one of scales/biases
-    static constexpr int kSlot = kAff ? 16384 + 2 * kBM * SB : kBM * 144;
-    static constexpr int kReal = kAff ? 16 + 2 * kST : 18;
-    static constexpr int kCW = 3;  // transfers per wave per slot
-    static_assert(kReal <= kCW * kWaves && kReal > 2 * kWaves, "two full rounds of transfers and a partial third");
+    static constexpr int kSlot = kAff ? 16384 + 2 * kBM * SB : BM * 144;
+    static constexpr int kReal = kAff ? 16 + 2 * kST : BM * 144 / 1024;
+    static constexpr int kCW = kAff ? 3 : (kReal + kWaves - 1) / kWaves;  // transfers per wave per slot
+    static_assert(kReal <= kCW * kWaves && kReal > (kCW - 1) * kWaves, "full rounds of transfers and a partial last");
 };
 
-template <WF F, int BT>
+// X and W rings.  The 256-row tile (36 KiB W slots) keeps two of each: a
+// stage of it is two of a 128-row tile's stages long per wave, so two slots
+// hide as much latency as three do there.
+template <WF F, int BT, int BM = kBM>
 struct Ring {
     static constexpr int kXSlot = BT * 256;
     static constexpr int kLdsMax = 163840;
-    static constexpr int XR0 = BT == 128 ? 3 : BT == 64 ? 5 : 6;
-    static constexpr int RW = BT == 128 ? 3 : BT == 64 ? 4 : 5;
-    static constexpr int XR = XR0 * kXSlot + RW * Fmt<F>::kSlot + 1024 <= kLdsMax ? XR0 : XR0 - 1;
+    static constexpr int XR0 = BM == 2 * kBM ? 2 : BT == 128 ? 3 : BT == 64 ? 5 : 6;
+    static constexpr int RW = BM == 2 * kBM ? 2 : BT == 128 ? 3 : BT == 64 ? 4 : 5;
+    static constexpr int XR = XR0 * kXSlot + RW * Fmt<F, BM>::kSlot + 1024 <= kLdsMax ? XR0 : XR0 - 1;
     static constexpr int kWOff = XR * kXSlot;
-    static constexpr int kDummy = kWOff + RW * Fmt<F>::kSlot;
+    static constexpr int kDummy = kWOff + RW * Fmt<F, BM>::kSlot;
     static constexpr int kRing = kDummy + 1024;  // dummy transfers land in the last 1 KiB
     static constexpr int kRed = kWaves * (BT >= 64 ? 2 : 1) * 2 * 4 * 64 * 16;  // partial sums of one pass
     static constexpr int kLds = kRing > kRed ? kRing : kRed;
@@ -152,10 +156,17 @@ struct GemmArgs {
 
 typedef float float16_t __attribute__((ext_vector_type(16)));
 
-template <WF F, int BT, int MODE>
+// BM = 256 (dense GGUF only): the same 64-row x BT-token wave tile, with
+// the workgroup's 8 waves as 4 row quarters x 2 K halves instead of 2 row
+// halves x 4 K quarters.  Each X stage then feeds twice the rows: per MFMA the
+// compute unit takes in 40% fewer bytes (X dominates them), which is what
+// bounds this kernel at 512 tokens.  A wave's stage is two sub-stages (its two
+// blocks of the four), each scheduled like a 128-row stage; the wait and the
+// workgroup barrier come once per stage, after the second.
+template <WF F, int BT, int MODE, int BM = kBM>
 __global__ __launch_bounds__(kWaves * 64) void gemm_sk(GemmArgs a) {
-    using Fm = Fmt<F>;
-    using R = Ring<F, BT>;
+    using Fm = Fmt<F, BM>;
+    using R = Ring<F, BT, BM>;
     constexpr int NTF = BT / 32;        // token fragments per wave
     constexpr int NX = BT / 32;         // X transfers per wave per stage
     constexpr int SPS = Fm::SPS, XR = R::XR, RW = R::RW, CW = Fm::kCW;
@@ -163,12 +174,15 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_sk(GemmArgs a) {
     constexpr bool kGath = MODE == kGather || MODE == kDualSilu;
     constexpr bool kDual = MODE == kDualSilu || MODE == kDenseDual;
     static_assert(MODE != kDualSilu || Fm::kAff, "the gathered dual tiles are built for the affine pools");
+    static_assert(BM == kBM || MODE == kDense || MODE == kDenseDual, "the 256-row tile is dense only");
+    constexpr int KS = kWaves * 64 / BM;  // waves along K (4 or 2)
+    constexpr int NSUB = 4 / KS;          // 32-value blocks per wave per stage
 
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int h = lane >> 5, l32 = lane & 31;
-    const int kq = wave & 3, rq = wave >> 2;
+    const int kq = wave % KS, rq = wave / KS;
 
     // ---- tile
     int m0, t0 = 0, nt, p0 = 0;
@@ -194,7 +208,7 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_sk(GemmArgs a) {
         const int nwg = gridDim.x, b = blockIdx.x;
         const int per = nwg >> 3, rem = nwg & 7, xcd = b & 7;
         const int q = xcd * per + (xcd < rem ? xcd : rem) + (b >> 3);
-        m0 = (q % a.mtiles) * (kDual ? 64 : kBM);
+        m0 = (q % a.mtiles) * (kDual ? BM / 2 : BM);
         t0 = (q / a.mtiles) * BT;
         nt = min(BT, a.T - t0);
     }
@@ -218,21 +232,23 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_sk(GemmArgs a) {
     }
     const uint16_t* xbase = a.x;
 
-    // ---- W sources.  Transfer i = 8*ii + wave of a slot (ii < 3).  ii = 0, 1
-    // are 16-byte transfers of GGUF blocks / affine words (i < 16, always
-    // data); ii = 2 carries GGUF transfers 16-17, or the affine scales and
-    // biases, and is a dummy in the remaining waves.  The kind of each ii is a
+    // ---- W sources.  Transfer i = 8*ii + wave of a slot (ii < CW: 3, or 5 for
+    // the 256-row GGUF slot).  ii < CW - 1 are 16-byte transfers of GGUF
+    // blocks / affine words (always data); ii = CW - 1 carries the last GGUF
+    // transfers (16-17 of 18, 32-35 of 36), or the affine scales and biases,
+    // and is a dummy in the remaining waves.  The kind of each ii is a
     // compile-time fact and its base and LDS offset are wave-uniform, so the
     // issue code has no branches; lane offsets are fixed per lane.
     const int64_t rb_main = Fm::kAff ? K / 2 : (K / 32) * (F == WF::Q8_0 ? 34 : 18);
     const int64_t rb_sc = Fm::kAff ? 2 * (K / Fm::G) : 0;
-    constexpr bool k2s16 = !Fm::kAff || Fm::kS16;  // ii = 2 moves 16 bytes per lane (else 4)
-    const uint8_t* wsrc[3];  // tile base (row m0 of its matrix)
-    uint32_t woff[3];
-    uint32_t wdst[3];        // LDS offset inside the slot
+    constexpr bool k2s16 = !Fm::kAff || Fm::kS16;  // ii = CW - 1 moves 16 bytes per lane (else 4)
+    constexpr int L = CW - 1;  // the last transfer of a slot, partly dummies
+    const uint8_t* wsrc[CW];   // tile base (row m0 of its matrix)
+    uint32_t woff[CW];
+    uint32_t wdst[CW];         // LDS offset inside the slot
     bool real2 = true;
 #pragma unroll
-    for (int ii = 0; ii < 2; ++ii) {
+    for (int ii = 0; ii < L; ++ii) {
         const int i = 8 * ii + wave;
         int r, cp;
         if constexpr (!Fm::kAff) {
@@ -246,23 +262,23 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_sk(GemmArgs a) {
             r = g >> 3;
             cp = (g & 7) ^ (r & 7);
         }
-        const bool second = kDual && i >= (Fm::kAff ? 8 : 9);
-        const int rr = second ? r - 64 : r;
+        const bool second = kDual && i >= (Fm::kAff ? 8 : Fm::kReal / 2);  // up rows BM/2 .. BM-1
+        const int rr = second ? r - BM / 2 : r;
         const int ra = min(m0 + rr, M - 1) - m0;
         wsrc[ii] = (second ? wB : wA) + static_cast<int64_t>(m0) * rb_main;
         woff[ii] = static_cast<uint32_t>(ra * rb_main + 16 * cp);
         wdst[ii] = 1024 * i;
     }
     if constexpr (!Fm::kAff) {
-        const int i = 16 + wave;
-        real2 = i < 18;
+        const int i = 8 * L + wave;
+        real2 = i < Fm::kReal;
         const int g = 64 * i + lane, r = g / 9, cp = g % 9;
-        const bool second = kDual;  // rows 64 .. 127
-        const int rr = second ? r - 64 : r;
+        const bool second = kDual;  // rows past BM/2
+        const int rr = second ? r - BM / 2 : r;
         const int ra = min(m0 + rr, M - 1) - m0;
-        wsrc[2] = (second ? wB : wA) + static_cast<int64_t>(m0) * rb_main;
-        woff[2] = real2 ? static_cast<uint32_t>(ra * rb_main + 16 * cp) : 0u;
-        wdst[2] = 1024 * i;
+        wsrc[L] = (second ? wB : wA) + static_cast<int64_t>(m0) * rb_main;
+        woff[L] = real2 ? static_cast<uint32_t>(ra * rb_main + 16 * cp) : 0u;
+        wdst[L] = 1024 * i;
     } else {
         const int j0 = wave;
         real2 = j0 < 2 * Fm::kST;
@@ -274,17 +290,17 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_sk(GemmArgs a) {
         if constexpr (Fm::kS16) {
             r = 64 * j + lane;
             inrow = 0;
-            wdst[2] = 16384 + (isb ? kBM * Fm::SB : 0) + 1024 * j;
+            wdst[L] = 16384 + (isb ? kBM * Fm::SB : 0) + 1024 * j;
         } else {
             const int d = 64 * j + lane, per = Fm::SB / 4;
             r = d / per;
             inrow = 4 * (d % per);
-            wdst[2] = 16384 + (isb ? kBM * Fm::SB : 0) + 256 * j;
+            wdst[L] = 16384 + (isb ? kBM * Fm::SB : 0) + 256 * j;
         }
         const int rr = second ? r - 64 : r;
         const int ra = min(m0 + rr, M - 1) - m0;
-        wsrc[2] = (real2 ? base : sA) + static_cast<int64_t>(m0) * rb_sc;
-        woff[2] = real2 ? static_cast<uint32_t>(ra * rb_sc + inrow) : 0u;
+        wsrc[L] = (real2 ? base : sA) + static_cast<int64_t>(m0) * rb_sc;
+        woff[L] = real2 ? static_cast<uint32_t>(ra * rb_sc + inrow) : 0u;
     }
     // byte offset of group gi inside a row: GGUF blocks / affine words
     auto goff_main = [&](int gi) -> int64_t {
@@ -308,18 +324,18 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_sk(GemmArgs a) {
     auto issue_w = [&](int gi) {  // W group gi into its ring slot
         if (gi < 0) {
 #pragma unroll
-            for (int ii = 0; ii < 3; ++ii) dma4_asm(0u, a.w, lds0 + R::kDummy);
+            for (int ii = 0; ii < CW; ++ii) dma4_asm(0u, a.w, lds0 + R::kDummy);
             return;
         }
         const uint32_t slot = lds0 + R::kWOff + (gi % RW) * Fm::kSlot;
         const int gc = gi < ngr ? gi : ngr - 1;
         const int64_t om = goff_main(gc);
-        dma16_asm(woff[0], wsrc[0] + om, slot + wdst[0]);
-        dma16_asm(woff[1], wsrc[1] + om, slot + wdst[1]);
+#pragma unroll
+        for (int ii = 0; ii < L; ++ii) dma16_asm(woff[ii], wsrc[ii] + om, slot + wdst[ii]);
         const int64_t o2 = Fm::kAff ? static_cast<int64_t>(Fm::SB) * gc : om;
-        const uint32_t d2 = real2 ? slot + wdst[2] : lds0 + R::kDummy;
-        if constexpr (k2s16) dma16_asm(woff[2], wsrc[2] + o2, d2);
-        else dma4_asm(woff[2], wsrc[2] + o2, d2);
+        const uint32_t d2 = real2 ? slot + wdst[L] : lds0 + R::kDummy;
+        if constexpr (k2s16) dma16_asm(woff[L], wsrc[L] + o2, d2);
+        else dma4_asm(woff[L], wsrc[L] + o2, d2);
     };
     auto floordiv = [](int v, int d) { return v >= 0 ? v / d : -((-v + d - 1) / d); };
     auto issue_stage = [&](int s) {
@@ -328,13 +344,15 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_sk(GemmArgs a) {
         if (ph == SPS - 1) issue_w(floordiv(s, SPS) + RW);
     };
 
-    // ---- operand reads of stage u
-    uint32_t xrd[2];
+    // ---- operand reads of sub-stage j of stage u: block NSUB*kq + j of the stage
+    uint32_t xrd[NSUB][2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) xrd[i] = 256 * l32 + 16 * ((4 * kq + 2 * i + h) ^ (lane & 15));
+    for (int j = 0; j < NSUB; ++j)
+#pragma unroll
+        for (int i = 0; i < 2; ++i) xrd[j][i] = 256 * l32 + 16 * ((4 * (NSUB * kq + j) + 2 * i + h) ^ (lane & 15));
     const int row0 = 64 * rq + l32;  // tile row of fragment 0
     // qs bytes 8h.. of a block start 2 mod 4 bytes into LDS for even blocks
-    const uint32_t wsh = (kq & 1) ? 0u : 2u;
+    auto wshift = [&](int j) -> uint32_t { return ((NSUB * kq + j) & 1) ? 0u : 2u; };
     const NibUnpack nib;
     uint32_t c64 = 0x64646464u, mixmask = 0x00F0000Fu, mixbits = 0x54006400u;
     asm volatile("" : "+v"(c64), "+s"(mixmask), "+v"(mixbits));
@@ -354,13 +372,14 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_sk(GemmArgs a) {
         u32x4_t v[2][2];     // [k-step][row fragment]: fp16 weight pairs
         uint32_t t[2][4];    // [row fragment] prepared bytes shared by a fragment's units
     };
-    auto read_raw = [&](int u, Raw& o) {
+    auto read_raw = [&](int u, int j, Raw& o) {
+        const int kb = NSUB * kq + j;  // block of the stage
         const uint8_t* xs = lds + (u % XR) * kXSlot;
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int ft = 0; ft < NTF; ++ft)
-                o.xa[i][ft] = *reinterpret_cast<const half8_t*>(xs + xrd[i] + 8192 * ft);
+                o.xa[i][ft] = *reinterpret_cast<const half8_t*>(xs + xrd[j][i] + 8192 * ft);
         const uint8_t* ws = lds + R::kWOff + ((u / SPS) % RW) * Fm::kSlot;
 #pragma unroll
         for (int fr = 0; fr < 2; ++fr) {
@@ -369,7 +388,7 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_sk(GemmArgs a) {
             // third dword is read even when unused (inside the slot, or the bytes
             // after the ring), so no branch splits the loop body
             if constexpr (F == WF::Q4_0) {
-                const int jj = 4 * (u & 1) + kq;
+                const int jj = 4 * (u & 1) + kb;
                 const uint8_t* rowp = ws + 144 * rt;
                 o.d[fr][0] = *reinterpret_cast<const uint16_t*>(rowp + 18 * jj);
                 const uint32_t* qp = reinterpret_cast<const uint32_t*>(rowp + ((18 * jj + 2 + 8 * h) & ~3));
@@ -377,7 +396,7 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_sk(GemmArgs a) {
                 o.q[fr][1] = qp[1];
                 o.q[fr][2] = qp[2];
             } else if constexpr (F == WF::Q8_0) {
-                const int blk = 8 * (u & 1) + 34 * kq;
+                const int blk = 8 * (u & 1) + 34 * kb;
                 const uint8_t* rowp = ws + 144 * rt;
                 o.d[fr][0] = *reinterpret_cast<const uint16_t*>(rowp + blk);
 #pragma unroll
@@ -388,11 +407,11 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_sk(GemmArgs a) {
                     o.q[fr][3 * i + 2] = qp[2];
                 }
             } else {
-                // words 16(u & 1) + 4kq + 2i + h of the row: chunk 4(u & 1) + kq
-                const uint8_t* chunk = ws + 128 * rt + 16 * ((4 * (u & 1) + kq) ^ (rt & 7));
+                // words 16(u & 1) + 4kb + 2i + h of the row: chunk 4(u & 1) + kb
+                const uint8_t* chunk = ws + 128 * rt + 16 * ((4 * (u & 1) + kb) ^ (rt & 7));
                 o.q[fr][0] = *reinterpret_cast<const uint32_t*>(chunk + 4 * h);
                 o.q[fr][1] = *reinterpret_cast<const uint32_t*>(chunk + 4 * h + 8);
-                const int gi = (128 * (u & 1) + 32 * kq) / Fm::G;
+                const int gi = (128 * (u & 1) + 32 * kb) / Fm::G;
                 const uint8_t* sp = ws + 16384 + Fm::SB * rt + 2 * gi;
                 o.d[fr][0] = *reinterpret_cast<const uint16_t*>(sp);
                 o.d[fr][1] = *reinterpret_cast<const uint16_t*>(sp + kBM * Fm::SB);
@@ -402,7 +421,7 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_sk(GemmArgs a) {
     // Dequant unit (ks, z) of the weight fragments: k-step ks, row fragment
     // z / 2, pairs 2(z & 1) .. +1 of the fragment's four.  A k-step's four units
     // run in order (unit 0 of a fragment prepares the bytes its units share).
-    auto dq_unit = [&](int ks, int z, const Raw& r, Wb& o) {
+    auto dq_unit = [&](int ks, int z, const Raw& r, Wb& o, uint32_t wsh) {
         const int fr = z >> 1, hf = z & 1;
         if constexpr (F == WF::Q4_0) {
             // k-step 0 takes the low nibbles, k-step 1 the high nibbles of the same bytes
@@ -469,9 +488,9 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_sk(GemmArgs a) {
     lds_barrier();
     Raw rcur, rnxt;
     Wb wcur, wnxt;
-    read_raw(0, rcur);
+    read_raw(0, 0, rcur);
 #pragma unroll
-    for (int z = 0; z < 4; ++z) dq_unit(0, z, rcur, wcur);
+    for (int z = 0; z < 4; ++z) dq_unit(0, z, rcur, wcur, wshift(0));
 
     // A stage in two halves, one per k-step of its MFMAs:
     //  1. the k-step 0 MFMAs of stage s (operands already in registers), with
@@ -493,25 +512,34 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_sk(GemmArgs a) {
         for (int u = 0; u < 4; ++u)
             if ((u * nz) / 4 == z - zfirst) unit(u);
     };
-    auto stage = [&](auto P_, int s) {
+    // Sub-stage J of stage s.  Only the last one waits, meets the workgroup
+    // at the barrier and issues transfers; an earlier one reads the next
+    // block of the same stage, which landed before the previous barrier.
+    auto sub_stage = [&](auto P_, auto J_, int s) {
         constexpr int PH = decltype(P_)::value;  // s % SPS
+        constexpr int J = decltype(J_)::value;
+        const uint32_t sh_cur = wshift(J), sh_nxt = wshift(J + 1 < NSUB ? J + 1 : 0);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int z = 0; z < NH; ++z) {
             mfma_z(z, rcur, wcur);
-            spread(z, 0, NH, [&](int u) { dq_unit(1, u, rcur, wcur); });
+            spread(z, 0, NH, [&](int u) { dq_unit(1, u, rcur, wcur, sh_cur); });
             __builtin_amdgcn_sched_barrier(0);
         }
-        wait_vmcnt_asm<wait_count(PH, SPS, XR, RW, NX, CW)>();
-        lds_barrier();
-        issue_x(s + XR);
-        if constexpr (PH == SPS - 1) issue_w(s / SPS + RW);
-        read_raw(s + 1, rnxt);
+        if constexpr (J == NSUB - 1) {
+            wait_vmcnt_asm<wait_count(PH, SPS, XR, RW, NX, CW)>();
+            lds_barrier();
+            issue_x(s + XR);
+            if constexpr (PH == SPS - 1) issue_w(s / SPS + RW);
+            read_raw(s + 1, 0, rnxt);
+        } else {
+            read_raw(s, J + 1, rnxt);
+        }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int z = NH; z < 2 * NH; ++z) {
             mfma_z(z, rcur, wcur);
-            spread(z - NH, Z0, NH - Z0, [&](int u) { dq_unit(0, u, rnxt, wnxt); });
+            spread(z - NH, Z0, NH - Z0, [&](int u) { dq_unit(0, u, rnxt, wnxt, sh_nxt); });
             __builtin_amdgcn_sched_barrier(0);
         }
         rcur = rnxt;
@@ -521,6 +549,10 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_sk(GemmArgs a) {
         for (int fr = 0; fr < 2; ++fr)
 #pragma unroll
             for (int e = 0; e < 4; ++e) wcur.t[fr][e] = wnxt.t[fr][e];
+    };
+    auto stage = [&](auto P_, int s) {
+        sub_stage(P_, std::integral_constant<int, 0>{}, s);
+        if constexpr (NSUB == 2) sub_stage(P_, std::integral_constant<int, 1>{}, s);
     };
     if constexpr (SPS == 2) {
         for (int s = 0; s < nst; s += 2) {
@@ -545,7 +577,7 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_sk(GemmArgs a) {
     auto ksum = [&](int wbase, int f, int fr, int j) {
         float4_t sum = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int src = 0; src < 4; ++src) sum += *reinterpret_cast<const float4_t*>(red + 4 * (unit(wbase + src, f, fr, j) * 64 + lane));
+        for (int src = 0; src < KS; ++src) sum += *reinterpret_cast<const float4_t*>(red + 4 * (unit(wbase + src, f, fr, j) * 64 + lane));
         return sum;
     };
     auto yrow = [&](int t) -> int64_t { return kGath ? static_cast<int64_t>(p0 + t) : static_cast<int64_t>(t0 + t); };
@@ -564,12 +596,13 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_sk(GemmArgs a) {
                 }
         __syncthreads();
         if constexpr (!kDual) {
-            // wave (kq, rq) stores units v = 2*PF*kq .. +2*PF-1 of row half rq
+            // wave (kq, rq) stores units v = UPW*kq .. +UPW-1 of row block rq
+            constexpr int UPW = 8 * PF / KS;
 #pragma unroll
-            for (int z = 0; z < 2 * PF; ++z) {
-                const int v = 2 * PF * kq + z;
+            for (int z = 0; z < UPW; ++z) {
+                const int v = UPW * kq + z;
                 const int j = v & 3, fr = (v >> 2) & 1, f = v >> 3;
-                const float4_t sum = ksum(4 * rq, f, fr, j);
+                const float4_t sum = ksum(KS * rq, f, fr, j);
                 const int m = m0 + 64 * rq + 32 * fr + l32;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -578,14 +611,16 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_sk(GemmArgs a) {
                 }
             }
         } else {
-            // 64 output rows: wave w takes units v = PF*w .. of the gate half,
-            // pairing each gate sum (waves 0-3) with the up sum (waves 4-7)
+            // BM/2 output rows in GB 64-row blocks: wave w takes units
+            // UD*w .. of the gate half, pairing each gate sum (row block gb,
+            // waves KS*gb ..) with the up sum of row block gb + GB
+            constexpr int GB = BM / 128, UD = GB * PF;
 #pragma unroll
-            for (int z = 0; z < PF; ++z) {
-                const int v = PF * wave + z;
+            for (int z = 0; z < UD; ++z) {
+                const int va = UD * wave + z, gb = va / (8 * PF), v = va % (8 * PF);
                 const int j = v & 3, fr = (v >> 2) & 1, f = v >> 3;
-                const float4_t gs = ksum(0, f, fr, j), us = ksum(4, f, fr, j);
-                const int m = m0 + 32 * fr + l32;
+                const float4_t gs = ksum(KS * gb, f, fr, j), us = ksum(KS * (gb + GB), f, fr, j);
+                const int m = m0 + 64 * gb + 32 * fr + l32;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int t = 32 * (pass * PF + f) + 8 * j + 4 * h + i;
@@ -596,19 +631,19 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_sk(GemmArgs a) {
     }
 }
 
-template <WF F, int BT, int MODE>
+template <WF F, int BT, int MODE, int BM = kBM>
 int launch_sk(const GemmArgs& a, unsigned nwg, hipStream_t stream) {
-    using R = Ring<F, BT>;
-    const void* fn = reinterpret_cast<const void*>(&gemm_sk<F, BT, MODE>);
+    using R = Ring<F, BT, BM>;
+    const void* fn = reinterpret_cast<const void*>(&gemm_sk<F, BT, MODE, BM>);
     if (int rc = prepare_lds(fn, R::kLds)) return rc;
-    hipLaunchKernelGGL((gemm_sk<F, BT, MODE>), dim3(nwg), dim3(kWaves * 64), R::kLds, stream, a);
+    hipLaunchKernelGGL((gemm_sk<F, BT, MODE, BM>), dim3(nwg), dim3(kWaves * 64), R::kLds, stream, a);
     return check_hip(hipGetLastError(), "prefill gemm launch");
 }
 
 // Dense GEMM over token chunks of at most 2^30 / mtiles tiles per launch.
-template <WF F, int BT>
+template <WF F, int BT, int BM = kBM>
 int dense_gemm(GemmArgs a, hipStream_t stream) {
-    const int64_t mtiles = (a.M + kBM - 1) / kBM;
+    const int64_t mtiles = (a.M + BM - 1) / BM;
     a.mtiles = static_cast<int>(mtiles);
     const int64_t tchunk = std::max<int64_t>(1, (int64_t(1) << 30) / mtiles) * BT;
     const int T = a.T;
@@ -620,26 +655,46 @@ int dense_gemm(GemmArgs a, hipStream_t stream) {
         a.y = y0 + t * a.ldy;
         a.T = tc;
         const unsigned nwg = static_cast<unsigned>(mtiles * ((tc + BT - 1) / BT));
-        if (int rc = launch_sk<F, BT, kDense>(a, nwg, stream)) return rc;
+        if (int rc = launch_sk<F, BT, kDense, BM>(a, nwg, stream)) return rc;
     }
     return GDSLLM_OK;
+}
+
+// Whether 256-row tiles beat 128-row ones at 128 tokens for `rows` weight
+// rows.  A 256-row tile gives each wave twice a 128-row tile's work (the same
+// wave tile over two blocks per stage) while the compute unit takes in 40%
+// fewer bytes per MFMA (X, the larger operand, feeds twice the rows), and the
+// kernel is bound by that intake at hundreds of tokens.  So the 256-row tile
+// pays when it takes at most half as many rounds of the CUs: 11008 rows at 512
+// tokens (1 round against 2; 83.5 -> 69.8 us for Q4_0 on MI355X) and 32000
+// rows (2 against 4; 180 -> 153 us), not the 22016 gate/up rows of the fused
+// gate/up/SiLU launch (2 against 3, measured no faster).
+inline bool rows256_pays(int64_t rows, int64_t T) {
+    const int64_t tt = (T + 127) / 128, cu = cu_count();
+    const int64_t r128 = ((rows + 127) / 128 * tt + cu - 1) / cu;
+    const int64_t r256 = ((rows + 255) / 256 * tt + cu - 1) / cu;
+    return 2 * r256 <= r128;
 }
 
 // A 128-token tile halves the dequant work and the X traffic per MFMA
 // (measured 1.35-1.4x on 11008 and 32000 rows at 512 tokens), but gives half
-// as many workgroups: it is taken only when it still fills every CU.
+// as many workgroups: it is taken only when it still fills every CU.  GGUF
+// weights may then take 256-row tiles (rows256_pays).
 template <WF F>
 int dense_gemm_auto(const GemmArgs& a, hipStream_t stream) {
     const int64_t mtiles = (a.M + kBM - 1) / kBM;
     const int64_t tiles128 = mtiles * ((a.T + 127) / 128);
-    return tiles128 >= cu_count() ? dense_gemm<F, 128>(a, stream) : dense_gemm<F, 64>(a, stream);
+    const int bt = tiles128 >= cu_count() ? 128 : 64;
+    if constexpr (!is_affine(F))
+        if (bt == 128 && rows256_pays(a.M, a.T)) return dense_gemm<F, 128, 2 * kBM>(a, stream);
+    return bt == 128 ? dense_gemm<F, 128>(a, stream) : dense_gemm<F, 64>(a, stream);
 }
 
-// Gate/up/SiLU over token chunks: 64 output rows per workgroup (gate rows in
+// Gate/up/SiLU over token chunks: BM/2 output rows per workgroup (gate rows in
 // one half, up rows in the other), the 128-token tile when it fills every CU.
-template <WF F, int BT>
+template <WF F, int BT, int BM = kBM>
 int dense_dual_gemm(GemmArgs a, hipStream_t stream) {
-    const int64_t mtiles = (a.M + 63) / 64;
+    const int64_t mtiles = (a.M + BM / 2 - 1) / (BM / 2);
     a.mtiles = static_cast<int>(mtiles);
     const int64_t tchunk = std::max<int64_t>(1, (int64_t(1) << 30) / mtiles) * BT;
     const int T = a.T;
@@ -651,15 +706,19 @@ int dense_dual_gemm(GemmArgs a, hipStream_t stream) {
         a.y = y0 + t * a.ldy;
         a.T = tc;
         const unsigned nwg = static_cast<unsigned>(mtiles * ((tc + BT - 1) / BT));
-        if (int rc = launch_sk<F, BT, kDenseDual>(a, nwg, stream)) return rc;
+        if (int rc = launch_sk<F, BT, kDenseDual, BM>(a, nwg, stream)) return rc;
     }
     return GDSLLM_OK;
 }
 
+// The gate/up rows of a 256-row tile (128 + 128) as for the dense GEMM.
 template <WF F>
 int dense_dual_gemm_auto(const GemmArgs& a, hipStream_t stream) {
     const int64_t tiles128 = (a.M + 63) / 64 * ((a.T + 127) / 128);
-    return tiles128 >= cu_count() ? dense_dual_gemm<F, 128>(a, stream) : dense_dual_gemm<F, 64>(a, stream);
+    const int bt = tiles128 >= cu_count() ? 128 : 64;
+    if constexpr (!is_affine(F))
+        if (bt == 128 && rows256_pays(2 * static_cast<int64_t>(a.M), a.T)) return dense_dual_gemm<F, 128, 2 * kBM>(a, stream);
+    return bt == 128 ? dense_dual_gemm<F, 128>(a, stream) : dense_dual_gemm<F, 64>(a, stream);
 }
 
 // ------------------------------------------------------------ MoE prefill --

@@ -321,8 +321,10 @@ int gdsllm_dequant_gemm_affine_q4(const void* weight, const void* scales, const 
                                   void* stream);
 /* The MLP input of a prefill chunk in one launch: h[t][r] =
  * fp16(fp16(silu(g)) * u) with g = fp16(sum_k x[t][k] * gate[r][k]) and u
- * likewise for up (GGUF Q4_0 / Q8_0 [ffn_dim][in_dim], the bits
- * gdsllm_dequant_gemm_* gives for each), torch's fp16 SiLU and product.
+ * likewise for up (GGUF Q4_0 / Q8_0 [ffn_dim][in_dim]; g and u are the bits
+ * gdsllm_dequant_gemm_* gives for each when both take the same row tile,
+ * else equal up to fp32 reassociation of each row's sum: 256-row tiles add
+ * two K halves, 128-row tiles four K quarters), torch's fp16 SiLU and product.
  * Replaces the reference's two prefill projections and its elementwise SiLU
  * (runtime/llama.py:253-256 over dequant_linear, llama.py:160-166); the
  * prefill form of gdsllm_fused_*_gate_up_silu.  in_dim % 256 == 0, weights

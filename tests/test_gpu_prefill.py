@@ -57,22 +57,57 @@ def test_dequant_gemm_affine_q4(gpu, T, M, K, g):
 
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
 def test_dequant_gemm_tile_width_keeps_bits(gpu, fmt):
-    """11008 rows at 512 tokens take the 128-token tile, 64 tokens the 64-token
+    """8192 rows at 512 tokens take the 128x128 tile, 64 tokens the 128x64
     tile: the same MFMA sequence per output, so the shared rows are equal bit
-    for bit (and within the GEMV tolerance of the oracle)."""
-    M, K = 11008, 4096
-    w = (syn.q4_0_weights if fmt == "q4_0" else syn.q8_0_weights)(M, K, gen(5400))
-    x = syn.activations(512, K, gen(5401))
+    for bit (and within the GEMV tolerance of the oracle).  11008 rows at 512
+    tokens take the 256-row tile, whose two K halves add the same products in
+    another order: within fp32 reassociation of the 64-token result (one fp16
+    ulp plus 2^-16 of ||w_r * x||)."""
+    K = 4096
+    for M in (8192, 11008):
+        w = (syn.q4_0_weights if fmt == "q4_0" else syn.q8_0_weights)(M, K, gen(5400 + M))
+        x = syn.activations(512, K, gen(5401))
+        wd, xd = w.to(gpu), x.to(gpu)
+        fn = capi().gdsllm_dequant_gemm_q4_0 if fmt == "q4_0" else capi().gdsllm_dequant_gemm_q8_0
+        y = torch.empty(512, M, dtype=torch.float16, device=gpu)
+        y64 = torch.empty(64, M, dtype=torch.float16, device=gpu)
+        check(fn(ptr(wd), ptr(xd), ptr(y), M, K, 512, K, M, stream()))
+        check(fn(ptr(wd), ptr(xd), ptr(y64), M, K, 64, K, M, stream()))
+        torch.cuda.synchronize()
+        deq = (oq.dequant_q4_0 if fmt == "q4_0" else oq.dequant_q8_0)(to_np(w)).reshape(M, K)
+        if M == 8192:
+            assert torch.equal(y[:64].view(torch.int16), y64.view(torch.int16)), "tile width changed the result"
+        else:
+            a, b = to_np(y)[:64].astype(np.float64), to_np(y64).astype(np.float64)
+            bound = oq.fp16_ulp(np.maximum(np.abs(a), np.abs(b))) + oq.row_norms(deq, to_np(x)[:64]) * 2.0 ** -16
+            bad = np.abs(a - b) > bound
+            assert not bad.any(), f"{int(bad.sum())} outputs apart beyond reassociation, first at {np.argwhere(bad)[0]}"
+        assert_gemv_close(to_np(y)[448:], deq, to_np(x)[448:], f"{fmt} gemm {M} rows, last token tile")
+
+
+# (T, M, K) that the planner gives 256-row tiles on a 256-CU MI355X (the
+# 128-row tiles would take two rounds of the CUs, these one): ragged last row
+# tile (10000 = 39 x 256 + 16, 12000 = 46 x 256 + 224), ragged last token
+# tile, one and four W groups.  Every case also holds on other CU counts: the
+# oracle checks whichever tile the planner takes.
+ROW256_CASES = [(512, 10000, 256), (500, 12000, 1024), (300, 12000, 1024)]
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("T,M,K", ROW256_CASES, ids=[f"T{t}_{m}x{k}" for t, m, k in ROW256_CASES])
+def test_dequant_gemm_256_row_tile(gpu, fmt, T, M, K):
+    w = (syn.q4_0_weights if fmt == "q4_0" else syn.q8_0_weights)(M, K, gen(5450 + M + K))
+    x = syn.activations(T, K, gen(5451 + T))
+    deq = (oq.dequant_q4_0 if fmt == "q4_0" else oq.dequant_q8_0)(to_np(w)).reshape(M, K)
     wd, xd = w.to(gpu), x.to(gpu)
     fn = capi().gdsllm_dequant_gemm_q4_0 if fmt == "q4_0" else capi().gdsllm_dequant_gemm_q8_0
-    y = torch.empty(512, M, dtype=torch.float16, device=gpu)
-    y64 = torch.empty(64, M, dtype=torch.float16, device=gpu)
-    check(fn(ptr(wd), ptr(xd), ptr(y), M, K, 512, K, M, stream()))
-    check(fn(ptr(wd), ptr(xd), ptr(y64), M, K, 64, K, M, stream()))
+    y = torch.full((T, M + 3), 7.0, dtype=torch.float16, device=gpu)
+    check(fn(ptr(wd), ptr(xd), ptr(y), M, K, T, K, M + 3, stream()))
     torch.cuda.synchronize()
-    assert torch.equal(y[:64].view(torch.int16), y64.view(torch.int16)), "tile width changed the result"
-    deq = (oq.dequant_q4_0 if fmt == "q4_0" else oq.dequant_q8_0)(to_np(w)).reshape(M, K)
-    assert_gemv_close(to_np(y)[448:], deq, to_np(x)[448:], f"{fmt} gemm last token tile")
+    yh = to_np(y)
+    rel, mx = assert_gemv_close(yh[:, :M].copy(), deq, to_np(x), f"{fmt} gemm T{T} {M}x{K}")
+    assert (yh[:, M:] == 7.0).all(), "columns past the rows were written"
+    print(f"{fmt} gemm 256-row tile T{T} {M}x{K}: rel={rel:.2e} max={mx:.2e}")
 
 
 @pytest.mark.parametrize("fmt", ["q8_0", "affine"])
@@ -334,16 +369,23 @@ def test_runtime_q8_0_prefill_projection(gpu):
 
 # (fmt, T, F, K): the 7B gate/up shape at a 512-token chunk (128-token tiles)
 # and at 64 tokens (64-token tiles), ragged rows and tokens, a short K
+# 6000 rows at 500-512 tokens: 128 + 128-row gate/up tiles on a 256-CU GPU
+# (one round of 188 tiles against two of 376), ragged last tile
 GATE_UP_CASES = [("q4_0", 512, 11008, 4096), ("q4_0", 64, 11008, 4096), ("q4_0", 7, 300, 256),
-                 ("q4_0", 100, 1000, 512), ("q8_0", 512, 11008, 4096), ("q8_0", 33, 260, 1024)]
+                 ("q4_0", 100, 1000, 512), ("q8_0", 512, 11008, 4096), ("q8_0", 33, 260, 1024),
+                 ("q4_0", 512, 6000, 1024), ("q8_0", 500, 6000, 512)]
 
 
 @pytest.mark.parametrize("fmt,T,F,K", GATE_UP_CASES, ids=[f"{f}_T{t}_{m}x{k}" for f, t, m, k in GATE_UP_CASES])
 def test_dequant_gemm_gate_up_silu(gpu, fmt, T, F, K):
     """h = fp16(fp16(silu(g)) * u) for a prefill chunk in one launch.  (1)
     Against g and u from the dense GEMM: within one fp16 ulp of silu times |u|
-    plus one ulp of h (the room the device's expf leaves against numpy's).
-    (2) End to end against the oracle's g and u: relative L2 of h."""
+    plus one ulp of h (the room the device's expf leaves against numpy's),
+    plus what fp32 reassociation of g and u allows (one fp16 ulp plus 2^-16
+    of ||w_r * x|| each, carried through silu (slope below 1.1) and the
+    product): the two launches may add a row's products in different orders
+    (128- or 256-row tiles, 2 or 4 K parts).  (2) End to end against the
+    oracle's g and u: relative L2 of h."""
     make = syn.q4_0_weights if fmt == "q4_0" else syn.q8_0_weights
     dq = oq.dequant_q4_0 if fmt == "q4_0" else oq.dequant_q8_0
     gemm = capi().gdsllm_dequant_gemm_q4_0 if fmt == "q4_0" else capi().gdsllm_dequant_gemm_q8_0
@@ -362,15 +404,20 @@ def test_dequant_gemm_gate_up_silu(gpu, fmt, T, F, K):
     hk = to_np(h).astype(np.float64)
     assert np.all(np.isfinite(hk)), "h not written everywhere"
     gn, un = to_np(g), to_np(u)
+    dg, du = dq(to_np(wg)).reshape(F, K), dq(to_np(wu)).reshape(F, K)
+    eg = oq.fp16_ulp(gn) + oq.row_norms(dg, to_np(x)) * 2.0 ** -16
+    eu = oq.fp16_ulp(un) + oq.row_norms(du, to_np(x)) * 2.0 ** -16
     sg = oq.silu_fp16(gn)
     href = (sg.astype(np.float32) * un.astype(np.float32)).astype(np.float16)
-    bound = oq.fp16_ulp(sg) * np.abs(un.astype(np.float64)) + oq.fp16_ulp(href)
+    ua, sa = np.abs(un.astype(np.float64)), np.abs(sg.astype(np.float64))
+    bound = (oq.fp16_ulp(sg) * ua + oq.fp16_ulp(href) + 1.1 * eg * (ua + eu) + sa * eu
+             + oq.fp16_ulp(sa + 1.1 * eg) * (ua + eu))
     bad = np.abs(hk - href.astype(np.float64)) > bound
     assert not bad.any(), f"{int(bad.sum())} of {bad.size} h values off; first at {np.argwhere(bad)[0]}"
     rows = np.arange(T) if T <= 64 else np.random.default_rng(T).choice(T, 64, replace=False)
     xr = to_np(x)[rows]
-    gq = oq.gemv(dq(to_np(wg)).reshape(F, K), xr).astype(np.float16)
-    uq = oq.gemv(dq(to_np(wu)).reshape(F, K), xr).astype(np.float16)
+    gq = oq.gemv(dg, xr).astype(np.float16)
+    uq = oq.gemv(du, xr).astype(np.float16)
     h_oracle = (oq.silu_fp16(gq).astype(np.float32) * uq.astype(np.float32)).astype(np.float64)
     rel = float(np.linalg.norm(hk[rows] - h_oracle) / np.linalg.norm(h_oracle))
     print(f"gate_up_silu {fmt} T{T} {F}x{K}: rel L2 {rel:.2e}")

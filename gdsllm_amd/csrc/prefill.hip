@@ -71,7 +71,7 @@ enum class WF { Q4_0, Q8_0, AFF32, AFF64, AFF128 };
 enum Mode { kDense = 0, kGather = 1, kDualSilu = 2, kDenseDual = 3 };
 
 constexpr int kWaves = 8;
-constexpr int kBM = 128;     // weight rows per workgroup (256 for the dense GGUF tile below)
+constexpr int kBM = 128;     // weight rows per workgroup (or 256: the GGUF tile of gemm_sk)
 constexpr int kStageK = 128; // k values per stage
 
 constexpr bool is_affine(WF f) { return f == WF::AFF32 || f == WF::AFF64 || f == WF::AFF128; }
@@ -156,7 +156,7 @@ struct GemmArgs {
 
 typedef float float16_t __attribute__((ext_vector_type(16)));
 
-// BM = 256 (dense GGUF only): the same 64-row x BT-token wave tile, with
+// BM = 256 (GGUF, dense and gate/up/SiLU): the same 64-row x BT-token wave tile, with
 // the workgroup's 8 waves as 4 row quarters x 2 K halves instead of 2 row
 // halves x 4 K quarters.  Each X stage then feeds twice the rows: per MFMA the
 // compute unit takes in 40% fewer bytes (X dominates them), which is what
@@ -174,7 +174,7 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_sk(GemmArgs a) {
     constexpr bool kGath = MODE == kGather || MODE == kDualSilu;
     constexpr bool kDual = MODE == kDualSilu || MODE == kDenseDual;
     static_assert(MODE != kDualSilu || Fm::kAff, "the gathered dual tiles are built for the affine pools");
-    static_assert(BM == kBM || MODE == kDense || MODE == kDenseDual, "the 256-row tile is dense only");
+    static_assert(BM == kBM || MODE == kDense || MODE == kDenseDual, "the 256-row tile serves the dense modes only");
     constexpr int KS = kWaves * 64 / BM;  // waves along K (4 or 2)
     constexpr int NSUB = 4 / KS;          // 32-value blocks per wave per stage
 

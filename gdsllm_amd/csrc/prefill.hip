@@ -71,7 +71,7 @@ enum class WF { Q4_0, Q8_0, AFF32, AFF64, AFF128 };
 enum Mode { kDense = 0, kGather = 1, kDualSilu = 2, kDenseDual = 3 };
 
 constexpr int kWaves = 8;
-constexpr int kBM = 128;     // weight rows per workgroup (or 256: the GGUF tile of gemm_sk)
+constexpr int kBM = 128;     // weight rows per workgroup (or 256: the dense tile of gemm_sk)
 constexpr int kStageK = 128; // k values per stage
 
 constexpr bool is_affine(WF f) { return f == WF::AFF32 || f == WF::AFF64 || f == WF::AFF128; }
@@ -79,7 +79,7 @@ constexpr int aff_group(WF f) { return f == WF::AFF32 ? 32 : f == WF::AFF64 ? 64
 
 // W slot geometry per format.
 //   SPS      stages per slot
-//   kSlot    bytes of one slot (BM rows; BM = 256 for GGUF only)
+//   kSlot    bytes of one slot (BM = 128 or 256 rows)
 //   kReal    transfers that carry data per slot; kCW per wave (dummies past kReal)
 //   GGUF: a 144-byte window per row (9 chunks): Q4_0 two stages (8 blocks of
 //   18 bytes); Q8_0 one stage (4 blocks of 34 = 136 bytes, starting 0 or 8
@@ -88,15 +88,16 @@ constexpr int aff_group(WF f) { return f == WF::AFF32 ? 32 : f == WF::AFF64 ? 64
 template <WF F, int BM = kBM>
 struct Fmt {
     static constexpr bool kAff = is_affine(F);
-    static_assert(BM == kBM || (BM == 2 * kBM && !kAff), "256-row slots hold GGUF windows only");
+    static_assert(BM == kBM || BM == 2 * kBM, "128- or 256-row slots");
     static constexpr int G = kAff ? aff_group(F) : 32;
     static constexpr int SPS = F == WF::Q8_0 ? 1 : 2;
     static constexpr int SB = kAff ? 512 / G : 0;                          // scale bytes per row per slot
     static constexpr bool kS16 = SB == 16;                                 // scales move in 16-byte transfers
-    static constexpr int kST = kAff ? (kS16 ? 2 : SB * kBM / 256) : 0;     // transfers for one of scales/biases
-    static constexpr int kSlot = kAff ? 16384 + 2 * kBM * SB : BM * 144;
-    static constexpr int kReal = kAff ? 16 + 2 * kST : BM * 144 / 1024;
-    static constexpr int kCW = kAff ? 3 : (kReal + kWaves - 1) / kWaves;  // transfers per wave per slot
+    static constexpr int kST = kAff ? (kS16 ? 2 * BM / kBM : SB * BM / 256) : 0;  // transfers for one of scales/biases
+    static constexpr int kWords = 128 * BM;                                // affine: bytes of words per slot
+    static constexpr int kSlot = kAff ? kWords + 2 * BM * SB : BM * 144;
+    static constexpr int kReal = kAff ? kWords / 1024 + 2 * kST : BM * 144 / 1024;
+    static constexpr int kCW = (kReal + kWaves - 1) / kWaves;              // transfers per wave per slot
     static_assert(kReal <= kCW * kWaves && kReal > (kCW - 1) * kWaves, "full rounds of transfers and a partial last");
 };
 
@@ -156,7 +157,7 @@ struct GemmArgs {
 
 typedef float float16_t __attribute__((ext_vector_type(16)));
 
-// BM = 256 (GGUF, dense and gate/up/SiLU): the same 64-row x BT-token wave tile, with
+// BM = 256 (the dense modes): the same 64-row x BT-token wave tile, with
 // the workgroup's 8 waves as 4 row quarters x 2 K halves instead of 2 row
 // halves x 4 K quarters.  Each X stage then feeds twice the rows: per MFMA the
 // compute unit takes in 40% fewer bytes (X dominates them), which is what
@@ -243,12 +244,14 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_sk(GemmArgs a) {
     const int64_t rb_sc = Fm::kAff ? 2 * (K / Fm::G) : 0;
     constexpr bool k2s16 = !Fm::kAff || Fm::kS16;  // ii = CW - 1 moves 16 bytes per lane (else 4)
     constexpr int L = CW - 1;  // the last transfer of a slot, partly dummies
+    // transfers per wave of GGUF blocks / affine words that are always data
+    constexpr int NWI = Fm::kAff ? 2 * BM / kBM : L;
     const uint8_t* wsrc[CW];   // tile base (row m0 of its matrix)
     uint32_t woff[CW];
     uint32_t wdst[CW];         // LDS offset inside the slot
-    bool real2 = true;
+    bool real[CW];             // false: a dummy transfer
 #pragma unroll
-    for (int ii = 0; ii < L; ++ii) {
+    for (int ii = 0; ii < NWI; ++ii) {
         const int i = 8 * ii + wave;
         int r, cp;
         if constexpr (!Fm::kAff) {
@@ -262,45 +265,50 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_sk(GemmArgs a) {
             r = g >> 3;
             cp = (g & 7) ^ (r & 7);
         }
-        const bool second = kDual && i >= (Fm::kAff ? 8 : Fm::kReal / 2);  // up rows BM/2 .. BM-1
+        const bool second = kDual && i >= (Fm::kAff ? 8 * NWI / 2 : Fm::kReal / 2);  // up rows BM/2 .. BM-1
         const int rr = second ? r - BM / 2 : r;
         const int ra = min(m0 + rr, M - 1) - m0;
         wsrc[ii] = (second ? wB : wA) + static_cast<int64_t>(m0) * rb_main;
         woff[ii] = static_cast<uint32_t>(ra * rb_main + 16 * cp);
         wdst[ii] = 1024 * i;
+        real[ii] = true;
     }
     if constexpr (!Fm::kAff) {
         const int i = 8 * L + wave;
-        real2 = i < Fm::kReal;
+        real[L] = i < Fm::kReal;
         const int g = 64 * i + lane, r = g / 9, cp = g % 9;
         const bool second = kDual;  // rows past BM/2
         const int rr = second ? r - BM / 2 : r;
         const int ra = min(m0 + rr, M - 1) - m0;
         wsrc[L] = (second ? wB : wA) + static_cast<int64_t>(m0) * rb_main;
-        woff[L] = real2 ? static_cast<uint32_t>(ra * rb_main + 16 * cp) : 0u;
+        woff[L] = real[L] ? static_cast<uint32_t>(ra * rb_main + 16 * cp) : 0u;
         wdst[L] = 1024 * i;
     } else {
-        const int j0 = wave;
-        real2 = j0 < 2 * Fm::kST;
-        const bool isb = j0 >= Fm::kST;
-        const int j = isb ? j0 - Fm::kST : j0;
-        const bool second = kDual && j >= Fm::kST / 2;
-        const uint8_t* base = isb ? (second ? bB : bA) : (second ? sB : sA);
-        int r, inrow;
-        if constexpr (Fm::kS16) {
-            r = 64 * j + lane;
-            inrow = 0;
-            wdst[L] = 16384 + (isb ? kBM * Fm::SB : 0) + 1024 * j;
-        } else {
-            const int d = 64 * j + lane, per = Fm::SB / 4;
-            r = d / per;
-            inrow = 4 * (d % per);
-            wdst[L] = 16384 + (isb ? kBM * Fm::SB : 0) + 256 * j;
+        // scales then biases: transfer j0 = 8 (ii - NWI) + wave of the 2 kST
+#pragma unroll
+        for (int ii = NWI; ii < CW; ++ii) {
+            const int j0 = 8 * (ii - NWI) + wave;
+            real[ii] = j0 < 2 * Fm::kST;
+            const bool isb = j0 >= Fm::kST;
+            const int j = isb ? j0 - Fm::kST : j0;
+            const bool second = kDual && j >= Fm::kST / 2;
+            const uint8_t* base = isb ? (second ? bB : bA) : (second ? sB : sA);
+            int r, inrow;
+            if constexpr (Fm::kS16) {
+                r = 64 * j + lane;
+                inrow = 0;
+                wdst[ii] = Fm::kWords + (isb ? BM * Fm::SB : 0) + 1024 * j;
+            } else {
+                const int d = 64 * j + lane, per = Fm::SB / 4;
+                r = d / per;
+                inrow = 4 * (d % per);
+                wdst[ii] = Fm::kWords + (isb ? BM * Fm::SB : 0) + 256 * j;
+            }
+            const int rr = second ? r - BM / 2 : r;
+            const int ra = min(m0 + rr, M - 1) - m0;
+            wsrc[ii] = (real[ii] ? base : sA) + static_cast<int64_t>(m0) * rb_sc;
+            woff[ii] = real[ii] ? static_cast<uint32_t>(ra * rb_sc + inrow) : 0u;
         }
-        const int rr = second ? r - 64 : r;
-        const int ra = min(m0 + rr, M - 1) - m0;
-        wsrc[L] = (real2 ? base : sA) + static_cast<int64_t>(m0) * rb_sc;
-        woff[L] = real2 ? static_cast<uint32_t>(ra * rb_sc + inrow) : 0u;
     }
     // byte offset of group gi inside a row: GGUF blocks / affine words
     auto goff_main = [&](int gi) -> int64_t {
@@ -331,11 +339,14 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_sk(GemmArgs a) {
         const int gc = gi < ngr ? gi : ngr - 1;
         const int64_t om = goff_main(gc);
 #pragma unroll
-        for (int ii = 0; ii < L; ++ii) dma16_asm(woff[ii], wsrc[ii] + om, slot + wdst[ii]);
+        for (int ii = 0; ii < NWI; ++ii) dma16_asm(woff[ii], wsrc[ii] + om, slot + wdst[ii]);
         const int64_t o2 = Fm::kAff ? static_cast<int64_t>(Fm::SB) * gc : om;
-        const uint32_t d2 = real2 ? slot + wdst[L] : lds0 + R::kDummy;
-        if constexpr (k2s16) dma16_asm(woff[L], wsrc[L] + o2, d2);
-        else dma4_asm(woff[L], wsrc[L] + o2, d2);
+#pragma unroll
+        for (int ii = NWI; ii < CW; ++ii) {
+            const uint32_t d2 = real[ii] ? slot + wdst[ii] : lds0 + R::kDummy;
+            if constexpr (k2s16) dma16_asm(woff[ii], wsrc[ii] + o2, d2);
+            else dma4_asm(woff[ii], wsrc[ii] + o2, d2);
+        }
     };
     auto floordiv = [](int v, int d) { return v >= 0 ? v / d : -((-v + d - 1) / d); };
     auto issue_stage = [&](int s) {
@@ -412,9 +423,9 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_sk(GemmArgs a) {
                 o.q[fr][0] = *reinterpret_cast<const uint32_t*>(chunk + 4 * h);
                 o.q[fr][1] = *reinterpret_cast<const uint32_t*>(chunk + 4 * h + 8);
                 const int gi = (128 * (u & 1) + 32 * kb) / Fm::G;
-                const uint8_t* sp = ws + 16384 + Fm::SB * rt + 2 * gi;
+                const uint8_t* sp = ws + Fm::kWords + Fm::SB * rt + 2 * gi;
                 o.d[fr][0] = *reinterpret_cast<const uint16_t*>(sp);
-                o.d[fr][1] = *reinterpret_cast<const uint16_t*>(sp + kBM * Fm::SB);
+                o.d[fr][1] = *reinterpret_cast<const uint16_t*>(sp + BM * Fm::SB);
             }
         }
     };
@@ -678,15 +689,14 @@ inline bool rows256_pays(int64_t rows, int64_t T) {
 
 // A 128-token tile halves the dequant work and the X traffic per MFMA
 // (measured 1.35-1.4x on 11008 and 32000 rows at 512 tokens), but gives half
-// as many workgroups: it is taken only when it still fills every CU.  GGUF
-// weights may then take 256-row tiles (rows256_pays).
+// as many workgroups: it is taken only when it still fills every CU.  It may
+// then take 256-row tiles (rows256_pays).
 template <WF F>
 int dense_gemm_auto(const GemmArgs& a, hipStream_t stream) {
     const int64_t mtiles = (a.M + kBM - 1) / kBM;
     const int64_t tiles128 = mtiles * ((a.T + 127) / 128);
     const int bt = tiles128 >= cu_count() ? 128 : 64;
-    if constexpr (!is_affine(F))
-        if (bt == 128 && rows256_pays(a.M, a.T)) return dense_gemm<F, 128, 2 * kBM>(a, stream);
+    if (bt == 128 && rows256_pays(a.M, a.T)) return dense_gemm<F, 128, 2 * kBM>(a, stream);
     return bt == 128 ? dense_gemm<F, 128>(a, stream) : dense_gemm<F, 64>(a, stream);
 }
 

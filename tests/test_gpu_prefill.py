@@ -93,16 +93,25 @@ def test_dequant_gemm_tile_width_keeps_bits(gpu, fmt):
 ROW256_CASES = [(512, 10000, 256), (500, 12000, 1024), (300, 12000, 1024)]
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0", "affine32", "affine64", "affine128"])
 @pytest.mark.parametrize("T,M,K", ROW256_CASES, ids=[f"T{t}_{m}x{k}" for t, m, k in ROW256_CASES])
 def test_dequant_gemm_256_row_tile(gpu, fmt, T, M, K):
-    w = (syn.q4_0_weights if fmt == "q4_0" else syn.q8_0_weights)(M, K, gen(5450 + M + K))
     x = syn.activations(T, K, gen(5451 + T))
-    deq = (oq.dequant_q4_0 if fmt == "q4_0" else oq.dequant_q8_0)(to_np(w)).reshape(M, K)
-    wd, xd = w.to(gpu), x.to(gpu)
-    fn = capi().gdsllm_dequant_gemm_q4_0 if fmt == "q4_0" else capi().gdsllm_dequant_gemm_q8_0
+    xd = x.to(gpu)
     y = torch.full((T, M + 3), 7.0, dtype=torch.float16, device=gpu)
-    check(fn(ptr(wd), ptr(xd), ptr(y), M, K, T, K, M + 3, stream()))
+    if fmt.startswith("affine"):
+        g = int(fmt[6:])
+        words, scales, biases = syn.affine_q4_weights([M, K], g, gen(5452 + M + g))
+        deq = affine_dequant_np(words, scales, biases, g).reshape(M, K)
+        wd, sd, bd = words.to(gpu), scales.to(gpu), biases.to(gpu)
+        check(capi().gdsllm_dequant_gemm_affine_q4(ptr(wd), ptr(sd), ptr(bd), ptr(xd), ptr(y), M, K, g, T, K, M + 3,
+                                                   stream()))
+    else:
+        w = (syn.q4_0_weights if fmt == "q4_0" else syn.q8_0_weights)(M, K, gen(5450 + M + K))
+        deq = (oq.dequant_q4_0 if fmt == "q4_0" else oq.dequant_q8_0)(to_np(w)).reshape(M, K)
+        wd = w.to(gpu)
+        fn = capi().gdsllm_dequant_gemm_q4_0 if fmt == "q4_0" else capi().gdsllm_dequant_gemm_q8_0
+        check(fn(ptr(wd), ptr(xd), ptr(y), M, K, T, K, M + 3, stream()))
     torch.cuda.synchronize()
     yh = to_np(y)
     rel, mx = assert_gemv_close(yh[:, :M].copy(), deq, to_np(x), f"{fmt} gemm T{T} {M}x{K}")

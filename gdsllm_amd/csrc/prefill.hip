@@ -219,7 +219,10 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_sk(GemmArgs a) {
 
     // ---- X sources: transfer i of this wave (i = NX*wave + ii) fills 16-byte
     // slot 64i + l of a stage tile: token 4i + l/16, chunk (l & 15) ^ (token & 15).
-    // Tokens past the tile read its last token.
+    // Tokens past the tile read its last token.  The lane offsets are 32-bit:
+    // the dense modes put the tile's first token into the 64-bit base (the
+    // in-tile offsets stay below 2 * 128 * 2^24 bytes), the gathered modes
+    // address whole rows of an X their entry point bounds below 4 GiB.
     uint32_t xoff[NX];
 #pragma unroll
     for (int ii = 0; ii < NX; ++ii) {
@@ -228,10 +231,10 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_sk(GemmArgs a) {
         const int tl = t < nt ? t : nt - 1;
         int64_t row;
         if constexpr (kGath) row = a.tok ? a.tok[p0 + tl] : p0 + tl;  // no list: X rows are the positions
-        else row = t0 + tl;
+        else row = tl;
         xoff[ii] = static_cast<uint32_t>(2 * (row * a.ldx + 8 * c));
     }
-    const uint16_t* xbase = a.x;
+    const uint16_t* xbase = kGath ? a.x : a.x + static_cast<int64_t>(t0) * a.ldx;
 
     // ---- W sources.  Transfer i = 8*ii + wave of a slot (ii < CW: 3, or 5 for
     // the 256-row GGUF slot).  ii < CW - 1 are 16-byte transfers of GGUF
@@ -961,6 +964,16 @@ int check_dense(const std::string& n, const void* weight, const void* x, const v
     return GDSLLM_OK;
 }
 
+// The weight transfers address the rows of a tile (up to 256) by 32-bit
+// offsets from the tile's first row: Q8_0 rows (in_dim * 34 / 32 bytes) must
+// keep 255 rows + one stage within 4 GiB (in_dim below 15,852,288).
+int check_q8_rows(const std::string& n, int64_t in_dim) {
+    if (255 * (in_dim / 32 * 34) + 1024 >= (int64_t(1) << 32))
+        return set_error(GDSLLM_ERR_UNSUPPORTED, n + ": Q8_0 in_dim too large for the MFMA GEMM, got " +
+                                                     std::to_string(in_dim));
+    return GDSLLM_OK;
+}
+
 int off_grid(const std::string& n, int64_t in_dim) {
     return set_error(GDSLLM_ERR_UNSUPPORTED,
                      n + ": in_dim must be a multiple of 256 for the MFMA GEMM, got " + std::to_string(in_dim));
@@ -995,6 +1008,7 @@ extern "C" int gdsllm_dequant_gemm_q8_0(const void* weight, const void* x, void*
     if (int rc = check_dense("dequant_gemm_q8_0", weight, x, y, out_dim, in_dim, tokens, ldx, ldy, empty)) return rc;
     if (empty) return ok();
     if (in_dim % 256 != 0) return off_grid("dequant_gemm_q8_0", in_dim);
+    if (int rc = check_q8_rows("dequant_gemm_q8_0", in_dim)) return rc;
     return run_dense<WF::Q8_0>(weight, nullptr, nullptr, x, y, out_dim, in_dim, tokens, ldx, ldy, stream);
 }
 
@@ -1113,6 +1127,8 @@ int gate_up_silu_entry(const std::string& n, const void* gate, const void* up, c
     if (reinterpret_cast<uintptr_t>(up) % 16)
         return set_error(GDSLLM_ERR_UNSUPPORTED, n + ": weight and x rows must be 16-byte aligned (ldx % 8 == 0)");
     if (in_dim % 256 != 0) return off_grid(n, in_dim);
+    if (F == WF::Q8_0)
+        if (int rc = check_q8_rows(n, in_dim)) return rc;
     GemmArgs a{};
     a.w = static_cast<const uint8_t*>(gate);
     a.w2 = static_cast<const uint8_t*>(up);

@@ -8,7 +8,9 @@ the same contract:
   * decode with batch > 1 (x [B, 1, K], B <= 8) runs one batched fused GEMV
     instead of failing the reference's x.view(-1) size check;
   * Q4_0 and Q8_0 prefill run the fused MFMA dequant-GEMM instead of
-    dequant + GEMM (the dequant route stays for shapes it does not serve);
+    dequant + GEMM where that is faster (prefill_takes_fused_gemm: chunks of
+    up to 512 tokens over matrices of 2048 rows or more); the dequant route
+    stays for the other chunks and for shapes the kernel does not serve;
   * per-column int8 weights (runtime/llama.py:162-165) go through
     gds_io_ext.int8_linear: a fused GEMV at decode, a bit-exact dequant and one
     GEMM at prefill, instead of an fp32 copy of the whole matrix per call.
@@ -46,6 +48,28 @@ def _fused_dequant_gemv(x: torch.Tensor, meta: dict) -> torch.Tensor:
     return out.unsqueeze(1)
 
 
+# Measured on MI355X (Q4_0 and Q8_0, LLaMA-7B/70B projection shapes, 64 to
+# 2048 tokens), fused MFMA dequant-GEMM against the bit-exact dequant into a
+# scratch matrix + hipBLASLt: the fused GEMM wins up to 512 tokens (11008 x
+# 4096 Q4_0 at 512: 69 against 73 us; 28672 x 8192 at 128: 108 against 235
+# us) and loses from 1024 on (11008 x 4096 Q4_0 at 2048: 217 against 182 us;
+# it dequantizes every weight once per 128-token tile, the route once per
+# call), on matrices under 2048 rows (1024 x 8192 at 512: 51 against 39 us)
+# and where its tiles leave most compute units idle (4096 x 11008 at 64
+# tokens: 32 tiles, 63 against 53 us).
+FUSED_GEMM_MAX_TOKENS = 512
+FUSED_GEMM_MIN_ROWS = 2048
+FUSED_GEMM_MIN_TILES = 64  # 128-row x 64-token tiles
+
+
+def prefill_takes_fused_gemm(out_dim: int, tokens: int) -> bool:
+    """Whether a prefill projection of `tokens` rows of x onto `out_dim` rows
+    of quantized weights takes the fused MFMA dequant-GEMM (else dequant +
+    F.linear)."""
+    tiles = -(-out_dim // 128) * -(-tokens // 64)
+    return tokens <= FUSED_GEMM_MAX_TOKENS and out_dim >= FUSED_GEMM_MIN_ROWS and tiles >= FUSED_GEMM_MIN_TILES
+
+
 def _fused_dequant_gemm(x: torch.Tensor, meta: dict) -> Optional[torch.Tensor]:
     """Prefill Q4_0 / Q8_0 projection on the MFMA dequant-GEMM: (B, S, K) ->
     (B, S, M); None for a shape or alignment the kernels do not serve."""
@@ -60,9 +84,10 @@ def dequant_linear(
     if isinstance(w, dict) and "gguf_type" in w:
         if x.shape[1] == 1 and x.shape[0] <= 8:
             return _fused_dequant_gemv(x, w)
-        out = _fused_dequant_gemm(x, w)
-        if out is not None:
-            return out
+        if prefill_takes_fused_gemm(int(w["shape"][0]), x.numel() // x.shape[-1]):
+            out = _fused_dequant_gemm(x, w)
+            if out is not None:
+                return out
         w = _dequant_gguf(w, scratch)
     elif w.dtype == torch.int8:
         # per-column int8: fused GEMV for up to 8 rows of x, else the bit-exact

@@ -23,6 +23,7 @@ import torch
 import torch.nn.functional as F
 
 from . import ext
+from .llama import prefill_takes_fused_gemm
 
 
 def _dequant_affine_q4(meta: dict, scratch: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -53,11 +54,13 @@ def _fused_affine_q4_gemm(x: torch.Tensor, meta: dict) -> Optional[torch.Tensor]
 
 
 def _affine_linear(x: torch.Tensor, meta: dict, scratch: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """F.linear(x, dequant(meta)) for a prefill chunk: the fused GEMM, else the
+    """F.linear(x, dequant(meta)) for a prefill chunk: the fused GEMM where it
+    is the faster route (llama.prefill_takes_fused_gemm), else the
     reference's dequant -> F.linear (runtime/qwen_moe.py:72-73)."""
-    out = _fused_affine_q4_gemm(x, meta)
-    if out is not None:
-        return out
+    if prefill_takes_fused_gemm(int(meta["shape"][0]), x.numel() // x.shape[-1]):
+        out = _fused_affine_q4_gemm(x, meta)
+        if out is not None:
+            return out
     return F.linear(x, _dequant_affine_q4(meta, scratch))
 
 

@@ -145,6 +145,62 @@ def test_dequant_gemm_strided(gpu, fmt):
     assert (yh[:, M:] == 7.0).all(), "padding columns of y were written"
 
 
+BIG_X_FMTS = ["q4_0", "q8_0", "affine64", "gate_up_q4_0"]
+
+
+@pytest.mark.parametrize("fmt", BIG_X_FMTS)
+def test_dequant_gemm_x_beyond_4gib(gpu, fmt):
+    """x rows 2^23 elements apart over 300 tokens (5 GB): token tiles past
+    4 GiB of x read their own rows.  The outputs equal bit for bit those of
+    the same call on a compact copy of x (the same tiles and products), and
+    sampled rows are checked against the oracle."""
+    T, M, K, g = 300, 256, 4096, 64
+    ldx = 1 << 23
+    x = syn.activations(T, K, gen(5700))
+    xbig = torch.empty(T, ldx, dtype=torch.float16, device=gpu)
+    assert xbig.numel() * 2 > (1 << 32)
+    xbig[:, :K].copy_(x.to(gpu))
+    xd = x.to(gpu)
+    y_big = torch.full((T, M), float("nan"), dtype=torch.float16, device=gpu)
+    y_ref = torch.full((T, M), float("nan"), dtype=torch.float16, device=gpu)
+    if fmt in ("q4_0", "q8_0", "gate_up_q4_0"):
+        make = syn.q8_0_weights if fmt == "q8_0" else syn.q4_0_weights
+        w = make(M, K, gen(5701))
+        wd = w.to(gpu)
+        deq = (oq.dequant_q8_0 if fmt == "q8_0" else oq.dequant_q4_0)(to_np(w)).reshape(M, K)
+        if fmt == "gate_up_q4_0":
+            wu = syn.q4_0_weights(M, K, gen(5702))
+            wud = wu.to(gpu)
+            fn = capi().gdsllm_dequant_gemm_gate_up_silu_q4_0
+            for xx, lx, yy in ((xbig, ldx, y_big), (xd, K, y_ref)):
+                check(fn(ptr(wd), ptr(wud), ptr(xx), ptr(yy), M, K, T, lx, M, stream()))
+        else:
+            fn = capi().gdsllm_dequant_gemm_q8_0 if fmt == "q8_0" else capi().gdsllm_dequant_gemm_q4_0
+            for xx, lx, yy in ((xbig, ldx, y_big), (xd, K, y_ref)):
+                check(fn(ptr(wd), ptr(xx), ptr(yy), M, K, T, lx, M, stream()))
+    else:
+        words, scales, biases = syn.affine_q4_weights([M, K], g, gen(5703))
+        deq = affine_dequant_np(words, scales, biases, g).reshape(M, K)
+        wd, sd, bd = words.to(gpu), scales.to(gpu), biases.to(gpu)
+        for xx, lx, yy in ((xbig, ldx, y_big), (xd, K, y_ref)):
+            check(capi().gdsllm_dequant_gemm_affine_q4(ptr(wd), ptr(sd), ptr(bd), ptr(xx), ptr(yy), M, K, g, T, lx, M,
+                                                       stream()))
+    torch.cuda.synchronize()
+    del xbig
+    assert torch.equal(y_big.view(torch.int16), y_ref.view(torch.int16)), "x beyond 4 GiB changed the result"
+    rows = np.array([0, 1, 63, 64, 127, 128, 191, 192, 255, 256, 299])
+    if fmt == "gate_up_q4_0":
+        du = oq.dequant_q4_0(to_np(wu)).reshape(M, K)
+        xr = to_np(x)[rows]
+        gq = oq.gemv(deq, xr).astype(np.float16)
+        uq = oq.gemv(du, xr).astype(np.float16)
+        h = (oq.silu_fp16(gq).astype(np.float32) * uq.astype(np.float32)).astype(np.float64)
+        rel = float(np.linalg.norm(to_np(y_big)[rows].astype(np.float64) - h) / np.linalg.norm(h))
+        assert rel <= oq.GEMV_REL_L2, f"h rel L2 {rel:.3e}"
+    else:
+        assert_gemv_close(to_np(y_big)[rows].copy(), deq, to_np(x)[rows].copy(), f"{fmt} gemm, x beyond 4 GiB")
+
+
 def test_dequant_gemm_unsupported_shapes(gpu):
     """Shapes off the MFMA kernels' grid are refused as unsupported (the caller
     keeps the dequant route), before any launch."""
@@ -154,6 +210,10 @@ def test_dequant_gemm_unsupported_shapes(gpu):
     assert capi().gdsllm_dequant_gemm_affine_q4(ptr(y), ptr(y), ptr(y), ptr(y), ptr(y), 4, 256, 256, 2, 256, 4,
                                                 stream()) == 2
     assert b"group_size" in capi().gdsllm_last_error()
+    # Q8_0 rows whose 32-bit in-tile offsets would pass 4 GiB (in_dim from 15,852,288 on)
+    big_k = 15_852_288
+    assert capi().gdsllm_dequant_gemm_q8_0(ptr(y), ptr(y), ptr(y), 256, big_k, 2, big_k, 256, stream()) == 2
+    assert b"in_dim too large" in capi().gdsllm_last_error()
 
 
 # ------------------------------------------------------------ MoE prefill --
@@ -361,11 +421,13 @@ def test_runtime_moe_prefill_matches_per_expert_route(gpu, tmp_path):
 
 
 def test_runtime_q8_0_prefill_projection(gpu):
-    """dequant_linear on a Q8_0 weight with a prefill chunk takes the MFMA GEMM."""
+    """dequant_linear on a Q8_0 weight with a prefill chunk the MFMA GEMM
+    serves faster (4096 rows, 128 tokens: 64 tiles) takes it."""
     from gdsllm_amd.runtime import ext
     from gdsllm_amd.runtime import llama
 
-    M, K, T = 1024, 4096, 48
+    M, K, T = 4096, 4096, 128
+    assert llama.prefill_takes_fused_gemm(M, T)
     w = syn.q8_0_weights(M, K, gen(6000))
     handle = ext().GdsBufferHandle.from_tensor(w.reshape(-1).to(gpu))
     meta = {"buffer": handle, "shape": [M, K], "gguf_type": "q8_0", "offset": 0}

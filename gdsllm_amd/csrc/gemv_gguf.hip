@@ -548,6 +548,9 @@ struct RowsTarget {
     int m[kMaxGroup];
     int gb_end[kMaxGroup];  // groups: workgroups [gb_end[i-1], gb_end[i]) serve matrix i
     int n;
+    // 1: a wave issues its next stage after consuming the whole current one
+    // (waves that share a SIMD); 0: rows 0-1's slots as soon as they are read
+    int late_issue;
 };
 
 // One stage: stage row 0 of window super-block sb0 starts at base0 (pairing:
@@ -828,12 +831,26 @@ __global__ __launch_bounds__(WV * 64) void gguf_gemv_rows(const RowsTarget targe
         // across rows.
         const bool active = lane < st.nsb * 4;
         const RowsStage nx = stage_at(t + 1);
-        auto consume = [&](auto exact_c) {
+        auto consume = [&](auto exact_c, auto late_c) {
             constexpr bool EX = decltype(exact_c)::value;
             wait_vmcnt<C - kRowDone[0]>();
             if (active) rows_pair_impl<F, NB, 0, 1, EX>(buf, xs, acc, nu, lane);
             wait_vmcnt<C - kRowDone[1]>();
             if (active) rows_pair_impl<F, NB, 1, 1, EX>(buf, xs, acc, nu, lane);
+            if constexpr (decltype(late_c)::value) {
+                // the next stage goes out once this one is read: a wave that
+                // would wait for room in the request queue does so after its
+                // products (7B gate/up and lm_head: 11.7 -> 11.3 and 13.9 ->
+                // 13.7 us; the 4096 x 11008 down projection, one wave per
+                // SIMD, is faster with the early refill)
+                wait_vmcnt<C - kRowDone[2]>();
+                if (active) rows_pair_impl<F, NB, 2, 1, EX>(buf, xs, acc, nu, lane);
+                wait_vmcnt<0>();
+                if (active) rows_pair_impl<F, NB, 3, 1, EX>(buf, xs, acc, nu, lane);
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                if (next) rows_issue<F, 0, C, PAIRED>(buf, nx, X, row_bytes, goff, true, lane);
+                return;
+            }
             // refill slots of rows 0-1 once their reads have returned
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             if (next) {
@@ -850,10 +867,13 @@ __global__ __launch_bounds__(WV * 64) void gguf_gemv_rows(const RowsTarget targe
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             if (next) rows_issue<F, kEarly, C, PAIRED>(buf, nx, X, row_bytes, goff, true, lane);
         };
-        if (kRowsExact && xs.exact)
-            consume(std::true_type{});
-        else
-            consume(std::false_type{});
+        if (target.late_issue) {
+            if (kRowsExact && xs.exact) consume(std::true_type{}, std::true_type{});
+            else consume(std::false_type{}, std::true_type{});
+        } else {
+            if (kRowsExact && xs.exact) consume(std::true_type{}, std::false_type{});
+            else consume(std::false_type{}, std::false_type{});
+        }
         if constexpr (SW) {
             // this window's four row sums; written with raw LDS stores (a
             // compiler-visible one would wait for the transfers in flight)
@@ -1982,6 +2002,10 @@ bool plan_rows(RowsTarget& tg, int K, int& grid, int& wv, int& tmax) {
             }
         }
     }
+    // late next-stage issue where it measured faster: gate/up pairs (three
+    // 4-wave workgroups per CU) and 8-wave plans; not for 8192 x 8192 (two
+    // per CU: 8.94 -> 9.24 us) or single workgroups per CU
+    tg.late_issue = MODE == 2 || wv >= 8 ? 1 : 0;
     return grid > 0;
 }
 

@@ -1032,6 +1032,92 @@ def cpu_baseline(weights_dev, x_dev, y_gpu, seconds: float):
         "ok": bool(rel <= oq.GEMV_REL_L2 and mx <= oq.GEMV_MAX_NORM)}
 
 
+CPU_ROW_CAP = 4096  # rows of one matrix timed on the host; the time scales linearly with rows
+
+
+def _q8_bytes(m: int, k: int) -> int:
+    return m * (k // 32) * 34
+
+
+def cpu_baseline_configs(seconds_per_shape: float) -> dict:
+    """The CPU restatement of the reference's route (bit-exact dequant, then
+    F.linear in fp32; oracle/cpu_baseline.py) for the other workloads, each
+    as dequant-only and dequant + GEMV time and GB/s over the GPU's
+    algorithmic bytes: the Q8_0 LLaMA-7B layer (7 GEMVs), the top-10
+    affine-Q4 expert gather (the reference's per-expert decode loop,
+    runtime/qwen_moe.py:455-474), the Q4_0 LLaMA-70B layer at batch 1, and
+    the LLaMA-7B Q4_0 decode sweep as the sum of its 224 + 1 GEMVs.  Each
+    distinct matrix shape is timed once (median of >= 10 runs after 2
+    warm-ups, at most CPU_ROW_CAP rows, the time scaled by rows / timed rows)
+    and the shapes are summed with their counts.  Runs on the threads the
+    caller has set."""
+    import torch
+
+    from gdsllm_amd import synthetic as syn
+    from oracle import cpu_baseline as cb
+
+    gen = torch.Generator().manual_seed(1050)
+    cache = {}
+
+    def shape_s(kind, m, k):
+        if (kind, m, k) in cache:
+            return cache[(kind, m, k)]
+        r = min(m, CPU_ROW_CAP)
+        x = syn.activations(1, k, gen)
+        if kind == "q4_0":
+            w = syn.q4_0_weights(r, k, gen)
+            dq, tot = (lambda: cb.dequant_q4_0(w)), (lambda: cb.q4_0_gemv(w, x, r, k))
+        else:
+            w = syn.q8_0_weights(r, k, gen)
+            dq, tot = (lambda: cb.dequant_q8_0(w)), (lambda: cb.q8_0_gemv(w, x, r, k))
+        d_s, _ = _median_s(dq, seconds_per_shape / 3)
+        t_s, _ = _median_s(tot, seconds_per_shape * 2 / 3)
+        cache[(kind, m, k)] = (d_s * m / r, t_s * m / r)
+        return cache[(kind, m, k)]
+
+    def layer(kind, shapes):
+        d = sum(shape_s(kind, m, k)[0] for m, k in shapes)
+        t = sum(shape_s(kind, m, k)[1] for m, k in shapes)
+        return d, t
+
+    def entry(d_s, t_s, nbytes, **extra):
+        return {"us": round(t_s * 1e6, 1), "GB_s": round(nbytes / t_s / 1e9, 3),
+                "dequant_only_us": round(d_s * 1e6, 1), "dequant_only_GB_s": round(nbytes / d_s / 1e9, 3),
+                "algorithmic_bytes": nbytes, **extra}
+
+    out = {}
+    d, t = layer("q8_0", LAYER_SHAPES)
+    out["q8_0_layer_7b_b1"] = entry(d, t, sum(_q8_bytes(m, k) + 2 * k + 2 * m for m, k in LAYER_SHAPES))
+    # top-10 expert gather: the selected experts' matrices only (what the loop reads)
+    E, H, Fd, g, k = 10, 4096, 1024, 64, 10
+    pools = [syn.affine_q4_weights(sh, g, gen) for sh in ([E, Fd, H], [E, Fd, H], [E, H, Fd])]
+    xm = syn.activations(1, H, gen)
+    wts = torch.softmax(torch.randn(k, generator=gen), 0).to(torch.float16)
+    idx = list(range(k))
+    def dq_moe():
+        for p in pools:
+            for e in idx:
+                cb.dequant_affine_q4(p[0][e], p[1][e], p[2][e], g)
+
+    gather = lambda: cb.moe_gather_decode(*pools, xm, idx, wts, g)  # noqa: E731
+    for _ in range(3):  # the allocator's first passes over these temporaries are slower
+        dq_moe()
+        gather()
+    d_s, _ = _median_s(dq_moe, seconds_per_shape / 3)
+    t_s, _ = _median_s(gather, seconds_per_shape * 2 / 3)
+    out["moe_affine_q4_top10"] = entry(d_s, t_s, MOE_GATE_UP_BYTES + MOE_DOWN_BYTES - 10 * 1024 * 2 + 4096 * 2)
+    d, t = layer("q4_0", LAYER_70B)
+    out["q4_0_layer_70b_b1"] = entry(d, t, sum(q4_bytes(m, k) + 2 * k + 2 * m for m, k in LAYER_70B))
+    d, t = layer("q4_0", LAYER_SHAPES)
+    dl, tl = shape_s("q4_0", *LM_HEAD)
+    d, t = N_LAYERS * d + dl, N_LAYERS * t + tl
+    out["decode_sweep_7b"] = entry(d, t, sweep_bytes(), tok_s=round(1.0 / t, 3))
+    out["sample"] = (f"each distinct matrix shape once: median of >= 10 runs after 2 warm-ups on at most "
+                     f"{CPU_ROW_CAP} rows, scaled by rows; layers and the sweep as the sum of their GEMVs; "
+                     f"the expert gather as the reference's loop over 10 experts")
+    return out
+
+
 def profile_case(case: str, reps: int, dev) -> int:
     """One workload launched `reps` times eagerly (no graph), for a profiler's
     kernel trace or counters; prints one JSON line and returns 0.
@@ -1099,6 +1185,8 @@ def main() -> int:
     ap.add_argument("--chunk", type=int, default=64, help="launches per captured graph")
     ap.add_argument("--sweep-tokens", type=int, default=100, help="timed 7B decode-sweep tokens (0 = skip)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget (0 = skip)")
+    ap.add_argument("--cpu-config-seconds", type=float, default=1.0,
+                    help="CPU baseline budget per matrix shape of the other workloads (0 = skip)")
     ap.add_argument("--profile-case", default="",
                     help="run only one workload, eagerly, for a profiler: gemm:M,K,T (Q4_0 prefill GEMM), "
                          "gemv:M,K,B (Q4_0 GEMV), moe (top-10 gather, fresh picks per call); then exit")
@@ -1179,6 +1267,14 @@ def main() -> int:
         cpu, parity = cpu_baseline(g["weights0"], g["x"], g["y0"], args.cpu_seconds)
         print(f"# cpu baseline: {cpu['us_per_call']} us/call on {cpu['cores']} threads; parity {parity}",
               file=sys.stderr, flush=True)
+        if args.cpu_config_seconds > 0:
+            prev = torch.get_num_threads()
+            torch.set_num_threads(cpu["torch_threads"])
+            try:
+                cpu["configs"] = cpu_baseline_configs(args.cpu_config_seconds)
+            finally:
+                torch.set_num_threads(prev)
+            print(f"# cpu baseline configs: {cpu['configs']}", file=sys.stderr, flush=True)
 
     line = {
         "metric": METRIC,

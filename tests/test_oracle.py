@@ -179,6 +179,52 @@ def test_cpu_baseline_dequant_is_the_oracle_bit_for_bit():
     assert rel <= oq.GEMV_REL_L2 and mx <= oq.GEMV_MAX_NORM
 
 
+def test_cpu_baseline_q8_0_affine_and_moe_loop_pinned():
+    """The Q8_0 and affine-Q4 restatements timed as CPU baselines dequantize
+    bit for bit as the oracle (special scales included); their GEMVs and the
+    per-expert MoE decode loop stay within the GEMV tolerance of the oracle."""
+    from oracle import cpu_baseline
+
+    rng = np.random.default_rng(31)
+    n = 64
+    raw = rng.integers(0, 256, size=(n, 34), dtype=np.uint8)
+    d = np.concatenate([np.array(SPECIAL_D, np.float16), rng.uniform(-0.01, 0.01, n - len(SPECIAL_D)).astype(np.float16)])
+    raw[:, :2] = d.view(np.uint8).reshape(n, 2)
+    got = cpu_baseline.dequant_q8_0(torch.from_numpy(raw.copy())).numpy().view(np.uint16)
+    assert np.array_equal(got, oq.dequant_q8_0(raw).view(np.uint16))
+    M, K, g = 40, 512, 64
+    words, scales, biases = syn.affine_q4_weights([M, K], g, torch.Generator().manual_seed(32))
+    want = oq.dequant_affine_q4(words.numpy(), scales.numpy(), biases.numpy(), M * K, g)
+    got = cpu_baseline.dequant_affine_q4(words, scales, biases, g).numpy().reshape(-1)
+    assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
+    x = syn.activations(1, K, torch.Generator().manual_seed(33))
+    w8 = syn.q8_0_weights(M, K, torch.Generator().manual_seed(34))
+    deq8 = oq.dequant_q8_0(w8.numpy()).reshape(M, K)
+    y8 = cpu_baseline.q8_0_gemv(w8, x, M, K).numpy()
+    rel, mx = oq.gemv_errors(y8.astype(np.float64), oq.gemv(deq8, x.numpy()), oq.row_norms(deq8, x.numpy()))
+    assert rel <= oq.GEMV_REL_L2 and mx <= oq.GEMV_MAX_NORM
+    ya = cpu_baseline.affine_gemv(words, scales, biases, x, g).numpy()
+    deqa = want.reshape(M, K)
+    rel, mx = oq.gemv_errors(ya.astype(np.float64), oq.gemv(deqa, x.numpy()), oq.row_norms(deqa, x.numpy()))
+    assert rel <= oq.GEMV_REL_L2 and mx <= oq.GEMV_MAX_NORM
+    # the MoE decode loop over 6 experts, top 3, against oracle.moe_gather
+    E, H, F, k = 6, 256, 128, 3
+    gen = torch.Generator().manual_seed(35)
+    pools = [syn.affine_q4_weights(sh, g, gen) for sh in ([E, F, H], [E, F, H], [E, H, F])]
+    xm = syn.activations(1, H, gen)
+    idx = [4, 0, 2]
+    wts = torch.softmax(torch.randn(k, generator=gen), 0).to(torch.float16)
+
+    def dq(pool, e, rows, cols):
+        return oq.dequant_affine_q4(pool[0][e].numpy(), pool[1][e].numpy(), pool[2][e].numpy(), rows * cols,
+                                    g).reshape(rows, cols)
+
+    ref, _ = oq.moe_gather(xm.numpy(), lambda e: dq(pools[0], e, F, H), lambda e: dq(pools[1], e, F, H),
+                           lambda e: dq(pools[2], e, H, F), idx, wts.numpy())
+    got = cpu_baseline.moe_gather_decode(pools[0], pools[1], pools[2], xm, idx, wts, g).numpy().reshape(-1)
+    assert float(np.linalg.norm(got - ref) / np.linalg.norm(ref)) <= oq.GEMV_REL_L2
+
+
 def test_q8_0_matches_exact_rounding():
     rng = np.random.default_rng(2)
     n = 64

@@ -1127,7 +1127,10 @@ def profile_case(case: str, reps: int, dev) -> int:
       moe                                           top-10 gather, `reps` calls
       moe_step                                      the decode MoE step, 8-launch
                                                     and 4-launch forms, `reps` calls each
-      moe_prefill                                   grouped MoE prefill, 512 tokens"""
+      moe_prefill                                   grouped MoE prefill, 512 tokens
+      q8_layer                                      Q8_0 LLaMA-7B layer at batch 1, as 7
+                                                    GEMVs and as 4 fused launches, `reps`
+                                                    passes over 3 layers each"""
     import torch
 
     from gdsllm_amd import capi, check
@@ -1160,6 +1163,10 @@ def profile_case(case: str, reps: int, dev) -> int:
     elif kind == "moe_prefill":
         res = bench_moe_prefill(dev, reps=reps, reference=False)
         print(json.dumps({"profile_case": case, "chunks": reps, "result": res}), flush=True)
+        return 0
+    elif kind == "q8_layer":
+        res = bench_q8_layer(dev, reps=reps)
+        print(json.dumps({"profile_case": case, "passes": reps, "result": res}), flush=True)
         return 0
     else:
         print(f"bench.py: unknown --profile-case {case!r}", file=sys.stderr)

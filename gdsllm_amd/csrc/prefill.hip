@@ -103,13 +103,18 @@ struct Fmt {
 
 // X and W rings.  The 256-row tile (36 KiB W slots) keeps two of each: a
 // stage of it is two of a 128-row tile's stages long per wave, so two slots
-// hide as much latency as three do there.
+// hide as much latency as three do there.  The 32-token tiles of the grouped
+// MoE prefill keep 4 X and 2 W slots (69 KiB with affine g64), so two
+// workgroups share a CU and one's pipeline fill and epilogue overlap the
+// other's stream: each tile job is short (one expert's ~10 tokens), and with
+// 6 + 5 slots (139 KiB, one workgroup per CU) the 512-token chunk over the
+// 512-expert pool took 1560 us, with 4 + 2 slots 1178-1227 us.
 template <WF F, int BT, int BM = kBM>
 struct Ring {
     static constexpr int kXSlot = BT * 256;
     static constexpr int kLdsMax = 163840;
-    static constexpr int XR0 = BM == 2 * kBM ? 2 : BT == 128 ? 3 : BT == 64 ? 5 : 6;
-    static constexpr int RW = BM == 2 * kBM ? 2 : BT == 128 ? 3 : BT == 64 ? 4 : 5;
+    static constexpr int XR0 = BM == 2 * kBM ? 2 : BT == 128 ? 3 : BT == 64 ? 5 : 4;
+    static constexpr int RW = BM == 2 * kBM ? 2 : BT == 128 ? 3 : BT == 64 ? 4 : 2;
     static constexpr int XR = XR0 * kXSlot + RW * Fmt<F, BM>::kSlot + 1024 <= kLdsMax ? XR0 : XR0 - 1;
     static constexpr int kWOff = XR * kXSlot;
     static constexpr int kDummy = kWOff + RW * Fmt<F, BM>::kSlot;

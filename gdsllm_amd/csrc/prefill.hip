@@ -679,33 +679,37 @@ int dense_gemm(GemmArgs a, hipStream_t stream) {
     return GDSLLM_OK;
 }
 
-// Whether 256-row tiles beat 128-row ones at 128 tokens for `rows` weight
-// rows.  A 256-row tile gives each wave twice a 128-row tile's work (the same
-// wave tile over two blocks per stage) while the compute unit takes in 40%
-// fewer bytes per MFMA (X, the larger operand, feeds twice the rows), and the
-// kernel is bound by that intake at hundreds of tokens.  So the 256-row tile
-// pays when it takes at most half as many rounds of the CUs: 11008 rows at 512
-// tokens (1 round against 2; 83.5 -> 69.8 us for Q4_0 on MI355X) and 32000
-// rows (2 against 4; 180 -> 153 us), not the 22016 gate/up rows of the fused
-// gate/up/SiLU launch (2 against 3, measured no faster).
-inline bool rows256_pays(int64_t rows, int64_t T) {
-    const int64_t tt = (T + 127) / 128, cu = cu_count();
-    const int64_t r128 = ((rows + 127) / 128 * tt + cu - 1) / cu;
-    const int64_t r256 = ((rows + 255) / 256 * tt + cu - 1) / cu;
-    return 2 * r256 <= r128;
+// Tile shape of a dense launch: the one with the least estimated time,
+// rounds of the CUs (tile jobs / CUs, rounded up) times the time of one tile
+// job, about 9 us of fixed cost (launch, pipeline fill, the K-part reduction)
+// plus 24 us x r per 4096 of K, r = 1.1 for 128 rows x 64 tokens, 1.7 for
+// 128 x 128 (the same dequant, twice the MFMAs) and 2.6 for 256 x 128 (twice
+// the dequant and the MFMAs, X shared by twice the rows): fitted to Q4_0 tile
+// jobs on MI355X (one round at K = 4096: 31-37, 51 and 69-75 us).  Ties take
+// the smaller tile.  So 512 tokens over 11008 rows take 256 x 128 (1 round
+// against 2 of 128 x 128 and 3 of 128 x 64), 256 tokens over 11008 rows and
+// 128 tokens over 28672 or 32000 rows take 128 x 128 (1 round against 2),
+// 512 tokens over 4096 rows 128 x 64.
+enum class Tile { k128x64, k128x128, k256x128 };
+inline Tile pick_tile(int64_t rows, int64_t T, int64_t K, bool allow256) {
+    const int64_t cu = cu_count();
+    auto rounds = [&](int64_t bm, int64_t bt) {
+        return static_cast<double>(((rows + bm - 1) / bm * ((T + bt - 1) / bt) + cu - 1) / cu);
+    };
+    const double unit = 24.0 * static_cast<double>(K) / 4096.0;
+    const double c64 = rounds(128, 64) * (9.0 + 1.1 * unit), c128 = rounds(128, 128) * (9.0 + 1.7 * unit),
+                 c256 = rounds(256, 128) * (9.0 + 2.6 * unit);
+    if (allow256 && c256 < c128 && c256 < c64) return Tile::k256x128;
+    return c128 < c64 ? Tile::k128x128 : Tile::k128x64;
 }
 
-// A 128-token tile halves the dequant work and the X traffic per MFMA
-// (measured 1.35-1.4x on 11008 and 32000 rows at 512 tokens), but gives half
-// as many workgroups: it is taken only when it still fills every CU.  It may
-// then take 256-row tiles (rows256_pays).
 template <WF F>
 int dense_gemm_auto(const GemmArgs& a, hipStream_t stream) {
-    const int64_t mtiles = (a.M + kBM - 1) / kBM;
-    const int64_t tiles128 = mtiles * ((a.T + 127) / 128);
-    const int bt = tiles128 >= cu_count() ? 128 : 64;
-    if (bt == 128 && rows256_pays(a.M, a.T)) return dense_gemm<F, 128, 2 * kBM>(a, stream);
-    return bt == 128 ? dense_gemm<F, 128>(a, stream) : dense_gemm<F, 64>(a, stream);
+    switch (pick_tile(a.M, a.T, a.K, true)) {
+        case Tile::k256x128: return dense_gemm<F, 128, 2 * kBM>(a, stream);
+        case Tile::k128x128: return dense_gemm<F, 128>(a, stream);
+        default: return dense_gemm<F, 64>(a, stream);
+    }
 }
 
 // Gate/up/SiLU over token chunks: BM/2 output rows per workgroup (gate rows in
@@ -729,14 +733,23 @@ int dense_dual_gemm(GemmArgs a, hipStream_t stream) {
     return GDSLLM_OK;
 }
 
-// The gate/up rows of a 256-row tile (128 + 128) as for the dense GEMM.
+// The tile shape as for the dense GEMM over the 2M gate and up rows (half
+// of a tile's rows from each), 256-row tiles only where they halve the
+// rounds of 128 x 128 ones (the 22016 rows of the LLaMA-7B gate/up/SiLU
+// launch at 512 tokens, 2 rounds against 3, measured 138.9 against 134.8 us
+// with 128-row tiles); affine weights keep 128-row tiles.
 template <WF F>
 int dense_dual_gemm_auto(const GemmArgs& a, hipStream_t stream) {
-    const int64_t tiles128 = (a.M + 63) / 64 * ((a.T + 127) / 128);
-    const int bt = tiles128 >= cu_count() ? 128 : 64;
-    if constexpr (!is_affine(F))
-        if (bt == 128 && rows256_pays(2 * static_cast<int64_t>(a.M), a.T)) return dense_dual_gemm<F, 128, 2 * kBM>(a, stream);
-    return bt == 128 ? dense_dual_gemm<F, 128>(a, stream) : dense_dual_gemm<F, 64>(a, stream);
+    const int64_t rows = 2 * static_cast<int64_t>(a.M), cu = cu_count();
+    const int64_t r128 = ((rows + 127) / 128 * ((a.T + 127) / 128) + cu - 1) / cu;
+    const int64_t r256 = ((rows + 255) / 256 * ((a.T + 127) / 128) + cu - 1) / cu;
+    switch (pick_tile(rows, a.T, a.K, !is_affine(F) && 2 * r256 <= r128)) {
+        case Tile::k256x128:
+            if constexpr (!is_affine(F)) return dense_dual_gemm<F, 128, 2 * kBM>(a, stream);
+            return dense_dual_gemm<F, 128>(a, stream);
+        case Tile::k128x128: return dense_dual_gemm<F, 128>(a, stream);
+        default: return dense_dual_gemm<F, 64>(a, stream);
+    }
 }
 
 // ------------------------------------------------------------ MoE prefill --

@@ -8,9 +8,9 @@ the same contract:
   * decode with batch > 1 (x [B, 1, K], B <= 8) runs one batched fused GEMV
     instead of failing the reference's x.view(-1) size check;
   * Q4_0 and Q8_0 prefill run the fused MFMA dequant-GEMM instead of
-    dequant + GEMM where that is faster (prefill_takes_fused_gemm: chunks of
-    up to 512 tokens over matrices of 2048 rows or more); the dequant route
-    stays for the other chunks and for shapes the kernel does not serve;
+    dequant + GEMM where that measured faster (prefill_takes_fused_gemm, per
+    format, rows, in_dim and chunk length); the dequant route stays for the
+    other chunks and for shapes the kernel does not serve;
   * per-column int8 weights (runtime/llama.py:162-165) go through
     gds_io_ext.int8_linear: a fused GEMV at decode, a bit-exact dequant and one
     GEMM at prefill, instead of an fp32 copy of the whole matrix per call.
@@ -48,26 +48,39 @@ def _fused_dequant_gemv(x: torch.Tensor, meta: dict) -> torch.Tensor:
     return out.unsqueeze(1)
 
 
-# Measured on MI355X (Q4_0 and Q8_0, LLaMA-7B/70B projection shapes, 64 to
-# 2048 tokens), fused MFMA dequant-GEMM against the bit-exact dequant into a
-# scratch matrix + hipBLASLt: the fused GEMM wins up to 512 tokens (11008 x
-# 4096 Q4_0 at 512: 69 against 73 us; 28672 x 8192 at 128: 108 against 235
-# us) and loses from 1024 on (11008 x 4096 Q4_0 at 2048: 217 against 182 us;
-# it dequantizes every weight once per 128-token tile, the route once per
-# call), on matrices under 2048 rows (1024 x 8192 at 512: 51 against 39 us)
-# and where its tiles leave most compute units idle (4096 x 11008 at 64
-# tokens: 32 tiles, 63 against 53 us).
+# Measured on MI355X: the fused MFMA dequant-GEMM against the bit-exact dequant
+# into a scratch matrix + hipBLASLt (the reference's route), Q4_0, Q8_0 and
+# affine-Q4 g64 over 4096x4096, 11008x4096, 4096x11008, 32000x4096, 8192x8192,
+# 1024x8192, 28672x8192, 8192x28672 and 2048x4096 at 64 to 1024 tokens.
+#  * Q4_0 and affine-Q4: the fused GEMM wins wherever its 128-row x 64-token
+#    tiles number at least 32 (64 over an in_dim past 8192, where each tile is
+#    long, or over 2048 rows), on 2048 rows or more, for chunks of up to 512
+#    tokens, and for longer chunks over up to 8192 rows (8192x28672 at 1024
+#    tokens: 464 against 503 us); it loses on 1024 rows (1024x8192 at 512
+#    tokens: 51 against 40 us), where few tiles leave most compute units idle
+#    (4096x11008 at 64 tokens: 62 against 53 us), and at 1024 tokens over
+#    11008 rows or more (11008x4096: 132 against 108 us), where it dequantizes
+#    every weight once per token tile and the route once per call.
+#  * Q8_0 (a W stage twice Q4_0's): the fused GEMM wins on 8192 rows or more
+#    up to 512 tokens (28672x8192 at 128 tokens: 97 against 247 us), except
+#    512 tokens over an in_dim of 4096 on fewer than 16384 rows (11008x4096:
+#    82 against 76 us); on 4096 rows the two are within 10% either way and the
+#    route is taken.
 FUSED_GEMM_MAX_TOKENS = 512
 FUSED_GEMM_MIN_ROWS = 2048
-FUSED_GEMM_MIN_TILES = 64  # 128-row x 64-token tiles
 
 
-def prefill_takes_fused_gemm(out_dim: int, tokens: int) -> bool:
+def prefill_takes_fused_gemm(out_dim: int, tokens: int, in_dim: int = 4096, gguf_type: str = "q4_0") -> bool:
     """Whether a prefill projection of `tokens` rows of x onto `out_dim` rows
-    of quantized weights takes the fused MFMA dequant-GEMM (else dequant +
-    F.linear)."""
+    of quantized weights (in_dim columns; gguf_type "q4_0", "q8_0" or
+    "affine_q4") takes the fused MFMA dequant-GEMM (else dequant + F.linear)."""
+    if gguf_type == "q8_0":
+        return (tokens <= FUSED_GEMM_MAX_TOKENS and out_dim >= 8192 and
+                not (in_dim <= 4096 and tokens > 256 and out_dim < 16384))
     tiles = -(-out_dim // 128) * -(-tokens // 64)
-    return tokens <= FUSED_GEMM_MAX_TOKENS and out_dim >= FUSED_GEMM_MIN_ROWS and tiles >= FUSED_GEMM_MIN_TILES
+    min_tiles = 64 if in_dim > 8192 or out_dim <= 2048 else 32
+    return (out_dim >= FUSED_GEMM_MIN_ROWS and tiles >= min_tiles and
+            (tokens <= FUSED_GEMM_MAX_TOKENS or out_dim <= 8192))
 
 
 def _fused_dequant_gemm(x: torch.Tensor, meta: dict) -> Optional[torch.Tensor]:
@@ -84,7 +97,7 @@ def dequant_linear(
     if isinstance(w, dict) and "gguf_type" in w:
         if x.shape[1] == 1 and x.shape[0] <= 8:
             return _fused_dequant_gemv(x, w)
-        if prefill_takes_fused_gemm(int(w["shape"][0]), x.numel() // x.shape[-1]):
+        if prefill_takes_fused_gemm(int(w["shape"][0]), x.numel() // x.shape[-1], int(w["shape"][1]), w["gguf_type"]):
             out = _fused_dequant_gemm(x, w)
             if out is not None:
                 return out

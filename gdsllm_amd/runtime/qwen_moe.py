@@ -57,7 +57,7 @@ def _affine_linear(x: torch.Tensor, meta: dict, scratch: Optional[torch.Tensor] 
     """F.linear(x, dequant(meta)) for a prefill chunk: the fused GEMM where it
     is the faster route (llama.prefill_takes_fused_gemm), else the
     reference's dequant -> F.linear (runtime/qwen_moe.py:72-73)."""
-    if prefill_takes_fused_gemm(int(meta["shape"][0]), x.numel() // x.shape[-1]):
+    if prefill_takes_fused_gemm(int(meta["shape"][0]), x.numel() // x.shape[-1], int(meta["shape"][1]), "affine_q4"):
         out = _fused_affine_q4_gemm(x, meta)
         if out is not None:
             return out

@@ -422,12 +422,12 @@ def test_runtime_moe_prefill_matches_per_expert_route(gpu, tmp_path):
 
 def test_runtime_q8_0_prefill_projection(gpu):
     """dequant_linear on a Q8_0 weight with a prefill chunk the MFMA GEMM
-    serves faster (4096 rows, 128 tokens: 64 tiles) takes it."""
+    serves faster (8192 rows, 128 tokens) takes it."""
     from gdsllm_amd.runtime import ext
     from gdsllm_amd.runtime import llama
 
-    M, K, T = 4096, 4096, 128
-    assert llama.prefill_takes_fused_gemm(M, T)
+    M, K, T = 8192, 4096, 128
+    assert llama.prefill_takes_fused_gemm(M, T, K, "q8_0")
     w = syn.q8_0_weights(M, K, gen(6000))
     handle = ext().GdsBufferHandle.from_tensor(w.reshape(-1).to(gpu))
     meta = {"buffer": handle, "shape": [M, K], "gguf_type": "q8_0", "offset": 0}

@@ -194,13 +194,22 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_sk(GemmArgs a) {
     int m0, t0 = 0, nt, p0 = 0;
     const uint8_t *wA = a.w, *sA = a.s, *bA = a.b, *wB = a.w2, *sB = a.s2, *bB = a.b2;
     if constexpr (kGath) {
-        const int tile = blockIdx.x / a.mtiles;
-        if (tile >= *a.ntiles) return;  // uniform: the grid covers the worst case
+        // The grid covers the worst case; the first ntiles * mtiles
+        // workgroups take a job, in the XCD-aware order of the dense modes
+        // over that count: an XCD takes a contiguous range of jobs, i.e. the
+        // row tiles of the same experts, so an expert's token rows of X come
+        // into one L2, not into all eight.
+        const int jobs = __builtin_amdgcn_readfirstlane(*a.ntiles) * a.mtiles, b = blockIdx.x;
+        if (b >= jobs) return;  // uniform
+        const int per = jobs >> 3, rem = jobs & 7, xcd = b & 7;
+        const int q = xcd * per + (xcd < rem ? xcd : rem) + (b >> 3);
+        const int tile = q / a.mtiles;
         const int4 td = a.tiles[tile];
-        m0 = (blockIdx.x % a.mtiles) * (kDual ? 64 : kBM);
-        p0 = td.y;
-        nt = td.z;
-        const int64_t e = td.x;
+        m0 = (q % a.mtiles) * (kDual ? 64 : kBM);
+        // wave-uniform values, said outright: the X issue branches on nt
+        p0 = __builtin_amdgcn_readfirstlane(td.y);
+        nt = __builtin_amdgcn_readfirstlane(td.z);
+        const int64_t e = __builtin_amdgcn_readfirstlane(td.x);
         wA += e * a.estride_w;
         sA += e * a.estride_s;
         bA += e * a.estride_b;
@@ -325,6 +334,14 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_sk(GemmArgs a) {
         else return 128 * static_cast<int64_t>(gi);
     };
 
+    // Gathered tiles: a transfer whose four tokens all lie past the tile's
+    // count (an expert's ~10 tokens in a 32-token tile) is a dummy, so the
+    // compute unit takes in only the token rows that exist.  Their slot rows
+    // keep older data; they feed only the MFMA outputs of those tokens, which
+    // are never stored.
+    bool xlive[NX];
+#pragma unroll
+    for (int ii = 0; ii < NX; ++ii) xlive[ii] = !kGath || 4 * (NX * wave + ii) < nt;
     auto issue_x = [&](int sx) {  // X of stage sx (any integer) into its ring slot
         const int sl = ((sx % XR) + XR) % XR;
         const uint32_t dst = lds0 + sl * kXSlot + 1024 * (NX * wave);
@@ -335,7 +352,10 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_sk(GemmArgs a) {
         }
         const uint16_t* base = xbase + kStageK * (sx < nst ? sx : nst - 1);
 #pragma unroll
-        for (int ii = 0; ii < NX; ++ii) dma16_asm(xoff[ii], base, dst + 1024 * ii);
+        for (int ii = 0; ii < NX; ++ii) {
+            if (xlive[ii]) dma16_asm(xoff[ii], base, dst + 1024 * ii);
+            else dma4_asm(0u, a.w, lds0 + R::kDummy);
+        }
     };
     auto issue_w = [&](int gi) {  // W group gi into its ring slot
         if (gi < 0) {

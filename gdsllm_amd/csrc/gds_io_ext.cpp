@@ -533,6 +533,42 @@ std::optional<torch::Tensor> fused_dequant_gemm(const Handle& h, torch::Tensor x
     return out;
 }
 
+// Prefill MLP input: h = fp16(fp16(silu(gate x)) * (up x)), x [..., in_dim] ->
+// h [..., out_dim] in one MFMA launch over both GGUF matrices (Q4_0 or Q8_0).
+// None when the library cannot serve the shape or alignment (the caller then
+// runs the two projections and the elementwise SiLU and product).
+std::optional<torch::Tensor> fused_gate_up_silu_gemm(const Handle& gate, const Handle& up, torch::Tensor x,
+                                                     std::vector<int64_t> weight_shape, const std::string& gguf_type,
+                                                     int64_t gate_offset, int64_t up_offset) {
+    const char* where = "fused_gate_up_silu_gemm";
+    check_handle(gate, where);
+    check_handle(up, where);
+    if (weight_shape.size() != 2) throw std::runtime_error(std::string(where) + ": weight_shape must be [out_dim, in_dim]");
+    if (gguf_type != "q4_0" && gguf_type != "q8_0")
+        throw std::runtime_error(std::string(where) + ": unsupported type '" + gguf_type + "'");
+    if (gate->device_id() != up->device_id()) throw std::runtime_error(std::string(where) + ": buffers on different devices");
+    const bool q4 = gguf_type == "q4_0";
+    const int64_t out_dim = weight_shape[0], in_dim = weight_shape[1];
+    torch::Tensor xf = x.contiguous();
+    const int dev = gate->device_id();
+    check_x(xf, dev, where);
+    if (in_dim <= 0 || in_dim % 32 != 0 || xf.size(-1) != in_dim)
+        throw std::runtime_error(std::string(where) + ": last dim of x must equal in_dim " + std::to_string(in_dim) +
+                                 " (a multiple of 32)");
+    const int64_t tokens = xf.numel() / in_dim;
+    check_range(gate, gate_offset, out_dim * (in_dim / 32) * (q4 ? 18 : 34), where);
+    check_range(up, up_offset, out_dim * (in_dim / 32) * (q4 ? 18 : 34), where);
+    auto out_shape = xf.sizes().vec();
+    out_shape.back() = out_dim;
+    torch::Tensor h = torch::empty(out_shape, fp16_on(dev));
+    const int rc = (q4 ? gdsllm_dequant_gemm_gate_up_silu_q4_0 : gdsllm_dequant_gemm_gate_up_silu_q8_0)(
+        at_offset(gate, gate_offset), at_offset(up, up_offset), xf.data_ptr(), h.data_ptr(), out_dim, in_dim, tokens,
+        in_dim, out_dim, OnDevice(dev).stream());
+    if (rc == GDSLLM_ERR_UNSUPPORTED) return std::nullopt;
+    check(rc, where);
+    return h;
+}
+
 // Prefill affine-Q4 projection: x [..., in_dim] -> [..., out_dim] on the MFMA
 // dequant-GEMM; None for shapes, groupings or alignments it does not serve.
 std::optional<torch::Tensor> fused_affine_q4_gemm(const Handle& h, torch::Tensor x, std::vector<int64_t> weight_shape,
@@ -876,6 +912,10 @@ PYBIND11_MODULE(gds_io_ext, m) {
     m.def("moe_prefill_affine_q4", &moe_prefill_affine_q4,
           "Prefill routed-expert MLP over stacked experts: x [T, H] -> expert_output [T, H] (None if not served).",
           py::arg("x"), py::arg("entries"), py::arg("top_k_indices"), py::arg("top_k_weights"));
+    m.def("fused_gate_up_silu_gemm", &fused_gate_up_silu_gemm,
+          "Prefill fp16(silu(gate . x) * (up . x)) on MFMA: x [..., K] -> h [..., M] (None if not served).",
+          py::arg("gate_handle"), py::arg("up_handle"), py::arg("x"), py::arg("weight_shape"), py::arg("gguf_type"),
+          py::arg("gate_offset"), py::arg("up_offset"));
     m.def("fused_dequant_gemm", &fused_dequant_gemm, "Prefill Q4_0/Q8_0 dequant-GEMM on MFMA: x [T, K] -> [T, M] (None if not served).",
           py::arg("handle"), py::arg("x"), py::arg("weight_shape"), py::arg("gguf_type"), py::arg("offset"));
     m.def("gemv_f16", &gemv_f16, "fp16-weight GEMV (router, shared-expert gate): x [..., K] -> [..., M].",

@@ -1949,16 +1949,17 @@ bool plan_rows(RowsTarget& tg, int K, int& grid, int& wv, int& tmax) {
     // 4-wave workgroups, unless 8-wave ones keep more row groups in flight
     // (single matrices whose x fills so much LDS that one 4-wave workgroup
     // fits per CU: the 8192 x 28672 down projection of a 70B layer), or as
-    // many where x spans several windows and 8-wave workgroups still give
-    // every CU one: x then comes into each CU once instead of once per
-    // workgroup (8192 x 8192 at batch 1 / 2: 8.86 / 10.91 against 9.13 /
-    // 11.22 us; 28672 x 8192 at batch 2: 31.6 against 32.6 us)
+    // many where x spans several windows and 8-wave workgroups give every CU
+    // one and every wave one row group: x then comes into each CU once
+    // instead of once per workgroup (8192 x 8192 at batch 1 / 2: 8.81 /
+    // 10.45 against 9.17 / 10.94 us; with several row groups per wave, 28672
+    // x 8192 at batch 2, 8-wave workgroups measured no faster)
     wv = kWaves;
     int resident = rows_resident<F, NB, MODE, kWaves>(NW);
     if constexpr (MODE == 0) {
         const int r8 = rows_resident<F, NB, MODE, 8>(NW);
         const int w8 = std::min(r8 * 8, rg_all), w4 = std::min(resident * kWaves, rg_all);
-        const bool tie8 = r8 > 0 && w8 == w4 && NW >= 2 && (rg_all + 7) / 8 >= cu_count();
+        const bool tie8 = r8 > 0 && w8 == w4 && NW >= 2 && (rg_all + 7) / 8 >= cu_count() && rg_all <= r8 * 8;
         if (w8 > w4 || tie8) {
             wv = 8;
             resident = r8;

@@ -130,10 +130,19 @@ def qkv_projections(x: torch.Tensor, weights: Dict, scratch: Optional[torch.Tens
     return tuple(dequant_linear(x, weights, n, scratch) for n in names)
 
 
+def _gguf_pair(g, u) -> bool:
+    """gate and up: GGUF weights of one type and shape on one device."""
+    return (isinstance(g, dict) and isinstance(u, dict) and "gguf_type" in g and
+            g.get("gguf_type") == u.get("gguf_type") and list(g["shape"]) == list(u["shape"]) and
+            g["buffer"].device_id == u["buffer"].device_id)
+
+
 def mlp(x: torch.Tensor, weights: Dict, scratch: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """SwiGLU MLP (runtime/llama.py:247-256).  At decode over GGUF weights,
-    h = fp16(silu(gate x) * (up x)) comes from one launch that never writes
-    gate or up (torch's fp16 rounding of silu and of the product), then down."""
+    """SwiGLU MLP (runtime/llama.py:247-256).  Over GGUF weights h =
+    fp16(silu(gate x) * (up x)) comes from one launch that never writes gate
+    or up (torch's fp16 rounding of silu and of the product), then down: the
+    fused GEMV at decode, the fused MFMA GEMM for a prefill chunk where the
+    projections take it (prefill_takes_fused_gemm)."""
     g, u = weights["mlp.gate_proj.weight"], weights["mlp.up_proj.weight"]
     if _gguf_decode(x, (g, u)) and list(g["shape"]) == list(u["shape"]):
         batch = x.shape[0]
@@ -141,6 +150,12 @@ def mlp(x: torch.Tensor, weights: Dict, scratch: Optional[torch.Tensor] = None) 
                                      g["gguf_type"], g["offset"], u["offset"])
         if h is not None:
             return dequant_linear(h.unsqueeze(1), weights, "mlp.down_proj", scratch)
+    elif (x.shape[1] > 1 or x.shape[0] > 8) and _gguf_pair(g, u) and g["gguf_type"] in ("q4_0", "q8_0") and \
+            prefill_takes_fused_gemm(int(g["shape"][0]), x.numel() // x.shape[-1], int(g["shape"][1]), g["gguf_type"]):
+        h = ext().fused_gate_up_silu_gemm(g["buffer"], u["buffer"], x, list(g["shape"]), g["gguf_type"],
+                                          g["offset"], u["offset"])
+        if h is not None:
+            return dequant_linear(h, weights, "mlp.down_proj", scratch)
     gate = dequant_linear(x, weights, "mlp.gate_proj", scratch)
     up = dequant_linear(x, weights, "mlp.up_proj", scratch)
     return dequant_linear(F.silu(gate) * up, weights, "mlp.down_proj", scratch)

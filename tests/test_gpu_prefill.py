@@ -438,6 +438,52 @@ def test_runtime_q8_0_prefill_projection(gpu):
     assert_gemv_close(to_np(y).reshape(T, M), oq.dequant_q8_0(to_np(w)).reshape(M, K), to_np(x), "q8_0 dequant_linear")
 
 
+@pytest.mark.parametrize("fmt,T,F,K", [("q4_0", 64, 4096, 1024), ("q8_0", 96, 8192, 512), ("q4_0", 8, 256, 512)])
+def test_runtime_mlp_prefill(gpu, fmt, T, F, K):
+    """runtime mlp on a prefill chunk over GGUF weights: where the rule sends
+    the projections to the fused GEMM, gate/up/SiLU is one launch
+    (fused_gate_up_silu_gemm) and down follows; else the reference's three
+    projections and elementwise SiLU.  Against the oracle composition: g and u
+    rounded to fp16, torch's fp16 SiLU and product, then down."""
+    from gdsllm_amd.runtime import ext, llama
+
+    make = syn.q4_0_weights if fmt == "q4_0" else syn.q8_0_weights
+    dq = oq.dequant_q4_0 if fmt == "q4_0" else oq.dequant_q8_0
+    shapes = {"mlp.gate_proj": (F, K), "mlp.up_proj": (F, K), "mlp.down_proj": (K, F)}
+    weights, mats = {}, {}
+    for i, (name, (m, k)) in enumerate(shapes.items()):
+        w = make(m, k, gen(6100 + i))
+        mats[name] = dq(to_np(w)).reshape(m, k)
+        weights[f"{name}.weight"] = {"buffer": ext().GdsBufferHandle.from_tensor(w.reshape(-1).to(gpu)),
+                                     "shape": [m, k], "gguf_type": fmt, "offset": 0}
+    fused = llama.prefill_takes_fused_gemm(F, T, K, fmt)
+    assert fused == (F >= 2048), "the cases pick both routes"
+    calls = []
+    real = ext().fused_gate_up_silu_gemm
+
+    def spy(*a, **kw):
+        calls.append(1)
+        return real(*a, **kw)
+
+    ext().fused_gate_up_silu_gemm = spy
+    try:
+        x = syn.activations(T, K, gen(6110))
+        y = llama.mlp(x.to(gpu).view(1, T, K), weights)
+        torch.cuda.synchronize()
+    finally:
+        ext().fused_gate_up_silu_gemm = real
+    assert len(calls) == (1 if fused else 0)
+    assert y.shape == (1, T, K)
+    g = oq.gemv(mats["mlp.gate_proj"], to_np(x)).astype(np.float16)
+    u = oq.gemv(mats["mlp.up_proj"], to_np(x)).astype(np.float16)
+    h = (oq.silu_fp16(g).astype(np.float32) * u.astype(np.float32)).astype(np.float16)
+    want = oq.gemv(mats["mlp.down_proj"], h)
+    got = to_np(y).reshape(T, K).astype(np.float64)
+    rel = float(np.linalg.norm(got - want) / np.linalg.norm(want))
+    print(f"mlp prefill {fmt} T{T} {F}x{K}: rel L2 {rel:.2e} ({'fused' if fused else 'route'})")
+    assert np.isfinite(got).all() and rel <= oq.GEMV_REL_L2, f"mlp rel L2 {rel:.3e}"
+
+
 # (fmt, T, F, K): the 7B gate/up shape at a 512-token chunk (128-token tiles)
 # and at 64 tokens (64-token tiles), ragged rows and tokens, a short K
 # 6000 rows at 500-512 tokens: 128 + 128-row gate/up tiles on a 256-CU GPU

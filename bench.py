@@ -589,8 +589,8 @@ LAYER_70B = [(8192, 8192), (1024, 8192), (1024, 8192), (8192, 8192), (28672, 819
 
 def bench_70b_layer(dev, layers_rotated: int = 2, reps: int = 20):
     """Q4_0 LLaMA-70B decoder layer (7 GEMVs, 481 MB of weights) at batch
-    1, 2, 4, 8, rotating over `layers_rotated` distinct layers; at batch 1
-    and 2 also with the decode-step fusions (4 launches per layer)."""
+    1, 2, 4, 8, rotating over `layers_rotated` distinct layers, as 7 launches
+    and with the decode-step fusions (4 launches per layer)."""
     import ctypes
 
     import torch
@@ -615,31 +615,30 @@ def bench_70b_layer(dev, layers_rotated: int = 2, reps: int = 20):
         nbytes = wbytes + sum(B * (2 * k + 2 * m) for m, k in LAYER_70B)
         out[f"b{B}"] = {"us_per_layer": round(ms * 1e3, 3), "GB_s": round(nbytes / (ms * 1e-3) / 1e9, 1),
                         "pct_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / 80, 1), "bytes_per_layer": nbytes}
-        if B <= 2:
-            # the same layer with the decode-step fusions of the 7B sweep:
-            # q/k/v in one grouped launch, gate/up/SiLU in one launch writing
-            # h, down on h: 4 launches instead of 7
-            h = torch.empty(B, 28672, dtype=torch.float16, device=dev)
-            lib = capi()
-            yq, yk, yv = (torch.empty(B, m, dtype=torch.float16, device=dev) for m in (8192, 1024, 1024))
-            dims = (ctypes.c_int64 * 3)(8192, 1024, 1024)
-            outs = (ctypes.c_void_p * 3)(yq.data_ptr(), yk.data_ptr(), yv.data_ptr())
-            groups = [(ctypes.c_void_p * 3)(lw[0].data_ptr(), lw[1].data_ptr(), lw[2].data_ptr()) for lw in layers]
+        # the same layer with the decode-step fusions of the 7B sweep:
+        # q/k/v in one grouped launch, gate/up/SiLU in one launch writing
+        # h, down on h: 4 launches instead of 7
+        h = torch.empty(B, 28672, dtype=torch.float16, device=dev)
+        lib = capi()
+        yq, yk, yv = (torch.empty(B, m, dtype=torch.float16, device=dev) for m in (8192, 1024, 1024))
+        dims = (ctypes.c_int64 * 3)(8192, 1024, 1024)
+        outs = (ctypes.c_void_p * 3)(yq.data_ptr(), yk.data_ptr(), yv.data_ptr())
+        groups = [(ctypes.c_void_p * 3)(lw[0].data_ptr(), lw[1].data_ptr(), lw[2].data_ptr()) for lw in layers]
 
-            def run_fused():
-                st = torch.cuda.current_stream().cuda_stream
-                for lw, grp in zip(layers, groups):
-                    check(lib.gdsllm_fused_q4_0_gemv_group(3, grp, outs, dims, xs[8192].data_ptr(), 8192, B, 8192, st))
-                    _gemv_call("q4_0", lw[3], xs[8192], ys[8192], 8192, 8192, B)
-                    check(lib.gdsllm_fused_q4_0_gate_up_silu(lw[4].data_ptr(), lw[5].data_ptr(), xs[8192].data_ptr(),
-                                                             h.data_ptr(), 28672, 8192, B, 8192, 28672, st))
-                    _gemv_call("q4_0", lw[6], h, ys[8192], 8192, 28672, B)
+        def run_fused():
+            st = torch.cuda.current_stream().cuda_stream
+            for lw, grp in zip(layers, groups):
+                check(lib.gdsllm_fused_q4_0_gemv_group(3, grp, outs, dims, xs[8192].data_ptr(), 8192, B, 8192, st))
+                _gemv_call("q4_0", lw[3], xs[8192], ys[8192], 8192, 8192, B)
+                check(lib.gdsllm_fused_q4_0_gate_up_silu(lw[4].data_ptr(), lw[5].data_ptr(), xs[8192].data_ptr(),
+                                                         h.data_ptr(), 28672, 8192, B, 8192, 28672, st))
+                _gemv_call("q4_0", lw[6], h, ys[8192], 8192, 28672, B)
 
-            msf = _replay_ms(run_fused, reps) / layers_rotated
-            fbytes = wbytes + B * 2 * (8192 + (8192 + 1024 + 1024) + 2 * 8192 + 8192 + 28672 + 28672 + 8192)
-            out[f"b{B}"]["fused_4_launches"] = {
-                "us_per_layer": round(msf * 1e3, 3), "GB_s": round(fbytes / (msf * 1e-3) / 1e9, 1),
-                "pct_of_hbm_peak": round(fbytes / (msf * 1e-3) / 1e9 / 80, 1), "bytes_per_layer": fbytes}
+        msf = _replay_ms(run_fused, reps) / layers_rotated
+        fbytes = wbytes + B * 2 * (8192 + (8192 + 1024 + 1024) + 2 * 8192 + 8192 + 28672 + 28672 + 8192)
+        out[f"b{B}"]["fused_4_launches"] = {
+            "us_per_layer": round(msf * 1e3, 3), "GB_s": round(fbytes / (msf * 1e-3) / 1e9, 1),
+            "pct_of_hbm_peak": round(fbytes / (msf * 1e-3) / 1e9 / 80, 1), "bytes_per_layer": fbytes}
     out["layers_rotated"] = layers_rotated
     return out
 

@@ -50,7 +50,8 @@ enum class Fmt { Q4_0, Q8_0 };
 // The batched kernels take the exact form always: the staged kernel
 // (kStagedExact), a fallback, and the Q4_0 MFMA kernels (kCodesExact), where
 // the weight operand is unbiased the same way and the offset-correction MFMAs
-// drop out.
+// drop out (deciding per wave from its slice of x, as the row-span kernel
+// does per window, measured no faster on the x-in-registers kernel).
 constexpr bool kRowsExact = true;
 constexpr bool kStagedExact = true;
 constexpr bool kCodesExact = true;
@@ -1537,19 +1538,66 @@ struct Cfg {
 // kept in registers (batch 8, us): 28672x8192 31.7 / 34.3, 13003x4096
 // 13.7 / 15.8, 9000x5120 12.2 / 14.2.
 using Tall = Cfg<16, 2, 4>;
+
+// Where a launch reads weights and writes results.  MODE 0: one matrix
+// (w[0], y[0], m[0]); 1: up to 4 matrices of the same in_dim sharing x, whose
+// 16-row tiles are numbered one matrix after another (tile_end[i]: one past
+// matrix i's last tile; the entries past the last matrix repeat the total);
+// 2: gate/up pairs, w[0] = gate and w[1] = up with m[0] rows each: tile t
+// holds gate rows 8t..8t+7 (row group 0) and the same up rows (row group 1),
+// and y[0][b*ldy[0] + r] receives h = fp16(silu(fp16 gate) * fp16 up).
+// tile_end[kMaxGroup - 1] is the launch's tile count in every mode.
+struct Target {
+    const uint8_t* w[kMaxGroup];
+    uint16_t* y[kMaxGroup];
+    int64_t ldy[kMaxGroup];
+    int m[kMaxGroup];
+    int tile_end[kMaxGroup];
+};
+
+// One tile: the weights of its first row (pairing: gate and up), where its
+// results go, its first row and its matrix's row count.
+struct Tile {
+    const uint8_t *w0, *w1;
+    uint16_t* y;
+    int64_t ldy;
+    int row0, m;
+};
+template <int MODE>
+__device__ __forceinline__ Tile tile_of(const Target& tg, int t) {
+    Tile r;
+    if constexpr (MODE == 1) {
+        const int i = (t >= tg.tile_end[0]) + (t >= tg.tile_end[1]) + (t >= tg.tile_end[2]);
+        int first;
+        switch (i) {
+            case 0: r.w0 = tg.w[0], r.y = tg.y[0], r.ldy = tg.ldy[0], r.m = tg.m[0], first = 0; break;
+            case 1: r.w0 = tg.w[1], r.y = tg.y[1], r.ldy = tg.ldy[1], r.m = tg.m[1], first = tg.tile_end[0]; break;
+            case 2: r.w0 = tg.w[2], r.y = tg.y[2], r.ldy = tg.ldy[2], r.m = tg.m[2], first = tg.tile_end[1]; break;
+            default: r.w0 = tg.w[3], r.y = tg.y[3], r.ldy = tg.ldy[3], r.m = tg.m[3], first = tg.tile_end[2]; break;
+        }
+        r.w1 = r.w0;
+        r.row0 = kRT * (t - first);
+    } else {
+        r.w0 = tg.w[0], r.w1 = tg.w[MODE == 2 ? 1 : 0], r.y = tg.y[0], r.ldy = tg.ldy[0], r.m = tg.m[0];
+        r.row0 = (MODE == 2 ? kRT / 2 : kRT) * t;
+    }
+    return r;
+}
 }  // namespace bx
 
-template <class C>
-__global__ __launch_bounds__(C::kWaves * 64) void gguf_gemv_q4_xreg(const uint8_t* __restrict__ W,
-                                                                    const uint16_t* __restrict__ X,
-                                                                    uint16_t* __restrict__ Y, int M, int K, int nb,
-                                                                    int64_t ldx, int64_t ldy) {
-    constexpr int RT = bx::kRT, NRG = RT / 8, NWD = bx::kNWD, NS = C::kNS;
+template <class C, int MODE>
+__global__ __launch_bounds__(C::kWaves * 64) void gguf_gemv_q4_xreg(const bx::Target tg,
+                                                                    const uint16_t* __restrict__ X, int K, int nb,
+                                                                    int64_t ldx) {
+    constexpr int RT = bx::kRT, NRG = RT / 8, NS = C::kNS;
+    // transfers per stage: 3 (16 rows of one matrix); pairing: 2 per matrix
+    // (chunks 0-63 of the 8 rows, then chunks 64-71 on 8 lanes)
+    constexpr int NWD = MODE == 2 ? 4 : bx::kNWD;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int S = K >> 8;
     const uint32_t row_bytes = static_cast<uint32_t>(S) * 144u;
-    const int ntiles = (M + RT - 1) / RT;
+    const int ntiles = tg.tile_end[kMaxGroup - 1];
     const int T = (ntiles - static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) - 1) / static_cast<int>(gridDim.x);
     const int nst = S > wave ? (S - 1 - wave) / C::kWaves + 1 : 0;  // super-blocks of this wave (<= NSB)
     const int Q = T * nst;
@@ -1558,35 +1606,47 @@ __global__ __launch_bounds__(C::kWaves * 64) void gguf_gemv_q4_xreg(const uint8_
     float* red0 = reinterpret_cast<float*>(lds + C::kWaves * NS * bx::kSlotBytes);
 
     // weight transfer j: chunk c = 64j + lane = row c / 9, chunk c % 9 of the
-    // row's super-block (rows past the tile's last valid row read that row)
-    auto w_offsets = [&](int nrows, uint32_t (&off)[NWD]) {
+    // row's super-block (rows past the tile's last valid row read that row).
+    // Pairing: chunks of one matrix's 8 rows, c = lane, then c = 64 + lane.
+    constexpr int NOFF = MODE == 2 ? 2 : NWD;
+    constexpr int kChunks = MODE == 2 ? 72 : RT * 9;
+    auto w_offsets = [&](int nrows, uint32_t (&off)[NOFF]) {
 #pragma unroll
-        for (int j = 0; j < NWD; ++j) {
-            const int c = min(64 * j + lane, RT * 9 - 1);
+        for (int j = 0; j < NOFF; ++j) {
+            const int c = min(64 * j + lane, kChunks - 1);
             const int r = c / 9;
             off[j] = static_cast<uint32_t>(min(r, nrows - 1)) * row_bytes + 16u * static_cast<uint32_t>(c - 9 * r);
         }
     };
-    uint32_t woff_full[NWD];
-    w_offsets(RT, woff_full);
+    uint32_t woff_full[NOFF];
+    w_offsets(MODE == 2 ? RT / 2 : RT, woff_full);
 
     int ii = 0, ss = 0, qs = 0;  // next stage to issue: tile ii, super-block step ss, slot qs
     auto issue = [&]() {
         const uint32_t slot = slot0 + qs * bx::kSlotBytes;
         const int sb = wave + C::kWaves * ss;
-        const int row0 = RT * (static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) * ii);
-        const uint8_t* wb = W + static_cast<int64_t>(row0) * row_bytes + 144 * sb;
-        uint32_t woff[NWD];
-        const int nrows = min(RT, M - row0);
-        if (nrows == RT) {
+        const bx::Tile tl = bx::tile_of<MODE>(tg, static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) * ii);
+        const int64_t at = static_cast<int64_t>(tl.row0) * row_bytes + 144 * sb;
+        uint32_t woff[NOFF];
+        const int nrows = min(MODE == 2 ? RT / 2 : RT, tl.m - tl.row0);
+        if (nrows == (MODE == 2 ? RT / 2 : RT)) {
 #pragma unroll
-            for (int j = 0; j < NWD; ++j) woff[j] = woff_full[j];
+            for (int j = 0; j < NOFF; ++j) woff[j] = woff_full[j];
         } else {
             w_offsets(nrows, woff);
         }
+        if constexpr (MODE == 2) {
+            // gate rows into row group 0, up rows into row group 1
+            dma16_asm(woff[0], tl.w0 + at, slot);
+            if (lane < 8) dma16_asm(woff[1], tl.w0 + at, slot + 1024);
+            dma16_asm(woff[0], tl.w1 + at, slot + 1152);
+            if (lane < 8) dma16_asm(woff[1], tl.w1 + at, slot + 1152 + 1024);
+        } else {
+            const uint8_t* wb = tl.w0 + at;
 #pragma unroll
-        for (int j = 0; j < NWD - 1; ++j) dma16_asm(woff[j], wb, slot + 1024 * j);
-        if (lane < bx::kLastLanes) dma16_asm(woff[NWD - 1], wb, slot + 1024 * (NWD - 1));
+            for (int j = 0; j < NWD - 1; ++j) dma16_asm(woff[j], wb, slot + 1024 * j);
+            if (lane < bx::kLastLanes) dma16_asm(woff[NWD - 1], wb, slot + 1024 * (NWD - 1));
+        }
         if (++ss == nst) {
             ss = 0;
             ++ii;
@@ -1620,13 +1680,25 @@ __global__ __launch_bounds__(C::kWaves * 64) void gguf_gemv_q4_xreg(const uint8_
         }
         lds_barrier();
         const int i = threadIdx.x;
-        const int row0 = RT * (static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) * ck);
-        if (i < 8 * RT) {
+        const bx::Tile tl = bx::tile_of<MODE>(tg, static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) * ck);
+        if constexpr (MODE == 2) {
+            // one thread per (batch row, pair): gate in rows 0-7, up in rows 8-15
+            if (i < 4 * RT) {
+                const int t = i >> 3, r = i & 7;
+                float gs = 0.f, us = 0.f;
+#pragma unroll
+                for (int w = 0; w < C::kWaves; ++w) {
+                    gs += red[(w * 8 + t) * RT + r];
+                    us += red[(w * 8 + t) * RT + 8 + r];
+                }
+                if (t < nb && tl.row0 + r < tl.m) tl.y[t * tl.ldy + tl.row0 + r] = silu_mul_h(gs, us);
+            }
+        } else if (i < 8 * RT) {
             const int t = i / RT, r = i - t * RT;
             float sum = 0.f;
 #pragma unroll
             for (int w = 0; w < C::kWaves; ++w) sum += red[(w * 8 + t) * RT + r];
-            if (t < nb && row0 + r < M) Y[t * ldy + row0 + r] = f2h_bits(sum);
+            if (t < nb && tl.row0 + r < tl.m) tl.y[t * tl.ldy + tl.row0 + r] = f2h_bits(sum);
         }
         ++ck;
     };
@@ -1671,7 +1743,6 @@ __global__ __launch_bounds__(C::kWaves * 64) void gguf_gemv_q4_xreg(const uint8_
     int issued = min(Q, NS);  // stages of weights issued
     for (int q = 0; q < issued; ++q) issue();
 
-    // offset corrections of every block of the slice, once
     const half8_t kneg = {static_cast<half_t>(-1032.0f), static_cast<half_t>(-1032.0f), static_cast<half_t>(-1032.0f),
                           static_cast<half_t>(-1032.0f), static_cast<half_t>(-72.0f),   static_cast<half_t>(-72.0f),
                           static_cast<half_t>(-72.0f),   static_cast<half_t>(-72.0f)};
@@ -1729,19 +1800,29 @@ __global__ __launch_bounds__(C::kWaves * 64) void gguf_gemv_q4_xreg(const uint8_
     }
 }
 
-template <class C>
-int launch_q4_xreg(const void* w, const uint16_t* x, uint16_t* y, int M, int K, int64_t batch, int64_t ldx,
-                   int64_t ldy, hipStream_t stream) {
+template <class C, int MODE>
+int launch_q4_xreg(const bx::Target& tg, const uint16_t* x, int K, int64_t batch, int64_t ldx, hipStream_t stream) {
     constexpr size_t lds = C::kLdsBytes;
-    const void* fn = reinterpret_cast<const void*>(&gguf_gemv_q4_xreg<C>);
+    const void* fn = reinterpret_cast<const void*>(&gguf_gemv_q4_xreg<C, MODE>);
     if (int rc = prepare_lds(fn, lds)) return rc;
-    const int tiles = (M + bx::kRT - 1) / bx::kRT;
+    const int tiles = tg.tile_end[kMaxGroup - 1];
     const int resident = blocks_per_cu(fn, lds, C::kWaves * 64) * cu_count();
     if (resident < 1) return set_error(GDSLLM_ERR_UNSUPPORTED, "gguf_gemv_q4_xreg: no workgroup fits a compute unit");
     const int grid = std::min(tiles, resident);
-    hipLaunchKernelGGL((gguf_gemv_q4_xreg<C>), dim3(grid), dim3(C::kWaves * 64), lds, stream,
-                       static_cast<const uint8_t*>(w), x, y, M, K, static_cast<int>(batch), ldx, ldy);
+    hipLaunchKernelGGL((gguf_gemv_q4_xreg<C, MODE>), dim3(grid), dim3(C::kWaves * 64), lds, stream, tg, x, K,
+                       static_cast<int>(batch), ldx);
     return check_hip(hipGetLastError(), "gguf_gemv_q4_xreg launch");
+}
+
+// Target of one matrix: tiles of 16 rows.
+bx::Target xreg_single(const void* w, void* y, int M, int64_t ldy) {
+    bx::Target tg{};
+    tg.w[0] = static_cast<const uint8_t*>(w);
+    tg.y[0] = static_cast<uint16_t*>(y);
+    tg.ldy[0] = ldy;
+    tg.m[0] = M;
+    for (int i = 0; i < kMaxGroup; ++i) tg.tile_end[i] = (M + bx::kRT - 1) / bx::kRT;
+    return tg;
 }
 
 // Choice between the two batched Q4_0 kernels.  The x-in-registers kernel
@@ -2119,7 +2200,7 @@ int gemv(const char* name, const void* w, const void* x, void* y, int64_t out_di
     rc = GDSLLM_OK;
     if (F == Fmt::Q4_0 && fast && batch >= 3 && x_al16 && (use_q4_xreg(M, K) || use_q4_xreg_few(M, K, batch)) &&
         2 * (7 * ldx + K) < (int64_t{1} << 31)) {
-        const int rc2 = launch_q4_xreg<bx::Tall>(w, xp, yp, M, K, batch, ldx, ldy, s);
+        const int rc2 = launch_q4_xreg<bx::Tall, 0>(xreg_single(w, y, M, ldy), xp, K, batch, ldx, s);
         return rc2 == GDSLLM_OK ? ok() : rc2;
     }
     if (F == Fmt::Q4_0 && fast && (batch >= 3 || b2_codes) && K <= (1 << 20) && x_al16) {
@@ -2160,8 +2241,21 @@ int gemv(const char* name, const void* w, const void* x, void* y, int64_t out_di
     return ok();
 }
 
+// Batch 3-8 launches of the x-in-registers kernel over several matrices
+// (groups, gate/up pairs): in_dim a multiple of 256 up to 8192 (one slice of
+// x per wave), 16-byte aligned weights and x rows, x offsets within 2^31.
+bool xreg_fits(const uint8_t* const* w, int n, const void* x, int64_t K, int64_t batch, int64_t ldx) {
+    if (batch < 3 || K % 256 != 0 || K > 8192 || reinterpret_cast<uintptr_t>(x) % 16 != 0 || ldx % 8 != 0 ||
+        2 * (7 * ldx + K) >= (int64_t{1} << 31))
+        return false;
+    for (int i = 0; i < n; ++i)
+        if (reinterpret_cast<uintptr_t>(w[i]) % 16 != 0) return false;
+    return true;
+}
+
 // n matrices sharing x (q/k/v of one layer): one launch when the row-span
-// kernel serves the shape, else one GEMV per matrix.
+// kernel (batch 1-2) or the x-in-registers kernel (Q4_0, batch 3-8) serves
+// the shape, else one GEMV per matrix.
 template <Fmt F>
 int gemv_group(const char* name, int n, const void* const* w, void* const* y, const int64_t* out_dims,
                const void* x, int64_t in_dim, int64_t batch, int64_t ldx, void* stream) {
@@ -2189,13 +2283,28 @@ int gemv_group(const char* name, int n, const void* const* w, void* const* y, co
     const int rc = n == 1 ? try_rows<F, 0>(tg, x, static_cast<int>(in_dim), batch, ldx, as_stream(stream))
                           : try_rows<F, 1>(tg, x, static_cast<int>(in_dim), batch, ldx, as_stream(stream));
     if (rc != -1) return rc == GDSLLM_OK ? ok() : rc;
+    if (F == Fmt::Q4_0 && n > 1 && xreg_fits(tg.w, n, x, in_dim, batch, ldx)) {
+        // batch 3-8: the x-in-registers kernel over the matrices' 16-row tiles
+        bx::Target xt{};
+        int tiles = 0;
+        for (int i = 0; i < n; ++i) {
+            xt.w[i] = tg.w[i], xt.y[i] = tg.y[i], xt.ldy[i] = tg.ldy[i], xt.m[i] = tg.m[i];
+            tiles += (tg.m[i] + bx::kRT - 1) / bx::kRT;
+            xt.tile_end[i] = tiles;
+        }
+        for (int i = n; i < kMaxGroup; ++i) xt.tile_end[i] = tiles;
+        const int rc2 = launch_q4_xreg<bx::Tall, 1>(xt, static_cast<const uint16_t*>(x), static_cast<int>(in_dim),
+                                                    batch, ldx, as_stream(stream));
+        return rc2 == GDSLLM_OK ? ok() : rc2;
+    }
     for (int i = 0; i < n; ++i)
         if (int e = gemv<F>(name, w[i], x, y[i], out_dims[i], in_dim, batch, ldx, out_dims[i], stream)) return e;
     return ok();
 }
 
-// h = fp16(silu(gate x) * (up x)) in one launch (the row-span kernel with
-// gate/up pairing).
+// h = fp16(silu(gate x) * (up x)) in one launch (gate/up pairing in the
+// row-span kernel at batch 1-2, in the x-in-registers kernel for Q4_0 at
+// batch 3-8).
 template <Fmt F>
 int gate_up_silu(const char* name, const void* w_gate, const void* w_up, const void* x, void* h, int64_t out_dim,
                  int64_t in_dim, int64_t batch, int64_t ldx, int64_t ldh, void* stream) {
@@ -2213,10 +2322,19 @@ int gate_up_silu(const char* name, const void* w_gate, const void* w_up, const v
     tg.y[0] = static_cast<uint16_t*>(h);
     tg.ldy[0] = ldh;
     tg.m[0] = tg.m[1] = static_cast<int>(out_dim);
-    const int rc = try_rows<F, 2>(tg, x, static_cast<int>(in_dim), batch, ldx, as_stream(stream));
+    int rc = try_rows<F, 2>(tg, x, static_cast<int>(in_dim), batch, ldx, as_stream(stream));
+    if (rc == -1 && F == Fmt::Q4_0 && xreg_fits(tg.w, 2, x, in_dim, batch, ldx)) {
+        // batch 3-8: the x-in-registers kernel, 8 gate and 8 up rows per tile
+        bx::Target xt{};
+        xt.w[0] = tg.w[0], xt.w[1] = tg.w[1], xt.y[0] = tg.y[0], xt.ldy[0] = ldh, xt.m[0] = static_cast<int>(out_dim);
+        for (int i = 0; i < kMaxGroup; ++i) xt.tile_end[i] = static_cast<int>((out_dim + bx::kRT / 2 - 1) / (bx::kRT / 2));
+        rc = launch_q4_xreg<bx::Tall, 2>(xt, static_cast<const uint16_t*>(x), static_cast<int>(in_dim), batch, ldx,
+                                         as_stream(stream));
+    }
     if (rc == -1)
         return set_error(GDSLLM_ERR_UNSUPPORTED,
-                         nm + ": needs batch <= 2, in_dim % 256 == 0, 16-byte aligned weights and x (ldx % 8 == 0)");
+                         nm + ": needs in_dim % 256 == 0, 16-byte aligned weights and x (ldx % 8 == 0), and for "
+                              "batch 3-8 Q4_0 with in_dim <= 8192");
     return rc == GDSLLM_OK ? ok() : rc;
 }
 

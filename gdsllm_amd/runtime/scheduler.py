@@ -78,8 +78,9 @@ class DecodeSweep:
 
     layers[l]: the layer's weight dict (entries {"buffer", "shape",
     "gguf_type", "offset"} as ModelWeights.load_layer gives them); lm_head:
-    the lm_head entry.  All weights one GGUF type; batch 1 or 2 (the fused
-    gate/up/SiLU launch serves up to 2 rows).
+    the lm_head entry.  All weights one GGUF type; batch 1 or 2, and for
+    Q4_0 with hidden % 256 == 0 and hidden <= 8192 batch 1-8 (the batches
+    the fused gate/up/SiLU launch serves).
     """
 
     def __init__(self, layers: Sequence[dict], lm_head: dict, batch: int = 1, device=None, use_graph: bool = True):
@@ -87,8 +88,8 @@ class DecodeSweep:
 
         if not layers:
             raise ValueError("DecodeSweep: no layers")
-        if batch not in (1, 2):
-            raise ValueError("DecodeSweep: batch must be 1 or 2")
+        if not 1 <= batch <= 8:
+            raise ValueError("DecodeSweep: batch must be in [1, 8]")
         metas = [[lw[f"{p}.weight"] for p in _LAYER_PROJ] for lw in layers]
         fmt = lm_head.get("gguf_type")
         for lm in metas:
@@ -106,6 +107,8 @@ class DecodeSweep:
             if any(int(m["shape"][1]) != H for m in lm[:6]) or int(lm[6]["shape"][1]) != Fd or \
                     int(lm[6]["shape"][0]) != H or [int(v) for v in lm[5]["shape"]] != [Fd, H]:
                 raise ValueError("DecodeSweep: layer shapes disagree")
+        if batch > 2 and not (fmt == "q4_0" and H % 256 == 0 and H <= 8192):
+            raise ValueError("DecodeSweep: batch 3-8 needs Q4_0 weights with hidden % 256 == 0 and hidden <= 8192")
         self.hidden, self.ffn, self.vocab = H, Fd, int(lm_head["shape"][0])
 
         def buf(n):

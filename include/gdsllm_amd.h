@@ -134,8 +134,11 @@ int gdsllm_fused_int8_gemv(const void* weight, const void* scale, const void* x,
  * gdsllm_fused_q4_0_gemv / gdsllm_fused_q8_0_gemv on each matrix (the same
  * bits, except where the single GEMV of a matrix too short to give every
  * compute unit a workgroup, with in_dim over 2-4 windows of 4096, adds its
- * window sums in another order: equal to fp32 rounding); shapes the
- * single-launch kernel does not serve fall back to one launch per matrix.    */
+ * window sums in another order, and for Q4_0 at batch 3-8, where the group
+ * launch sums the same block products in the x-in-registers kernel's order:
+ * equal to fp32 rounding); shapes no single-launch kernel serves (batch 3-8
+ * Q8_0, in_dim > 8192 or not a multiple of 256 at batch 3-8, unaligned
+ * weights or x) fall back to one launch per matrix.                          */
 int gdsllm_fused_q4_0_gemv_group(int n, const void* const* weights, void* const* ys,
                                  const int64_t* out_dims, const void* x, int64_t in_dim,
                                  int64_t batch, int64_t ldx, void* stream);
@@ -145,8 +148,8 @@ int gdsllm_fused_q8_0_gemv_group(int n, const void* const* weights, void* const*
 /* h[b][r] = fp16(silu(g) * u) with g = fp16((W_gate x_b)[r]), u = fp16((W_up x_b)[r])
  * and torch's fp16 semantics (silu in fp32 rounded to fp16, then the product
  * rounded to fp16), in one launch; gate and up outputs never reach memory.
- * Needs batch <= 2, in_dim % 256 == 0, 16-byte aligned weights and x with
- * ldx % 8 == 0 (else GDSLLM_ERR_UNSUPPORTED).                                */
+ * Needs in_dim % 256 == 0, 16-byte aligned weights and x with ldx % 8 == 0,
+ * and at batch 3-8 Q4_0 with in_dim <= 8192 (else GDSLLM_ERR_UNSUPPORTED).  */
 int gdsllm_fused_q4_0_gate_up_silu(const void* w_gate, const void* w_up, const void* x, void* h,
                                    int64_t out_dim, int64_t in_dim, int64_t batch, int64_t ldx,
                                    int64_t ldh, void* stream);

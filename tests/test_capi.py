@@ -115,7 +115,10 @@ def test_gate_up_silu_validation():
         fn = getattr(lib, name)
         assert fn(16, 16, 16, 16, 4, 48, 1, 48, 4, None) == 1 and "multiple of 32" in _err()
         assert fn(None, 16, 16, 16, 4, 256, 1, 256, 4, None) == 1 and "null" in _err()
-        assert fn(16, 16, 16, 16, 4, 256, 3, 256, 4, None) == 2 and "batch <= 2" in _err()
+        # batch 3-8: Q4_0 with in_dim <= 8192 only (the launch itself needs a GPU)
+        assert fn(16, 16, 16, 16, 4, 8448, 3, 8448, 4, None) == 2 and "batch 3-8" in _err()
+        if "q8_0" in name:
+            assert fn(16, 16, 16, 16, 4, 256, 3, 256, 4, None) == 2 and "batch 3-8" in _err()
         assert fn(16, 16, 18, 16, 4, 256, 1, 256, 4, None) == 2  # x off the 16-byte grid
         assert fn(16, 16, 16, 16, 4, 96, 1, 96, 4, None) == 2  # in_dim % 256 != 0
         assert fn(None, None, None, None, 0, 256, 1, 256, 0, None) == 0

@@ -78,7 +78,10 @@ def _check_sweep(sweep, mats, head, fmt, tag):
     _check(sweep.logits, head, sweep.final_in.cpu(), fmt, sweep.final_in.shape[1], f"{tag} lm_head", 50)
 
 
-def test_decode_sweep_llama7b_shapes_graph(gpu):
+@pytest.mark.parametrize("B", [1, 4])
+def test_decode_sweep_llama7b_shapes_graph(gpu, B):
+    """Batch 1 (row-span launches) and batch 4 (the grouped q/k/v and the
+    gate/up/SiLU launches of the x-in-registers kernel)."""
     from gdsllm_amd.runtime import ext
     from gdsllm_amd.runtime.scheduler import DecodeSweep
 
@@ -86,13 +89,13 @@ def test_decode_sweep_llama7b_shapes_graph(gpu):
     layers, mats = zip(*(_layer(gpu, shapes, "q4_0", 9000 + i) for i in range(2)))
     head = syn.q4_0_weights(32000, 4096, torch.Generator(device=gpu).manual_seed(9100))
     lm = {"buffer": ext().GdsBufferHandle.from_tensor(head), "shape": [32000, 4096], "gguf_type": "q4_0", "offset": 0}
-    sweep = DecodeSweep(list(layers), lm, batch=1)
+    sweep = DecodeSweep(list(layers), lm, batch=B)
     assert sweep.launches_per_token == 9
     for token in range(2):
         _fill(sweep, 9200 + token)
         sweep.run()
         torch.cuda.synchronize()
-        _check_sweep(sweep, mats, head, "q4_0", f"token {token}")
+        _check_sweep(sweep, mats, head, "q4_0", f"B={B} token {token}")
 
 
 def test_decode_sweep_loaded_q8_0_batch2(gpu, tmp_path):
@@ -121,7 +124,7 @@ def test_decode_sweep_loaded_q8_0_batch2(gpu, tmp_path):
     _check_sweep(sweep, mats, raw(head["lm_head.weight"]), "q8_0", "q8_0 b2")
 
 
-@pytest.mark.parametrize("fmt,B", [("q4_0", 1), ("q8_0", 2)])
+@pytest.mark.parametrize("fmt,B", [("q4_0", 1), ("q8_0", 2), ("q4_0", 6), ("q8_0", 3)])
 def test_qkv_projections_and_mlp_decode(gpu, fmt, B):
     from gdsllm_amd.runtime import llama
 

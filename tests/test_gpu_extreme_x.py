@@ -162,3 +162,42 @@ def test_moe_gather_phase1_extreme_x(gpu, H, F, case):
             wt, st, bt = (t[e] for t in pools[part])
             deq = affine_dequant_np(wt, st, bt, g).reshape(F, H)
             assert_matches_reference(gu[j, part][None, :], deq, x, f"moe {case} slot {j} {'gate' if part == 0 else 'up'}")
+
+
+@pytest.mark.parametrize("case", CASES)
+@pytest.mark.parametrize("M,K,B", [(1000, 4096, 5), (200, 8192, 3), (40, 256, 8)], ids=["1000x4096_b5", "200x8192_b3",
+                                                                                       "40x256_b8"])
+def test_q4_0_group_gate_up_extreme_x(gpu, M, K, B, case):
+    """Batch 3-8 groups and gate/up pairs (the x-in-registers kernel, which
+    takes the offset-corrected products only where a wave's slice of x has no
+    dominant block and no non-finite value): gate and up from the grouped
+    launch follow the reference; h from the pair launch follows silu(g) * u
+    of those outputs (the same per-row sums) with torch's fp16 semantics,
+    NaN and infinities included."""
+    seed = 8300 + M + B
+    gg = torch.Generator(device=gpu).manual_seed(seed)
+    wg, wu = syn.q4_0_weights(M, K, gg), syn.q4_0_weights(M, K, gg)
+    x = make_x(case, B, K, seed + 1)
+    xd = torch.from_numpy(x).to(gpu)
+    g, u, h = (torch.empty(B, M, dtype=torch.float16, device=gpu) for _ in range(3))
+    check(capi().gdsllm_fused_q4_0_gemv_group(2, (ctypes.c_void_p * 2)(ptr(wg), ptr(wu)),
+                                              (ctypes.c_void_p * 2)(ptr(g), ptr(u)), (ctypes.c_int64 * 2)(M, M),
+                                              ptr(xd), K, B, K, stream()))
+    check(capi().gdsllm_fused_q4_0_gate_up_silu(ptr(wg), ptr(wu), ptr(xd), ptr(h), M, K, B, K, M, stream()))
+    torch.cuda.synchronize()
+    rows = _rows(M, seed)
+    idx = torch.as_tensor(rows, device=gpu)
+    for t, w, part in ((g, wg, "gate"), (u, wu, "up")):
+        deq = oq.dequant_q4_0(to_np(w[idx])).reshape(len(rows), K)
+        assert_matches_reference(to_np(t)[:, rows], deq, x, f"group {part} {M}x{K} B={B} {case}")
+    gn, un, hn = to_np(g), to_np(u), to_np(h).astype(np.float64)
+    with np.errstate(invalid="ignore", over="ignore"):
+        sg = oq.silu_fp16(gn)
+        href = (sg.astype(np.float32) * un.astype(np.float32)).astype(np.float16).astype(np.float64)
+        bound = oq.fp16_ulp(sg) * np.abs(un.astype(np.float64)) + oq.fp16_ulp(href)
+    assert np.array_equal(np.isnan(hn), np.isnan(href)), f"h NaN pattern differs ({case})"
+    inf = np.isinf(href)
+    assert np.array_equal(hn[inf], href[inf]), f"h infinities differ ({case})"
+    fin = np.isfinite(href) & np.isfinite(bound)
+    bad = np.abs(hn[fin] - href[fin]) > bound[fin]
+    assert not bad.any(), f"{int(bad.sum())} h values off ({case})"

@@ -88,7 +88,7 @@ def test_q4_0_prefill_gemm_512_tokens(gpu, M, K):
     _check_rows(y, w, x, _sample_rows(M, seed), K, f"prefill T{T} {M}x{K}")
 
 
-@pytest.mark.parametrize("B", [1, 2])
+@pytest.mark.parametrize("B", [1, 2, 4, 8])
 def test_q4_0_70b_qkv_group_and_gate_up_silu(gpu, B):
     """The fused 70B layer of the benchmark: q, k, v (8192, 1024, 1024 rows x
     8192) in one grouped launch and h = silu(gate x) * (up x) for 28672 x 8192

@@ -174,7 +174,18 @@ def test_capi_rejects_bad_shapes_before_launch(gpu):
 
 
 GROUP_CASES = [((256, 64, 64), 512, 1), ((4096, 1024, 1024), 4096, 1), ((33, 7, 129), 1024, 2), ((100,), 256, 1),
-               ((8, 16, 24, 40), 2048, 2), ((5, 0, 9), 512, 1)]
+               ((8, 16, 24, 40), 2048, 2), ((5, 0, 9), 512, 1),
+               # batch 3-8: Q4_0 takes the x-in-registers kernel over the matrices'
+               # 16-row tiles (part tiles, an empty matrix, 1-2 super-blocks per
+               # wave, 0 for most waves at in_dim 256); in_dim 544 and 8448 fall
+               # back to one GEMV per matrix
+               ((33, 7, 129), 1024, 3), ((8, 16, 24, 40), 2048, 5), ((5, 0, 9), 256, 8), ((1000, 200, 200), 4096, 4),
+               ((300, 40), 8192, 8), ((17, 64), 7936, 7), ((40, 9), 544, 4), ((20, 30), 8448, 3)]
+
+
+def _xreg_group(fmt, K, B):
+    """Whether a Q4_0 group or gate/up pair at batch 3-8 takes the x-in-registers kernel."""
+    return fmt == "q4_0" and B >= 3 and K % 256 == 0 and K <= 8192
 
 
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
@@ -182,7 +193,10 @@ GROUP_CASES = [((256, 64, 64), 512, 1), ((4096, 1024, 1024), 4096, 1), ((33, 7, 
 def test_gemv_group(gpu, fmt, Ms, K, B):
     """n matrices sharing x in one call: each output matches the oracle, and is
     bit-identical to the single-matrix GEMV of the same matrix (the rows of a
-    group are computed exactly like the rows of one matrix)."""
+    group are computed exactly like the rows of one matrix), except where a
+    Q4_0 group at batch 3-8 takes the x-in-registers kernel: the same block
+    products summed in another order than the single GEMV's kernel, so within
+    one fp16 ulp plus 2^-16 of ||w_r * x|| of it."""
     import ctypes
 
     make = syn.q4_0_weights if fmt == "q4_0" else syn.q8_0_weights
@@ -204,8 +218,16 @@ def test_gemv_group(gpu, fmt, Ms, K, B):
             assert np.all(to_np(ys[i]) == 7.0), "an empty matrix must not be written"
             continue
         y = to_np(ys[i])
-        assert_gemv_close(y, dq(to_np(ws[i])).reshape(M, K), to_np(x), f"{fmt} group[{i}] {M}x{K} B{B}")
-        assert np.array_equal(y, to_np(gguf_gemv(fmt, wd[i], xd, M, K))), f"group[{i}] differs from the single GEMV"
+        deq = dq(to_np(ws[i])).reshape(M, K)
+        assert_gemv_close(y, deq, to_np(x), f"{fmt} group[{i}] {M}x{K} B{B}")
+        single = to_np(gguf_gemv(fmt, wd[i], xd, M, K))
+        if not _xreg_group(fmt, K, B):
+            assert np.array_equal(y, single), f"group[{i}] differs from the single GEMV"
+            continue
+        a, b = y.astype(np.float64), single.astype(np.float64)
+        bound = oq.fp16_ulp(np.maximum(np.abs(a), np.abs(b))) + oq.row_norms(deq, to_np(x)) * 2.0 ** -16
+        bad = np.abs(a - b) > bound
+        assert not bad.any(), f"group[{i}]: {int(bad.sum())} outputs apart beyond reassociation"
 
 
 # Fewer row groups than compute units and in_dim over 2-4 windows of 4096:
@@ -239,7 +261,11 @@ def test_gemv_split_windows(gpu, fmt, B, M, K):
     assert not bad.any(), f"{int(bad.sum())} outputs apart beyond reassociation, first at {np.argwhere(bad)[0]}"
 
 
-GATE_UP_CASES = [(300, 1024, 1), (11008, 4096, 1), (7, 256, 2), (1025, 2048, 2), (4096, 11008, 1), (16001, 1024, 1)]
+GATE_UP_CASES = [(300, 1024, 1), (11008, 4096, 1), (7, 256, 2), (1025, 2048, 2), (4096, 11008, 1), (16001, 1024, 1),
+                 # batch 3-8: Q4_0 pairs 8 gate and 8 up rows per tile of the
+                 # x-in-registers kernel (part tiles at 300, 1037, 7 and 129
+                 # rows); Q8_0 and in_dim 11008 are refused
+                 (300, 1024, 3), (11008, 4096, 4), (1037, 8192, 8), (7, 256, 5), (129, 7936, 7), (4096, 11008, 3)]
 
 
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
@@ -248,7 +274,12 @@ def test_gate_up_silu(gpu, fmt, M, K, B):
     """h = fp16(silu(g) * u) in one call.  (1) Against g, u from the single
     GEMV (same per-row sums, bit for bit): h within one fp16 ulp of silu times
     |u| plus one ulp of h, the room the device's expf leaves against numpy's.
-    (2) End to end against the oracle's g, u: relative L2 of h."""
+    (2) End to end against the oracle's g, u: relative L2 of h.  At batch 3-8
+    g and u come from the grouped launch of the two matrices, whose rows the
+    pair launch computes the same way; the shapes no batch 3-8 launch serves
+    are refused with GDSLLM_ERR_UNSUPPORTED."""
+    import ctypes
+
     make = syn.q4_0_weights if fmt == "q4_0" else syn.q8_0_weights
     dq = oq.dequant_q4_0 if fmt == "q4_0" else oq.dequant_q8_0
     wg, wu = make(M, K, gen(7000 + M)), make(M, K, gen(7001 + K))
@@ -256,10 +287,22 @@ def test_gate_up_silu(gpu, fmt, M, K, B):
     wgd, wud, xd = wg.to(gpu), wu.to(gpu), x.to(gpu)
     h = torch.empty(B, M, dtype=torch.float16, device=gpu)
     fn = capi().gdsllm_fused_q4_0_gate_up_silu if fmt == "q4_0" else capi().gdsllm_fused_q8_0_gate_up_silu
-    check(fn(ptr(wgd), ptr(wud), ptr(xd), ptr(h), M, K, B, K, M, stream()))
+    rc = fn(ptr(wgd), ptr(wud), ptr(xd), ptr(h), M, K, B, K, M, stream())
+    if B >= 3 and not _xreg_group(fmt, K, B):
+        assert rc == 2, f"batch {B} {fmt} {M}x{K}: expected GDSLLM_ERR_UNSUPPORTED (2), got {rc}"
+        return
+    check(rc)
     torch.cuda.synchronize()
     hk = to_np(h).astype(np.float64)
-    g, u = to_np(gguf_gemv(fmt, wgd, xd, M, K)), to_np(gguf_gemv(fmt, wud, xd, M, K))
+    if B >= 3:
+        gd, ud = (torch.empty(B, M, dtype=torch.float16, device=gpu) for _ in range(2))
+        check(capi().gdsllm_fused_q4_0_gemv_group(2, (ctypes.c_void_p * 2)(ptr(wgd), ptr(wud)),
+                                                  (ctypes.c_void_p * 2)(ptr(gd), ptr(ud)), (ctypes.c_int64 * 2)(M, M),
+                                                  ptr(xd), K, B, K, stream()))
+        torch.cuda.synchronize()
+        g, u = to_np(gd), to_np(ud)
+    else:
+        g, u = to_np(gguf_gemv(fmt, wgd, xd, M, K)), to_np(gguf_gemv(fmt, wud, xd, M, K))
     sg = oq.silu_fp16(g)
     href = (sg.astype(np.float32) * u.astype(np.float32)).astype(np.float16)
     bound = oq.fp16_ulp(sg) * np.abs(u.astype(np.float64)) + oq.fp16_ulp(href)

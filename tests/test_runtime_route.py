@@ -116,3 +116,36 @@ def test_affine_prefill_route(monkeypatch, M, T, fused):
     y = qwen_moe.affine_q4_linear(torch.zeros(1, T, K), {"p.weight": meta}, "p")
     assert y.shape == (1, T, M)
     assert rec.calls == (["fused"] if fused else ["dequant"])
+
+
+class _Buf:
+    device_id = 0
+
+
+def _sweep_layer(fmt, H, F):
+    from gdsllm_amd.runtime.scheduler import _LAYER_PROJ
+
+    shapes = [[H, H]] * 4 + [[F, H]] * 2 + [[H, F]]
+    return {f"{p}.weight": {"buffer": _Buf(), "shape": s, "gguf_type": fmt, "offset": 0}
+            for p, s in zip(_LAYER_PROJ, shapes)}
+
+
+@pytest.mark.parametrize("fmt,H,B,ok", [("q4_0", 512, 3, True), ("q4_0", 8192, 8, True), ("q8_0", 512, 3, False),
+                                        ("q4_0", 8448, 4, False), ("q4_0", 544, 3, False), ("q8_0", 512, 2, True),
+                                        ("q4_0", 512, 9, False), ("q4_0", 512, 0, False)])
+def test_decode_sweep_batch_rule(monkeypatch, fmt, H, B, ok):
+    """DecodeSweep takes batch 1-2 for both GGUF types and batch 3-8 where the
+    fused gate/up/SiLU launch serves it (Q4_0, hidden % 256 == 0 and <= 8192);
+    the rest is refused before any device memory is allocated."""
+    from gdsllm_amd.runtime import scheduler
+
+    class Stop(Exception):
+        pass
+
+    def no_alloc(*a, **k):
+        raise Stop()
+
+    monkeypatch.setattr(scheduler.torch, "zeros", no_alloc)
+    lm = {"buffer": _Buf(), "shape": [640, H], "gguf_type": fmt, "offset": 0}
+    with pytest.raises(Stop if ok else ValueError):
+        scheduler.DecodeSweep([_sweep_layer(fmt, H, 2 * H)], lm, batch=B, device="cpu")

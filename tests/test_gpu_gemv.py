@@ -313,3 +313,50 @@ def test_gate_up_silu(gpu, fmt, M, K, B):
     h_oracle = (oq.silu_fp16(gq).astype(np.float32) * uq.astype(np.float32)).astype(np.float64)
     rel = float(np.linalg.norm(hk - h_oracle) / np.linalg.norm(h_oracle))
     assert rel <= oq.GEMV_REL_L2, f"h end-to-end rel L2 {rel:.3e}"
+
+
+@pytest.mark.parametrize("B", [3, 8])
+def test_batched_group_and_pair_strides_and_alignment(gpu, B):
+    """Batch 3-8 Q4_0 group and gate/up pair with x rows ldx > in_dim apart
+    and h rows ldh > out_dim apart (the pair writes only its columns), then
+    x off the 16-byte grid: the group falls back to one GEMV per matrix (the
+    single GEMVs' bits), the pair is refused with GDSLLM_ERR_UNSUPPORTED."""
+    import ctypes
+
+    M, K = 300, 2048
+    ldx, ldh = K + 72, M + 40
+    wg, wu = syn.q4_0_weights(M, K, gen(7300)), syn.q4_0_weights(M, K, gen(7301))
+    x = syn.activations(B, K, gen(7302))
+    wgd, wud = wg.to(gpu), wu.to(gpu)
+    xbuf = torch.zeros(B * ldx + 8, dtype=torch.float16, device=gpu)
+    xs = xbuf[: B * ldx].view(B, ldx)
+    xs[:, :K].copy_(x.to(gpu))
+    g, u = (torch.empty(B, M, dtype=torch.float16, device=gpu) for _ in range(2))
+    grp = capi().gdsllm_fused_q4_0_gemv_group
+    check(grp(2, (ctypes.c_void_p * 2)(ptr(wgd), ptr(wud)), (ctypes.c_void_p * 2)(ptr(g), ptr(u)),
+              (ctypes.c_int64 * 2)(M, M), ptr(xs), K, B, ldx, stream()))
+    hbuf = torch.full((B, ldh), 5.0, dtype=torch.float16, device=gpu)
+    check(capi().gdsllm_fused_q4_0_gate_up_silu(ptr(wgd), ptr(wud), ptr(xs), ptr(hbuf), M, K, B, ldx, ldh, stream()))
+    torch.cuda.synchronize()
+    dq = oq.dequant_q4_0
+    for t, w, part in ((g, wg, "gate"), (u, wu, "up")):
+        assert_gemv_close(to_np(t), dq(to_np(w)).reshape(M, K), to_np(x), f"strided group {part} B{B}")
+    hk = to_np(hbuf).astype(np.float64)
+    assert np.all(hk[:, M:] == 5.0), "the pair wrote past out_dim"
+    sg = oq.silu_fp16(to_np(g))
+    href = (sg.astype(np.float32) * to_np(u).astype(np.float32)).astype(np.float16)
+    bound = oq.fp16_ulp(sg) * np.abs(to_np(u).astype(np.float64)) + oq.fp16_ulp(href)
+    assert not (np.abs(hk[:, :M] - href.astype(np.float64)) > bound).any(), "strided pair h"
+    # x off the 16-byte grid (ldx stays a multiple of 8 elements)
+    xo = xbuf[1: 1 + B * ldx].view(B, ldx)
+    xo[:, :K].copy_(x.to(gpu))
+    g2, u2 = (torch.empty(B, M, dtype=torch.float16, device=gpu) for _ in range(2))
+    check(grp(2, (ctypes.c_void_p * 2)(ptr(wgd), ptr(wud)), (ctypes.c_void_p * 2)(ptr(g2), ptr(u2)),
+              (ctypes.c_int64 * 2)(M, M), ptr(xo), K, B, ldx, stream()))
+    gs = torch.empty(B, M, dtype=torch.float16, device=gpu)
+    check(capi().gdsllm_fused_q4_0_gemv(ptr(wgd), ptr(xo), ptr(gs), M, K, B, ldx, M, stream()))
+    torch.cuda.synchronize()
+    assert torch.equal(g2, gs), "unaligned x: the group's fallback differs from the single GEMV"
+    assert_gemv_close(to_np(u2), dq(to_np(wu)).reshape(M, K), to_np(x), f"unaligned group up B{B}")
+    rc = capi().gdsllm_fused_q4_0_gate_up_silu(ptr(wgd), ptr(wud), ptr(xo), ptr(hbuf), M, K, B, ldx, ldh, stream())
+    assert rc == 2, f"unaligned x at batch {B}: expected GDSLLM_ERR_UNSUPPORTED (2), got {rc}"

@@ -16,8 +16,9 @@ launch stream; `value` is the per-launch rate.
 Also reported (same JSON line): the LLaMA-7B Q4_0 decode weight sweep, all 32
 layers resident (7 projection GEMVs per layer + lm_head 32000 x 4096, one HIP
 graph per token) as tokens/s, fused (q/k/v grouped, gate+up+SiLU in one
-launch: 129 launches) and unfused (225 launches), and the CPU baseline (torch
-restatement of dequant -> F.linear in fp32 on the host cores).
+launch: 129 launches) and unfused (225 launches), the fused sweep at batch 4
+and 8 (tokens/s over the batch), and the CPU baseline (torch restatement of
+dequant -> F.linear in fp32 on the host cores).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -173,7 +174,9 @@ def bench_decode_sweep(args, dev):
     data flow (llama.py:212-256): q/k/v in one grouped launch on the attention
     input, o on the attention output, gate+up+SiLU in one launch writing h,
     down on that h; lm_head last.  Same weights, same 224 + 1 projections.
-    Returns (ms fused, ms unfused, weights)."""
+    The fused sweep is also timed at batch 4 and 8 (one decode step of B
+    sequences per replay).  Returns (ms fused, ms unfused, weights, {B: ms per
+    step})."""
     import torch
 
     from gdsllm_amd import synthetic as syn
@@ -201,8 +204,9 @@ def bench_decode_sweep(args, dev):
     def entry(w, m, k):
         return {"buffer": ext().GdsBufferHandle.from_tensor(w), "shape": [m, k], "gguf_type": "q4_0", "offset": 0}
 
-    sweep = DecodeSweep([{f"{n}.weight": entry(w, m, k) for n, w, (m, k) in zip(names, lw, LAYER_SHAPES)}
-                         for lw in layers], entry(lm_head, *LM_HEAD), batch=1, device=dev)
+    layer_entries = [{f"{n}.weight": entry(w, m, k) for n, w, (m, k) in zip(names, lw, LAYER_SHAPES)} for lw in layers]
+    head_entry = entry(lm_head, *LM_HEAD)
+    sweep = DecodeSweep(layer_entries, head_entry, batch=1, device=dev)
     for b in [*sweep.attn_in, *sweep.attn_out, *sweep.mlp_in, sweep.final_in]:
         b.copy_(syn.activations(1, b.shape[1], gen))
     sweep.run()
@@ -220,7 +224,26 @@ def bench_decode_sweep(args, dev):
     end.record()
     torch.cuda.synchronize()
     ms_fused = start.elapsed_time(end) / args.sweep_tokens
-    return ms_fused, ms_unfused, (layers, lm_head)
+
+    # the same weights at batch 4 and 8 (one decode step of B sequences per
+    # replay: grouped q/k/v and gate/up/SiLU on the batched kernel)
+    batched = {}
+    for B in (4, 8):
+        sw = DecodeSweep(layer_entries, head_entry, batch=B, device=dev)
+        for b in [*sw.attn_in, *sw.attn_out, *sw.mlp_in, sw.final_in]:
+            b.copy_(syn.activations(B, b.shape[1], gen))
+        for _ in range(3):
+            sw.run()
+        torch.cuda.synchronize()
+        _gpu_delay()
+        start.record()
+        for _ in range(args.sweep_tokens):
+            sw.run()
+        end.record()
+        torch.cuda.synchronize()
+        batched[B] = start.elapsed_time(end) / args.sweep_tokens
+        del sw
+    return ms_fused, ms_unfused, (layers, lm_head), batched
 
 
 _EAGER = False  # --profile-case: launch eagerly instead of replaying graphs
@@ -1238,13 +1261,16 @@ def main() -> int:
 
     sweep, sweep_weights = None, None
     if args.sweep_tokens > 0:
-        ms_tok, ms_unf, sweep_weights = bench_decode_sweep(args, dev)
+        ms_tok, ms_unf, sweep_weights, batched = bench_decode_sweep(args, dev)
         sb = sweep_bytes()
         sweep = {"tok_s": round(1e3 / ms_tok, 1), "ms_per_token": round(ms_tok, 4), "launches_per_token": 129,
                  "bytes_per_token": sb, "GB_s": round(sb / (ms_tok * 1e-3) / 1e9, 1),
                  "fusion": "q/k/v grouped launch; gate+up+SiLU launch writing h; o, down, lm_head single",
                  "unfused": {"tok_s": round(1e3 / ms_unf, 1), "ms_per_token": round(ms_unf, 4),
                              "launches_per_token": 225, "GB_s": round(sb / (ms_unf * 1e-3) / 1e9, 1)}}
+        for B, ms_b in batched.items():
+            sweep[f"batch_{B}"] = {"tok_s": round(B * 1e3 / ms_b, 1), "ms_per_step": round(ms_b, 4),
+                                   "launches_per_step": 129, "GB_s": round(sb / (ms_b * 1e-3) / 1e9, 1)}
         print(f"# 7B decode sweep: {ms_tok:.4f} ms/token, {sweep['tok_s']} tok/s, {sweep['GB_s']} GB/s "
               f"(unfused 225 launches: {sweep['unfused']['tok_s']} tok/s)", file=sys.stderr, flush=True)
 

@@ -1317,14 +1317,16 @@ template <int RT>
 constexpr int lds_bytes() { return kWaves * 2 * slot_bytes<RT>() + 2 * red_bytes<RT>(); }
 }  // namespace bq
 
-template <int RT>
+template <int RT, int XT>
 __global__ __launch_bounds__(bq::kWaves * 64) void gguf_gemv_q4_codes(const uint8_t* __restrict__ W,
                                                                      const uint16_t* __restrict__ X,
                                                                      uint16_t* __restrict__ Y, int M, int K, int nb,
                                                                      int64_t ldx, int64_t ldy) {
     constexpr int NRG = RT / 8;        // row groups of 8 per stage
     constexpr int NWD = bq::w_dma<RT>();
-    constexpr int kOps = NWD + 4;      // transfers per stage
+    // x transfers per stage: 4 (batch rows 0-7), or 2 where batch <= 4
+    static_assert(XT == 2 || XT == 4, "x transfers per stage");
+    constexpr int kOps = NWD + XT;     // transfers per stage
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int S = K >> 8;
@@ -1366,7 +1368,7 @@ __global__ __launch_bounds__(bq::kWaves * 64) void gguf_gemv_q4_codes(const uint
         const int row0 = RT * (static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) * ii);
         const uint16_t* xb = X + 256 * sb;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) dma16_asm(xoff[j], xb, slot + RT * 144 + bq::kXStride * j);
+        for (int j = 0; j < XT; ++j) dma16_asm(xoff[j], xb, slot + RT * 144 + bq::kXStride * j);
         const uint8_t* wb = W + static_cast<int64_t>(row0) * row_bytes + 144 * sb;
         uint32_t woff[NWD];
         const int nrows = min(RT, M - row0);
@@ -1388,7 +1390,9 @@ __global__ __launch_bounds__(bq::kWaves * 64) void gguf_gemv_q4_codes(const uint
     // per-lane operand geometry
     const int g = lane >> 4, j = lane & 15, par = j >> 3;
     // x: batch row j & 7 of block 2p + par, elements 4g.. and 16+4g.. (bytes +32)
-    const uint32_t xrd = (j & 7) / 2 * bq::kXStride + (j & 1) * 512 + 64 * par + 8 * g;
+    // (batch rows past nb read row nb - 1, which the transfers hold)
+    const int xt = min(j & 7, nb - 1);
+    const uint32_t xrd = xt / 2 * bq::kXStride + (xt & 1) * 512 + 64 * par + 8 * g;
     // weights: row 8rg + (j & 7), block 2p + par; qs dword g starts at byte
     // 144r + 18(2p + par) + 2 + 4g, which is 2 mod 4 for the even block
     const uint32_t wrd = 144 * (j & 7) + (par ? 20 : 0) + 4 * g;
@@ -1490,16 +1494,16 @@ __global__ __launch_bounds__(bq::kWaves * 64) void gguf_gemv_q4_codes(const uint
     }
 }
 
-template <int RT>
+template <int RT, int XT>
 int launch_q4_codes(const void* w, const uint16_t* x, uint16_t* y, int M, int K, int64_t batch, int64_t ldx,
                     int64_t ldy, hipStream_t stream) {
     constexpr size_t lds = bq::lds_bytes<RT>();
-    const void* fn = reinterpret_cast<const void*>(&gguf_gemv_q4_codes<RT>);
+    const void* fn = reinterpret_cast<const void*>(&gguf_gemv_q4_codes<RT, XT>);
     if (int rc = prepare_lds(fn, lds)) return rc;
     const int tiles = (M + RT - 1) / RT;
     const int resident = blocks_per_cu(fn, lds, bq::kWaves * 64) * cu_count();
     const int grid = std::min(tiles, resident);
-    hipLaunchKernelGGL((gguf_gemv_q4_codes<RT>), dim3(grid), dim3(bq::kWaves * 64), lds, stream,
+    hipLaunchKernelGGL((gguf_gemv_q4_codes<RT, XT>), dim3(grid), dim3(bq::kWaves * 64), lds, stream,
                        static_cast<const uint8_t*>(w), x, y, M, K, static_cast<int>(batch), ldx, ldy);
     return check_hip(hipGetLastError(), "gguf_gemv_q4_codes launch");
 }
@@ -2204,8 +2208,12 @@ int gemv(const char* name, const void* w, const void* x, void* y, int64_t out_di
         return rc2 == GDSLLM_OK ? ok() : rc2;
     }
     if (F == Fmt::Q4_0 && fast && (batch >= 3 || b2_codes) && K <= (1 << 20) && x_al16) {
-        const int rc2 = q4_codes_rows(M) == 32 ? launch_q4_codes<32>(w, xp, yp, M, K, batch, ldx, ldy, s)
-                                               : launch_q4_codes<16>(w, xp, yp, M, K, batch, ldx, ldy, s);
+        const bool x2 = batch <= 4;  // x rows 0-3 in two transfers per stage
+        const int rc2 = q4_codes_rows(M) == 32
+                            ? (x2 ? launch_q4_codes<32, 2>(w, xp, yp, M, K, batch, ldx, ldy, s)
+                                  : launch_q4_codes<32, 4>(w, xp, yp, M, K, batch, ldx, ldy, s))
+                            : (x2 ? launch_q4_codes<16, 2>(w, xp, yp, M, K, batch, ldx, ldy, s)
+                                  : launch_q4_codes<16, 4>(w, xp, yp, M, K, batch, ldx, ldy, s));
         return rc2 == GDSLLM_OK ? ok() : rc2;
     }
     if (fast && batch >= 3 && K <= (1 << 20) && x_al16) {

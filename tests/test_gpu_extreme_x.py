@@ -90,6 +90,7 @@ GGUF = [
     ("q4_0", 9000, 4096, 3, 0), ("q4_0", 9000, 4096, 8, 0),  # x in registers (uneven 32-row tiles)
     ("q4_0", 1024, 8192, 4, 0),                              # x in registers (few tiles)
     ("q4_0", 8192, 4096, 5, 0), ("q4_0", 256, 16384, 8, 0),  # code kernel
+    ("q4_0", 8192, 4096, 3, 0),                              # code kernel, x rows 0-3 only
     ("q4_0", 512, 4096, 4, 2),                               # staged (x off the 16-byte grid)
     ("q4_0", 64, 4128, 3, 0),                                # generic (in_dim % 256 != 0)
     ("q8_0", 512, 4096, 1, 0), ("q8_0", 300, 11008, 2, 0),   # row-span

@@ -1715,15 +1715,18 @@ __global__ __launch_bounds__(C::kWaves * 64) void gguf_gemv_q4_xreg(const bx::Ta
     }
 
     // x slice: 4 transfers per super-block into the wave's slots (transfer jj
-    // holds batch rows 2jj, 2jj+1, rows past nb repeat row nb - 1; the
-    // super-blocks past this wave's last repeat it), then into registers.
+    // holds batch rows 2jj, 2jj+1, rows past nb repeat row nb - 1; 2 where
+    // nb <= 4; the super-blocks past this wave's last repeat it), then into
+    // registers.
     half8_t xa[C::kNSB][4];
     {
+        const int nxt = nb <= 4 ? 2 : 4;
 #pragma unroll
         for (int s2 = 0; s2 < C::kNSB; ++s2) {
             const int sb = wave + C::kWaves * min(s2, nst - 1);
 #pragma unroll
             for (int jj = 0; jj < 4; ++jj) {
+                if (jj >= nxt) break;
                 const int tr = min(2 * jj + (lane >> 5), nb - 1);
                 dma16_asm(static_cast<uint32_t>(2 * (tr * ldx + 8 * (lane & 31))), X + 256 * sb,
                           slot0 + 4096 * s2 + 1024 * jj);

@@ -53,6 +53,7 @@ def _lm_head_proj(h: torch.Tensor, tensors: dict, key: str = "lm_head.weight",
 
 _LAYER_PROJ = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
                "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj")
+_UNSUPPORTED = 2  # GDSLLM_ERR_UNSUPPORTED: a valid request no fused kernel serves
 
 
 def _ptr(meta: dict) -> int:
@@ -78,9 +79,12 @@ class DecodeSweep:
 
     layers[l]: the layer's weight dict (entries {"buffer", "shape",
     "gguf_type", "offset"} as ModelWeights.load_layer gives them); lm_head:
-    the lm_head entry.  All weights one GGUF type; batch 1 or 2, and for
-    Q4_0 with hidden % 256 == 0 and hidden <= 8192 batch 1-8 (the batches
-    the fused gate/up/SiLU launch serves).
+    the lm_head entry.  All weights one GGUF type; batch 1-8.  Where the
+    fused gate/up/SiLU launch does not serve the shape (Q8_0 at batch 3-8, a
+    hidden size it refuses) the layer's MLP input runs through the gate and
+    up GEMVs into scratch rows and h = silu(g) * u comes from torch's fp16
+    ops, the reference's own composition (runtime/llama.py:253-256): 5
+    launches per layer instead of 4, in the same graph.
     """
 
     def __init__(self, layers: Sequence[dict], lm_head: dict, batch: int = 1, device=None, use_graph: bool = True):
@@ -107,8 +111,6 @@ class DecodeSweep:
             if any(int(m["shape"][1]) != H for m in lm[:6]) or int(lm[6]["shape"][1]) != Fd or \
                     int(lm[6]["shape"][0]) != H or [int(v) for v in lm[5]["shape"]] != [Fd, H]:
                 raise ValueError("DecodeSweep: layer shapes disagree")
-        if batch > 2 and not (fmt == "q4_0" and H % 256 == 0 and H <= 8192):
-            raise ValueError("DecodeSweep: batch 3-8 needs Q4_0 weights with hidden % 256 == 0 and hidden <= 8192")
         self.hidden, self.ffn, self.vocab = H, Fd, int(lm_head["shape"][0])
 
         def buf(n):
@@ -121,6 +123,9 @@ class DecodeSweep:
         self.final_in = buf(int(lm_head["shape"][1]))
         self.q, self.k, self.v, self.o = ([buf(int(lm[i]["shape"][0])) for lm in metas] for i in range(4))
         self.h = [buf(Fd) for _ in range(L)]
+        # gate and up rows for layers whose fused gate/up/SiLU launch is refused
+        self._g, self._u = buf(Fd), buf(Fd)
+        self.fused_gate_up = True
         self.down = [buf(H) for _ in range(L)]
         self.logits = buf(self.vocab)
         c_vp, c_i64 = ctypes.c_void_p, ctypes.c_int64
@@ -144,7 +149,14 @@ class DecodeSweep:
             mo, ko = (int(v) for v in lm[3]["shape"])
             check(gemv(_ptr(lm[3]), self.attn_out[i].data_ptr(), self.o[i].data_ptr(), mo, ko, B, ko, mo, s))
             rc = gate_up(_ptr(lm[4]), _ptr(lm[5]), self.mlp_in[i].data_ptr(), self.h[i].data_ptr(), Fd, H, B, H, Fd, s)
-            if rc != 0:
+            if rc == _UNSUPPORTED:
+                # refused before any launch: the reference's composition
+                self.fused_gate_up = False
+                x = self.mlp_in[i].data_ptr()
+                check(gemv(_ptr(lm[4]), x, self._g.data_ptr(), Fd, H, B, H, Fd, s))
+                check(gemv(_ptr(lm[5]), x, self._u.data_ptr(), Fd, H, B, H, Fd, s))
+                torch.mul(F.silu(self._g), self._u, out=self.h[i])
+            elif rc != 0:
                 check(rc)
             check(gemv(_ptr(lm[6]), self.h[i].data_ptr(), self.down[i].data_ptr(), H, Fd, B, Fd, H, s))
         mv, kv = self.vocab, int(self.lm_head["shape"][1])
@@ -166,4 +178,6 @@ class DecodeSweep:
 
     @property
     def launches_per_token(self) -> int:
-        return 4 * len(self.metas) + 1
+        """Projection launches per token (the SiLU and product of a refused
+        gate/up/SiLU launch not counted)."""
+        return (4 if self.fused_gate_up else 5) * len(self.metas) + 1

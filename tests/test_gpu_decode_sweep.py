@@ -6,8 +6,10 @@ runtime/scheduler.py:303-386) and the fused decode units of runtime/llama.py
 * LLaMA-7B Q4_0 shapes, two layers plus lm_head 32000x4096, replayed from its
   HIP graph on two tokens with different inputs (every output checked on
   sampled rows, so the graph reads the inputs written before each run);
-* a converted Q8_0 directory loaded by ModelWeights at batch 2, without the
-  graph;
+* LLaMA-7B Q4_0 shapes at batch 4 (the batch 3-8 grouped and paired launches);
+* a converted Q8_0 directory loaded by ModelWeights at batch 2 without the
+  graph, and at batch 3 (gate/up/SiLU as two GEMVs and torch's SiLU and
+  product) under the graph;
 * qkv_projections and mlp at decode against the reference composition.
 """
 
@@ -98,7 +100,12 @@ def test_decode_sweep_llama7b_shapes_graph(gpu, B):
         _check_sweep(sweep, mats, head, "q4_0", f"B={B} token {token}")
 
 
-def test_decode_sweep_loaded_q8_0_batch2(gpu, tmp_path):
+@pytest.mark.parametrize("B,graph", [(2, False), (3, True)])
+def test_decode_sweep_loaded_q8_0(gpu, tmp_path, B, graph):
+    """A converted Q8_0 directory at batch 2 (fused gate/up/SiLU) and at batch
+    3, where the fused launch is refused and the sweep runs the two GEMVs and
+    torch's SiLU and product, captured in the token's graph and replayed for
+    two tokens."""
     from gdsllm_amd.runtime.scheduler import DecodeSweep
     from gdsllm_amd.runtime.torch_bridge import ModelWeights
     from gdsllm_amd.synthetic_model import write_llama
@@ -109,10 +116,13 @@ def test_decode_sweep_loaded_q8_0_batch2(gpu, tmp_path):
     loaded = [mw.load_layer(i) for i in range(2)]
     head, _hh = mw.load_special("lm_head")
     layers = [t for t, _h in loaded]
-    sweep = DecodeSweep(layers, head["lm_head.weight"], batch=2, use_graph=False)
-    _fill(sweep, 9301)
-    sweep.run()
-    torch.cuda.synchronize()
+    sweep = DecodeSweep(layers, head["lm_head.weight"], batch=B, use_graph=graph)
+    for token in range(2 if graph else 1):
+        _fill(sweep, 9301 + token)
+        sweep.run()
+        torch.cuda.synchronize()
+    assert sweep.fused_gate_up == (B <= 2)
+    assert sweep.launches_per_token == (4 if B <= 2 else 5) * 2 + 1
 
     def raw(meta):
         from gdsllm_amd.runtime import ext
@@ -121,7 +131,7 @@ def test_decode_sweep_loaded_q8_0_batch2(gpu, tmp_path):
         return ext().view_tensor(meta["buffer"], [m, k // 32 * 34], "uint8", meta["offset"])
 
     mats = [[raw(lw[f"{p}.weight"]) for p in PROJ] for lw in layers]
-    _check_sweep(sweep, mats, raw(head["lm_head.weight"]), "q8_0", "q8_0 b2")
+    _check_sweep(sweep, mats, raw(head["lm_head.weight"]), "q8_0", f"q8_0 b{B}")
 
 
 @pytest.mark.parametrize("fmt,B", [("q4_0", 1), ("q8_0", 2), ("q4_0", 6), ("q8_0", 3)])

@@ -130,13 +130,14 @@ def _sweep_layer(fmt, H, F):
             for p, s in zip(_LAYER_PROJ, shapes)}
 
 
-@pytest.mark.parametrize("fmt,H,B,ok", [("q4_0", 512, 3, True), ("q4_0", 8192, 8, True), ("q8_0", 512, 3, False),
-                                        ("q4_0", 8448, 4, False), ("q4_0", 544, 3, False), ("q8_0", 512, 2, True),
-                                        ("q4_0", 512, 9, False), ("q4_0", 512, 0, False)])
+@pytest.mark.parametrize("fmt,H,B,ok", [("q4_0", 512, 3, True), ("q4_0", 8192, 8, True), ("q8_0", 512, 3, True),
+                                        ("q4_0", 8448, 4, True), ("q8_0", 544, 8, True), ("q8_0", 512, 2, True),
+                                        ("q4_0", 512, 9, False), ("q4_0", 512, 0, False), ("q5_0", 512, 1, False)])
 def test_decode_sweep_batch_rule(monkeypatch, fmt, H, B, ok):
-    """DecodeSweep takes batch 1-2 for both GGUF types and batch 3-8 where the
-    fused gate/up/SiLU launch serves it (Q4_0, hidden % 256 == 0 and <= 8192);
-    the rest is refused before any device memory is allocated."""
+    """DecodeSweep takes batch 1-8 for both GGUF types (a gate/up/SiLU launch
+    the fused kernel refuses runs as two GEMVs and torch's SiLU and product);
+    other batches and types are refused before any device memory is
+    allocated."""
     from gdsllm_amd.runtime import scheduler
 
     class Stop(Exception):

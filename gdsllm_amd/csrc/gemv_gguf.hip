@@ -1542,6 +1542,14 @@ struct Cfg {
 // kept in registers (batch 8, us): 28672x8192 31.7 / 34.3, 13003x4096
 // 13.7 / 15.8, 9000x5120 12.2 / 14.2.
 using Tall = Cfg<16, 2, 4>;
+// in_dim <= 4096: 8 waves x 2 super-blocks, 4 slots (80 KiB, two workgroups
+// per CU, each with its own barrier) where there are at least two 16-row
+// tiles per CU.  Batch 3 / 4 / 8 against Tall, us: 11008x4096 9.5 / 9.6 /
+// 10.1 against 11.0 / 11.1 / 11.7; 13003x4096 12.0 / 12.2 / 12.9 against
+// 13.9 / 13.9 / 14.4; the 7B q/k/v group 10.0 / 10.3 / 10.8 against 11.6 /
+// 11.8 / 12.2 and gate/up pair 17.4 / 17.5 / 18.0 against 19.9 / 20.0 /
+// 20.4; with one tile per CU (4096x4096 at batch 3) 5.45 against 5.17.
+using Half = Cfg<8, 2, 4>;
 
 // Where a launch reads weights and writes results.  MODE 0: one matrix
 // (w[0], y[0], m[0]); 1: up to 4 matrices of the same in_dim sharing x, whose
@@ -1819,6 +1827,19 @@ int launch_q4_xreg(const bx::Target& tg, const uint16_t* x, int K, int64_t batch
     hipLaunchKernelGGL((gguf_gemv_q4_xreg<C, MODE>), dim3(grid), dim3(C::kWaves * 64), lds, stream, tg, x, K,
                        static_cast<int>(batch), ldx);
     return check_hip(hipGetLastError(), "gguf_gemv_q4_xreg launch");
+}
+
+// Which configuration a launch takes: Half for in_dim <= 4096 with at least
+// two 16-row tiles per CU (tiles16: the launch's rows in 16-row tiles; a
+// gate/up pair counts both matrices, so it chooses as the group of the two
+// does and their sums keep the same bits), else Tall.
+inline bool xreg_half(int K, int64_t tiles16) { return K <= 4096 && tiles16 >= 2 * cu_count(); }
+
+template <int MODE>
+int launch_xreg(const bx::Target& tg, const uint16_t* x, int K, int64_t batch, int64_t ldx, int64_t tiles16,
+                hipStream_t stream) {
+    return xreg_half(K, tiles16) ? launch_q4_xreg<bx::Half, MODE>(tg, x, K, batch, ldx, stream)
+                                 : launch_q4_xreg<bx::Tall, MODE>(tg, x, K, batch, ldx, stream);
 }
 
 // Target of one matrix: tiles of 16 rows.
@@ -2207,7 +2228,7 @@ int gemv(const char* name, const void* w, const void* x, void* y, int64_t out_di
     rc = GDSLLM_OK;
     if (F == Fmt::Q4_0 && fast && batch >= 3 && x_al16 && (use_q4_xreg(M, K) || use_q4_xreg_few(M, K, batch)) &&
         2 * (7 * ldx + K) < (int64_t{1} << 31)) {
-        const int rc2 = launch_q4_xreg<bx::Tall, 0>(xreg_single(w, y, M, ldy), xp, K, batch, ldx, s);
+        const int rc2 = launch_xreg<0>(xreg_single(w, y, M, ldy), xp, K, batch, ldx, (M + 15) / 16, s);
         return rc2 == GDSLLM_OK ? ok() : rc2;
     }
     if (F == Fmt::Q4_0 && fast && (batch >= 3 || b2_codes) && K <= (1 << 20) && x_al16) {
@@ -2304,8 +2325,8 @@ int gemv_group(const char* name, int n, const void* const* w, void* const* y, co
             xt.tile_end[i] = tiles;
         }
         for (int i = n; i < kMaxGroup; ++i) xt.tile_end[i] = tiles;
-        const int rc2 = launch_q4_xreg<bx::Tall, 1>(xt, static_cast<const uint16_t*>(x), static_cast<int>(in_dim),
-                                                    batch, ldx, as_stream(stream));
+        const int rc2 = launch_xreg<1>(xt, static_cast<const uint16_t*>(x), static_cast<int>(in_dim), batch, ldx,
+                                       tiles, as_stream(stream));
         return rc2 == GDSLLM_OK ? ok() : rc2;
     }
     for (int i = 0; i < n; ++i)
@@ -2339,8 +2360,8 @@ int gate_up_silu(const char* name, const void* w_gate, const void* w_up, const v
         bx::Target xt{};
         xt.w[0] = tg.w[0], xt.w[1] = tg.w[1], xt.y[0] = tg.y[0], xt.ldy[0] = ldh, xt.m[0] = static_cast<int>(out_dim);
         for (int i = 0; i < kMaxGroup; ++i) xt.tile_end[i] = static_cast<int>((out_dim + bx::kRT / 2 - 1) / (bx::kRT / 2));
-        rc = launch_q4_xreg<bx::Tall, 2>(xt, static_cast<const uint16_t*>(x), static_cast<int>(in_dim), batch, ldx,
-                                         as_stream(stream));
+        rc = launch_xreg<2>(xt, static_cast<const uint16_t*>(x), static_cast<int>(in_dim), batch, ldx,
+                            2 * ((out_dim + bx::kRT - 1) / bx::kRT), as_stream(stream));
     }
     if (rc == -1)
         return set_error(GDSLLM_ERR_UNSUPPORTED,

@@ -1884,12 +1884,15 @@ inline bool use_q4_xreg_few(int M, int K, int64_t batch) {
 }
 
 // Row-tile height for the code kernel.  A 16-row stage moves 1.8 bytes of x
-// per weight byte (a 32-row one 0.9), which costs more than the uneven last
-// round of 32-row tiles (measured on MI355X: 28672x8192 at batch 8 40.8 us
-// with 32-row tiles, 47.1 us with 16; 8192x8192 13.3 vs 15.8 us), so 16-row
-// tiles serve only matrices too short to give half the CUs a 32-row tile
-// (1024x8192: 8.7 us against 11.6).
-inline int q4_codes_rows(int M) { return (M + 31) / 32 >= cu_count() / 2 ? 32 : 16; }
+// per weight byte (a 32-row one 0.9), which costs more than an uneven round
+// of 32-row tiles (measured on MI355X: 28672x8192 at batch 8 40.8 us with
+// 32-row tiles, 47.1 us with 16; 8192x8192 13.3 vs 15.8 us; 5120x13824 at
+// batch 3 / 8 15.3 / 17.8 against 16.7 / 24.2), so 16-row tiles serve only
+// matrices of at most one 16-row tile per CU, where 32-row tiles leave CUs
+// idle (1024x8192: 8.7 us against 11.6; 4096x11008 at batch 3 / 4 / 8: 8.8 /
+// 9.6 / 11.9 against 12.4 / 12.7 / 14.6; 4096x4096 at batch 8: 6.5 against
+// 7.8).
+inline int q4_codes_rows(int M) { return (M + 15) / 16 <= cu_count() ? 16 : 32; }
 
 // Any in_dim % 32 == 0 and any alignment: one wave per row, one lane per block,
 // byte loads, the reference's per-element order of operations.

@@ -5,6 +5,7 @@ geometry and the kernel chosen differ from the smaller test shapes:
   28672x8192, down 8192x28672) at batch 1, 2, 4 and 8, and the layer's
   decode-step fusions at batch 1 and 2 (q/k/v in one grouped launch,
   gate/up/SiLU in one launch);
+* the LLaMA-7B projections and lm_head at batch 3, 4 and 8;
 * the LLaMA-7B lm_head 32000x4096 as the batch-1 GEMV and as the 512-token
   prefill GEMM, and the 512-token GEMMs of gate/up 11008x4096 and down
   4096x11008.
@@ -26,6 +27,7 @@ from helpers import assert_gemv_close, capi, check, oq, ptr, stream, syn, to_np
 pytestmark = pytest.mark.gpu
 
 LAYER_70B = [(8192, 8192), (1024, 8192), (28672, 8192), (8192, 28672)]
+LAYER_7B = [(4096, 4096), (11008, 4096), (4096, 11008), (32000, 4096)]
 
 
 def _weights(M, K, seed, dev):
@@ -45,6 +47,24 @@ def _check_rows(y, w, x, rows, K, what):
     deq = oq.dequant_q4_0(to_np(w[torch.as_tensor(rows, device=w.device)])).reshape(len(rows), K)
     rel, mx = assert_gemv_close(yn[:, rows].astype(np.float16), deq, to_np(x), what)
     print(f"{what}: rel_l2={rel:.2e} max_norm={mx:.2e}")
+
+
+@pytest.mark.parametrize("B", [3, 4, 8])
+@pytest.mark.parametrize("M,K", LAYER_7B, ids=[f"{m}x{k}" for m, k in LAYER_7B])
+def test_q4_0_gemv_7b_batched_shapes(gpu, M, K, B):
+    """The LLaMA-7B projections at batch 3-8, as the batched decode sweep runs
+    them: the x-in-registers kernel's two-workgroup form (11008 and 32000
+    rows), the 16-wave form (4096x4096 at batch 3-4), the code kernel with
+    16-row tiles over 4096 rows (the down projection; 4096x4096 at batch
+    8)."""
+    seed = 3600 + M // 1024 + K // 1024 + B
+    w = _weights(M, K, seed, gpu)
+    x = syn.activations(B, K, torch.Generator().manual_seed(seed + 1))
+    xd = x.to(gpu)
+    y = torch.empty(B, M, dtype=torch.float16, device=gpu)
+    check(capi().gdsllm_fused_q4_0_gemv(ptr(w), ptr(xd), ptr(y), M, K, B, K, M, stream()))
+    torch.cuda.synchronize()
+    _check_rows(y, w, x, _sample_rows(M, seed), K, f"7B {M}x{K} B={B}")
 
 
 @pytest.mark.parametrize("B", [1, 2, 4, 8])

@@ -46,10 +46,12 @@ def test_gguf_gemv_b1(gpu, fmt, M, K):
 # row, and 20 / 11 super-blocks over 8 waves)
 # 24 x 8192, 50 x 5120 and 3000 x 7936 take the 16-wave x-in-registers
 # variant (2, 1 and 0 super-blocks per wave, a part tile), as does 2500 x
-# 3072 at batch 3-4 (12 super-blocks over 16 waves)
+# 3072 at batch 3-4 (12 super-blocks over 16 waves); 4090 x 9216 takes the
+# code kernel with 16-row tiles (one per CU, a part tile), and 9000 x 5120,
+# 13003 x 1024 and 8300 x 256 the x-in-registers kernel's two-workgroup form
 BATCHED_SHAPES = [(70, 4096), (33, 11008), (20, 96), (24, 8192), (9, 28672), (13003, 1024), (40, 256), (8200, 512),
                   (50, 5120), (1000, 2816), (4100, 6144), (9000, 5120), (8300, 256), (8500, 2816), (3000, 7936),
-                  (2500, 3072)]
+                  (2500, 3072), (4090, 9216)]
 
 
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])

@@ -2077,6 +2077,24 @@ bool plan_rows(RowsTarget& tg, int K, int& grid, int& wv, int& tmax) {
             resident = r8;
         }
     }
+    if constexpr (MODE == 2 && F == Fmt::Q4_0 && NB == 1) {
+        // Q4_0 pairs at batch 1 over one window whose two-row stages give the
+        // resident 4-wave waves more than 1.75 and at most 2 each: one 12-wave
+        // workgroup per CU, which loads x into each CU once instead of three
+        // times.  Measured (us, 4-wave against 12-wave): 11008 x 4096 (1.79
+        // stages per wave) 11.33-11.47 / 10.69-11.11, 12288 x 4096 (2.0)
+        // 12.16-12.29 / 11.85-11.89; outside the range 10240 x 4096 (1.67)
+        // 10.33-10.57 / 10.56-10.65, 8192 x 4096 8.88 / 9.96, 14336 x 4096
+        // 14.16 / 14.90.
+        const int w4 = resident * kWaves;
+        if (NW == 1 && 4 * rg_all > 7 * w4 && rg_all <= 2 * w4) {
+            const int r12 = rows_resident<F, NB, MODE, 12>(NW);
+            if (r12 >= cu_count()) {
+                wv = 12;
+                resident = r12;
+            }
+        }
+    }
     if (resident == 0) return false;
     int need[kMaxGroup], total = 0;
     for (int i = 0; i < parts; ++i) {
@@ -2153,6 +2171,13 @@ int launch_rows(const RowsTarget& tg, const uint16_t* x, int K, int64_t ldx, int
         }
         if (wv == 8) {
             hipLaunchKernelGGL((gguf_gemv_rows<F, NB, MODE, 8>), dim3(grid), dim3(8 * 64), lds, stream, tg, x, K, ldx);
+            return check_hip(hipGetLastError(), "gguf_gemv launch");
+        }
+    }
+    if constexpr (MODE == 2 && F == Fmt::Q4_0 && NB == 1) {
+        if (wv == 12) {
+            hipLaunchKernelGGL((gguf_gemv_rows<F, NB, MODE, 12>), dim3(grid), dim3(12 * 64), lds, stream, tg, x, K,
+                               ldx);
             return check_hip(hipGetLastError(), "gguf_gemv launch");
         }
     }

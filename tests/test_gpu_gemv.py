@@ -264,6 +264,8 @@ def test_gemv_split_windows(gpu, fmt, B, M, K):
 
 
 GATE_UP_CASES = [(300, 1024, 1), (11008, 4096, 1), (7, 256, 2), (1025, 2048, 2), (4096, 11008, 1), (16001, 1024, 1),
+                 # batch 1 on one 12-wave workgroup per CU (11008 x 4096 too)
+                 (11501, 2048, 1),
                  # batch 3-8: Q4_0 pairs 8 gate and 8 up rows per tile of the
                  # x-in-registers kernel (part tiles at 300, 1037, 7 and 129
                  # rows); Q8_0 and in_dim 11008 are refused

@@ -1,0 +1,233 @@
+"""Property tests over drawn shapes (Hypothesis): every dispatch path of the
+fused GEMVs, the grouped and gate/up launches and the dequant kernels, through
+the C ABI, against the oracle.
+
+Each example draws out_dim, in_dim, batch, the x and y row strides and an
+x start off the 16-byte grid, so the planner's choices (row-span, code and
+x-in-registers kernels, their 8/12/16-wave forms, staged and generic paths)
+are all reached over the run, and checks two properties: the result is
+within the oracle tolerance (per-row error beyond one fp16 ulp <= 1e-2 of
+||w_r * x||, and relative L2 <= 2e-3 over 256 or more outputs;
+oracle.quant.gemv_errors), and nothing
+outside the output rows is written (y padding columns keep a sentinel).
+Dequantization is checked bit for bit.  The draws are derandomized, so a run
+is reproducible and a failure names its example.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+from hypothesis import HealthCheck, given, settings
+from hypothesis import strategies as st
+
+from helpers import affine_dequant_np, capi, check, gen, oq, ptr, stream, syn, to_np
+
+pytestmark = pytest.mark.gpu
+
+PROPS = settings(max_examples=120, deadline=None, derandomize=True, database=None, print_blob=True,
+                 suppress_health_check=[HealthCheck.function_scoped_fixture, HealthCheck.too_slow])
+SENTINEL = 7.0
+
+# in_dim: multiples of 256 (the fast kernels) and of 32 only (the generic path)
+in_dims = st.one_of(st.integers(1, 36).map(lambda v: 256 * v), st.integers(1, 200).map(lambda v: 32 * v))
+
+
+def _x_strided(B, K, ldx, x_off, seed, dev):
+    """x rows ldx elements apart, starting x_off elements into the allocation."""
+    x = syn.activations(B, K, gen(seed))
+    buf = torch.zeros(x_off + B * ldx + 8, dtype=torch.float16)
+    for b in range(B):
+        buf[x_off + b * ldx: x_off + b * ldx + K] = x[b]
+    return x, buf.to(dev), x_off
+
+
+def _gemv_close(y_test, w_fp16, x_fp16, what):
+    """The parity bound of the GEMV tests: per row, the error beyond one fp16
+    ulp within 1e-2 of ||w_r * x|| (a row whose terms cancel has no relative
+    precision to keep); over at least 256 outputs also relative L2 <= 2e-3."""
+    y_ref = oq.gemv(w_fp16, x_fp16)
+    rel, mx = oq.gemv_errors(np.asarray(y_test, dtype=np.float64), y_ref, oq.row_norms(w_fp16, x_fp16))
+    assert np.all(np.isfinite(y_test)), f"{what}: non-finite output"
+    assert mx <= oq.GEMV_MAX_NORM, f"{what}: max normalized error {mx:.3e} > {oq.GEMV_MAX_NORM}"
+    if y_ref.size >= 256:
+        assert rel <= oq.GEMV_REL_L2, f"{what}: rel L2 {rel:.3e} > {oq.GEMV_REL_L2}"
+
+
+def _y_padded(B, M, ldy, dev):
+    return torch.full((B * ldy + 8,), SENTINEL, dtype=torch.float16, device=dev)
+
+
+def _y_rows(y, B, M, ldy):
+    yh = to_np(y)
+    rows = np.stack([yh[b * ldy: b * ldy + M] for b in range(B)])
+    pad = np.concatenate([yh[b * ldy + M: (b + 1) * ldy] for b in range(B)] + [yh[B * ldy:]])
+    return rows, pad
+
+
+@PROPS
+@given(fmt=st.sampled_from(["q4_0", "q8_0"]), M=st.integers(1, 700), K=in_dims, B=st.integers(1, 8),
+       ldx_pad=st.integers(0, 9), ldy_pad=st.integers(0, 5), x_off=st.sampled_from([0, 0, 0, 8, 1, 3]),
+       seed=st.integers(0, 2 ** 16))
+def test_gguf_gemv_property(gpu, fmt, M, K, B, ldx_pad, ldy_pad, x_off, seed):
+    make = syn.q4_0_weights if fmt == "q4_0" else syn.q8_0_weights
+    dq = oq.dequant_q4_0 if fmt == "q4_0" else oq.dequant_q8_0
+    w = make(M, K, gen(seed))
+    ldx, ldy = K + ldx_pad, M + ldy_pad
+    x, xbuf, off = _x_strided(B, K, ldx, x_off, seed + 1, gpu)
+    y = _y_padded(B, M, ldy, gpu)
+    fn = capi().gdsllm_fused_q4_0_gemv if fmt == "q4_0" else capi().gdsllm_fused_q8_0_gemv
+    wd = w.to(gpu)  # device copies stay referenced until the launch has run
+    check(fn(ptr(wd), xbuf.data_ptr() + 2 * off, ptr(y), M, K, B, ldx, ldy, stream()))
+    torch.cuda.synchronize()
+    rows, pad = _y_rows(y, B, M, ldy)
+    what = f"{fmt} {M}x{K} B{B} ldx {ldx} ldy {ldy} x+{off}"
+    assert np.all(pad == SENTINEL), f"{what}: written outside the output rows"
+    _gemv_close(rows, dq(to_np(w)).reshape(M, K), to_np(x), what)
+
+
+# Matrices with thousands of rows: the launch plans that need many row groups
+# or tiles per CU (the 12-wave gate/up pairs, the two-workgroup batched form,
+# 16-row code-kernel tiles, two stage buffers per wave)
+LARGE = settings(PROPS, max_examples=12)
+large_rows = st.integers(4000, 13000)
+large_in = st.sampled_from([1024, 2048, 3072, 4096, 5120])
+
+
+@LARGE
+@given(fmt=st.sampled_from(["q4_0", "q8_0"]), M=large_rows, K=large_in, B=st.integers(1, 8),
+       seed=st.integers(0, 2 ** 16))
+def test_gguf_gemv_large_property(gpu, fmt, M, K, B, seed):
+    test_gguf_gemv_property.hypothesis.inner_test(gpu, fmt, M, K, B, 0, 3, 0, seed)
+
+
+@LARGE
+@given(fmt=st.sampled_from(["q4_0", "q8_0"]), M=large_rows, K=large_in, B=st.integers(1, 8),
+       seed=st.integers(0, 2 ** 16))
+def test_gate_up_silu_large_property(gpu, fmt, M, K, B, seed):
+    test_gate_up_silu_property.hypothesis.inner_test(gpu, fmt, M, K, B, 2, seed)
+
+
+@PROPS
+@given(fmt=st.sampled_from(["q4_0", "q8_0"]), Ms=st.lists(st.integers(0, 500), min_size=1, max_size=4),
+       K=in_dims, B=st.integers(1, 8), seed=st.integers(0, 2 ** 16))
+def test_gemv_group_property(gpu, fmt, Ms, K, B, seed):
+    make = syn.q4_0_weights if fmt == "q4_0" else syn.q8_0_weights
+    dq = oq.dequant_q4_0 if fmt == "q4_0" else oq.dequant_q8_0
+    n = len(Ms)
+    ws = [make(M, K, gen(seed + i)) if M else None for i, M in enumerate(Ms)]
+    x = syn.activations(B, K, gen(seed + 10))
+    xd = x.to(gpu)
+    wd = [w.to(gpu) if w is not None else None for w in ws]
+    ys = [_y_padded(B, M, M, gpu) for M in Ms]
+    fn = capi().gdsllm_fused_q4_0_gemv_group if fmt == "q4_0" else capi().gdsllm_fused_q8_0_gemv_group
+    check(fn(n, (ctypes.c_void_p * n)(*[ptr(w) if w is not None else None for w in wd]),
+             (ctypes.c_void_p * n)(*[ptr(y) for y in ys]), (ctypes.c_int64 * n)(*Ms), ptr(xd), K, B, K, stream()))
+    torch.cuda.synchronize()
+    for i, M in enumerate(Ms):
+        rows, pad = _y_rows(ys[i], B, M, M)
+        what = f"{fmt} group[{i}] of {Ms} x {K} B{B}"
+        assert np.all(pad == SENTINEL), f"{what}: written past its rows"
+        if M:
+            _gemv_close(rows, dq(to_np(ws[i])).reshape(M, K), to_np(x), what)
+
+
+@PROPS
+@given(fmt=st.sampled_from(["q4_0", "q8_0"]), M=st.integers(1, 600), K=in_dims, B=st.integers(1, 8),
+       ldh_pad=st.integers(0, 4), seed=st.integers(0, 2 ** 16))
+def test_gate_up_silu_property(gpu, fmt, M, K, B, ldh_pad, seed):
+    """h = fp16(silu(g) * u) against the oracle's g and u, element by element
+    within the GEMV tolerance carried through silu and the product (a g or u
+    that cancels to near zero has no relative precision), and over many
+    elements by relative L2; a batch 3-8 shape the pair launch does not serve
+    is refused with GDSLLM_ERR_UNSUPPORTED and writes nothing."""
+    make = syn.q4_0_weights if fmt == "q4_0" else syn.q8_0_weights
+    dq = oq.dequant_q4_0 if fmt == "q4_0" else oq.dequant_q8_0
+    wg, wu = make(M, K, gen(seed)), make(M, K, gen(seed + 1))
+    x = syn.activations(B, K, gen(seed + 2))
+    ldh = M + ldh_pad
+    h = _y_padded(B, M, ldh, gpu)
+    fn = capi().gdsllm_fused_q4_0_gate_up_silu if fmt == "q4_0" else capi().gdsllm_fused_q8_0_gate_up_silu
+    wgd, wud, xd = wg.to(gpu), wu.to(gpu), x.to(gpu)
+    rc = fn(ptr(wgd), ptr(wud), ptr(xd), ptr(h), M, K, B, K, ldh, stream())
+    torch.cuda.synchronize()
+    what = f"{fmt} gate/up {M}x{K} B{B} ldh {ldh}"
+    served = B <= 2 and K % 256 == 0 or (B <= 8 and fmt == "q4_0" and K % 256 == 0 and K <= 8192)
+    if not served:
+        assert rc == 2, f"{what}: expected GDSLLM_ERR_UNSUPPORTED (2), got {rc}"
+        assert np.all(to_np(h) == SENTINEL), f"{what}: a refused call wrote h"
+        return
+    check(rc)
+    rows, pad = _y_rows(h, B, M, ldh)
+    assert np.all(pad == SENTINEL), f"{what}: written outside h's rows"
+    wgq, wuq = dq(to_np(wg)).reshape(M, K), dq(to_np(wu)).reshape(M, K)
+    gx, ux = oq.gemv(wgq, to_np(x)), oq.gemv(wuq, to_np(x))
+    gq, uq = gx.astype(np.float16), ux.astype(np.float16)
+    h_oracle = (oq.silu_fp16(gq).astype(np.float32) * uq.astype(np.float32)).astype(np.float64)
+    hk = rows.astype(np.float64)
+    # each h within what the GEMV tolerance on g and u (one fp16 ulp plus
+    # 1e-2 of ||w_r * x||) carries through silu (slope below 1.1) and the
+    # product, plus the roundings of silu and of h
+    dg = oq.fp16_ulp(gx) + oq.GEMV_MAX_NORM * oq.row_norms(wgq, to_np(x))
+    du = oq.fp16_ulp(ux) + oq.GEMV_MAX_NORM * oq.row_norms(wuq, to_np(x))
+    sx = gx / (1.0 + np.exp(-np.clip(gx, -60, 60)))
+    ds = 1.1 * dg + oq.fp16_ulp(sx)
+    bound = np.abs(sx) * du + np.abs(ux) * ds + ds * du + 2 * oq.fp16_ulp(h_oracle)
+    bad = np.abs(hk - h_oracle) > bound
+    assert not bad.any(), f"{what}: {int(bad.sum())} h values beyond the carried GEMV tolerance"
+    if M * B >= 256:
+        rel = float(np.linalg.norm(hk - h_oracle) / max(np.linalg.norm(h_oracle), 1e-30))
+        assert rel <= oq.GEMV_REL_L2, f"{what}: h rel L2 {rel:.3e}"
+
+
+@PROPS
+@given(g=st.sampled_from([32, 64, 128]), M=st.integers(1, 500), kg=st.integers(1, 40), B=st.integers(1, 8),
+       ldx_pad=st.integers(0, 9), ldy_pad=st.integers(0, 5), seed=st.integers(0, 2 ** 16))
+def test_affine_gemv_property(gpu, g, M, kg, B, ldx_pad, ldy_pad, seed):
+    K = g * kg
+    words, scales, biases = syn.affine_q4_weights([M, K], g, gen(seed))
+    ldx, ldy = K + ldx_pad, M + ldy_pad
+    x, xbuf, off = _x_strided(B, K, ldx, 0, seed + 1, gpu)
+    y = _y_padded(B, M, ldy, gpu)
+    wd, sd, bd = words.to(gpu), scales.to(gpu), biases.to(gpu)
+    check(capi().gdsllm_fused_affine_q4_gemv(ptr(wd), ptr(sd), ptr(bd), xbuf.data_ptr(), ptr(y), M, K, g, B, ldx, ldy,
+                                             stream()))
+    torch.cuda.synchronize()
+    rows, pad = _y_rows(y, B, M, ldy)
+    what = f"affine g{g} {M}x{K} B{B} ldx {ldx} ldy {ldy}"
+    assert np.all(pad == SENTINEL), f"{what}: written outside the output rows"
+    _gemv_close(rows, affine_dequant_np(words, scales, biases, g).reshape(M, K), to_np(x), what)
+
+
+@PROPS
+@given(fmt=st.sampled_from(["q4_0", "q8_0"]), nblk=st.integers(1, 5000), seed=st.integers(0, 2 ** 16))
+def test_gguf_dequant_property(gpu, fmt, nblk, seed):
+    """Bit for bit, on raw blocks with every scale bit pattern allowed
+    (subnormal, infinite and NaN scales included)."""
+    bb = 18 if fmt == "q4_0" else 34
+    raw = torch.randint(0, 256, (nblk * bb,), dtype=torch.uint8, generator=gen(seed))
+    out = torch.full((nblk * 32 + 8,), SENTINEL, dtype=torch.float16, device=gpu)
+    fn = capi().gdsllm_dequant_q4_0 if fmt == "q4_0" else capi().gdsllm_dequant_q8_0
+    rd = raw.to(gpu)
+    check(fn(ptr(rd), ptr(out), nblk, stream()))
+    torch.cuda.synchronize()
+    got = to_np(out).view(np.uint16)
+    ref = (oq.dequant_q4_0 if fmt == "q4_0" else oq.dequant_q8_0)(to_np(raw)).reshape(-1).view(np.uint16)
+    assert np.array_equal(got[: nblk * 32], ref), f"{fmt} {nblk} blocks: bits differ"
+    assert np.all(to_np(out)[nblk * 32:] == SENTINEL), f"{fmt} {nblk} blocks: written past the end"
+
+
+@PROPS
+@given(g=st.sampled_from([32, 64, 128]), rows=st.integers(1, 300), kg=st.integers(1, 24), seed=st.integers(0, 2 ** 16))
+def test_affine_dequant_property(gpu, g, rows, kg, seed):
+    cols = g * kg
+    words, scales, biases = syn.affine_q4_weights([rows, cols], g, gen(seed))
+    n = rows * cols
+    out = torch.full((n + 8,), SENTINEL, dtype=torch.float16, device=gpu)
+    wd, sd, bd = words.to(gpu), scales.to(gpu), biases.to(gpu)
+    check(capi().gdsllm_dequant_affine_q4(ptr(wd), ptr(sd), ptr(bd), ptr(out), n, cols, g, stream()))
+    torch.cuda.synchronize()
+    ref = affine_dequant_np(words, scales, biases, g).reshape(-1).view(np.uint16)
+    assert np.array_equal(to_np(out)[:n].view(np.uint16), ref), f"affine g{g} {rows}x{cols}: bits differ"
+    assert np.all(to_np(out)[n:] == SENTINEL), f"affine g{g} {rows}x{cols}: written past the end"

@@ -139,7 +139,80 @@ def double_rounding_cases(n: int, seed: int):
     return nib.astype(np.uint32), s, b
 
 
+def moe_pool(E, H, F, g, seed, device="cpu"):
+    """Stacked affine-Q4 gate, up [E, F, H] and down [E, H, F] pools (words, scales, biases)."""
+    gg = gen(seed) if device == "cpu" else torch.Generator(device=device).manual_seed(seed)
+    gate = syn.affine_q4_weights([E, F, H], g, gg)
+    up = syn.affine_q4_weights([E, F, H], g, gg)
+    down = syn.affine_q4_weights([E, H, F], g, gg)
+    return gate, up, down
+
+
+def expert_fn(pool, g, E):
+    """e -> expert e's dequantized fp16 matrix (None outside [0, E)), for the oracle."""
+    def f(e):
+        if e < 0 or e >= E:
+            return None
+        w, s, b = (t[e].cpu() for t in pool)
+        N = w.shape[0]
+        return affine_dequant_np(w, s, b, g).reshape(N, -1)
+    return f
+
+
+def check_moe(y, ws, gate, up, down, x, idx, wts, g, E, hk=None):
+    """Three checks.  (1) phase 1: the fp16 gate/up rows in the workspace match
+    the oracle GEMVs under the GEMV tolerance, and h (when the kernel stores it)
+    is within one fp16 ulp of fp16(fp16(silu(g)) * u) built from those rows.
+    (2) phase 2: y matches the oracle's weighted down-projection of the
+    kernel's h (or of h built from its g/u), under the GEMV tolerance.  (3) end
+    to end: y matches the all-oracle result in relative L2 (one-ulp fp16
+    differences in g/u move h, so the per-row bound is not applied end to end)."""
+    xn = to_np(x).reshape(-1)
+    gf, uf, dn = expert_fn(gate, g, E), expert_fn(up, g, E), expert_fn(down, g, E)
+    wsn = to_np(ws)
+    hkn = to_np(hk) if hk is not None else None
+    for k, e in enumerate(idx):
+        e = int(e)
+        if gf(e) is None:
+            assert np.all(wsn[k] == 0), "rows of an out-of-range expert must be zero"
+            continue
+        assert_gemv_close(wsn[k, 0][None, :], gf(e), xn[None, :], f"gate k={k}")
+        assert_gemv_close(wsn[k, 1][None, :], uf(e), xn[None, :], f"up k={k}")
+    ref2 = None
+    norm2 = 0.0
+    for k, e in enumerate(idx):
+        e = int(e)
+        if gf(e) is None:
+            continue
+        h = (oq.silu_fp16(wsn[k, 0]).astype(np.float32) * wsn[k, 1].astype(np.float32)).astype(np.float16)
+        if hkn is not None:
+            # expf on the GPU and numpy's exp may round fp32 exp(-g) differently, which
+            # can move fp16(silu(g)) by one ulp; h = fp16(silu * u) then moves by up to
+            # that ulp times |u| plus its own rounding step
+            sg = oq.silu_fp16(wsn[k, 0])
+            bound = oq.fp16_ulp(sg) * np.abs(wsn[k, 1].astype(np.float64)) + oq.fp16_ulp(h)
+            bad = np.abs(hkn[k].astype(np.float64) - h.astype(np.float64)) > bound
+            if bad.any():
+                i = int(np.argmax(bad))
+                raise AssertionError(f"h k={k}: {int(bad.sum())} of {bad.size} differ; first n={i}: kernel {hkn[k][i]} "
+                                     f"expected {h[i]} from g={wsn[k, 0][i]} u={wsn[k, 1][i]}; bad n: {np.nonzero(bad)[0][:16]}")
+            h = hkn[k]
+        wk = float(np.float16(to_np(wts)[k]))
+        part = oq.gemv(dn(e), h)[0] * wk
+        ref2 = part if ref2 is None else ref2 + part
+        norm2 = norm2 + (wk ** 2) * oq.row_norms(dn(e), h)[0] ** 2
+    rel2, mx2 = oq.gemv_errors(to_np(y).astype(np.float64), ref2, np.sqrt(norm2))
+    assert rel2 <= oq.GEMV_REL_L2, f"moe phase-2 rel L2 {rel2:.3e}"
+    assert mx2 <= oq.GEMV_MAX_NORM, f"moe phase-2 max normalized {mx2:.3e}"
+    ref, _ = oq.moe_gather(xn, gf, uf, dn, idx, to_np(wts))
+    rel = float(np.linalg.norm(to_np(y).astype(np.float64) - ref) / np.linalg.norm(ref))
+    assert rel <= oq.GEMV_REL_L2, f"moe end-to-end rel L2 {rel:.3e}"
+    print(f"moe phase2 rel={rel2:.2e} max={mx2:.2e} end-to-end rel={rel:.2e}")
+    return rel2, mx2
+
+
 __all__ = [
     "gen", "stream", "ptr", "to_np", "on_gpu", "assert_gemv_close", "gguf_gemv", "affine_gemv", "moe_gather",
     "experts_struct", "writes_h", "affine_dequant_np", "double_rounding_cases", "syn", "oq", "capi", "check",
+    "moe_pool", "expert_fn", "check_moe",
 ]

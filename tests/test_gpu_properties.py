@@ -22,7 +22,7 @@ import torch
 from hypothesis import HealthCheck, given, settings
 from hypothesis import strategies as st
 
-from helpers import affine_dequant_np, capi, check, gen, oq, ptr, stream, syn, to_np
+from helpers import affine_dequant_np, capi, check, check_moe, gen, moe_gather, moe_pool, oq, ptr, stream, syn, to_np
 
 pytestmark = pytest.mark.gpu
 
@@ -161,24 +161,7 @@ def test_gate_up_silu_property(gpu, fmt, M, K, B, ldh_pad, seed):
     check(rc)
     rows, pad = _y_rows(h, B, M, ldh)
     assert np.all(pad == SENTINEL), f"{what}: written outside h's rows"
-    wgq, wuq = dq(to_np(wg)).reshape(M, K), dq(to_np(wu)).reshape(M, K)
-    gx, ux = oq.gemv(wgq, to_np(x)), oq.gemv(wuq, to_np(x))
-    gq, uq = gx.astype(np.float16), ux.astype(np.float16)
-    h_oracle = (oq.silu_fp16(gq).astype(np.float32) * uq.astype(np.float32)).astype(np.float64)
-    hk = rows.astype(np.float64)
-    # each h within what the GEMV tolerance on g and u (one fp16 ulp plus
-    # 1e-2 of ||w_r * x||) carries through silu (slope below 1.1) and the
-    # product, plus the roundings of silu and of h
-    dg = oq.fp16_ulp(gx) + oq.GEMV_MAX_NORM * oq.row_norms(wgq, to_np(x))
-    du = oq.fp16_ulp(ux) + oq.GEMV_MAX_NORM * oq.row_norms(wuq, to_np(x))
-    sx = gx / (1.0 + np.exp(-np.clip(gx, -60, 60)))
-    ds = 1.1 * dg + oq.fp16_ulp(sx)
-    bound = np.abs(sx) * du + np.abs(ux) * ds + ds * du + 2 * oq.fp16_ulp(h_oracle)
-    bad = np.abs(hk - h_oracle) > bound
-    assert not bad.any(), f"{what}: {int(bad.sum())} h values beyond the carried GEMV tolerance"
-    if M * B >= 256:
-        rel = float(np.linalg.norm(hk - h_oracle) / max(np.linalg.norm(h_oracle), 1e-30))
-        assert rel <= oq.GEMV_REL_L2, f"{what}: h rel L2 {rel:.3e}"
+    _h_close(rows, dq(to_np(wg)).reshape(M, K), dq(to_np(wu)).reshape(M, K), to_np(x), what)
 
 
 @PROPS
@@ -231,3 +214,116 @@ def test_affine_dequant_property(gpu, g, rows, kg, seed):
     ref = affine_dequant_np(words, scales, biases, g).reshape(-1).view(np.uint16)
     assert np.array_equal(to_np(out)[:n].view(np.uint16), ref), f"affine g{g} {rows}x{cols}: bits differ"
     assert np.all(to_np(out)[n:] == SENTINEL), f"affine g{g} {rows}x{cols}: written past the end"
+
+
+GEMM_FORMATS = ["q4_0", "q8_0", "aff32", "aff64", "aff128"]
+
+
+@PROPS
+@given(fmt=st.sampled_from(GEMM_FORMATS), M=st.integers(1, 700), K=in_dims, T=st.integers(1, 300),
+       ldx_pad=st.integers(0, 3), ldy_pad=st.integers(0, 5), seed=st.integers(0, 2 ** 16))
+def test_dequant_gemm_property(gpu, fmt, M, K, T, ldx_pad, ldy_pad, seed):
+    """The prefill dequant-GEMM (every tile shape the planner picks) on T
+    tokens; Q8_0 and affine weights off the 256 grid are refused with
+    GDSLLM_ERR_UNSUPPORTED and write nothing."""
+    g = int(fmt[3:]) if fmt.startswith("aff") else 0
+    if g and K % g:
+        K = max(g, K // g * g)
+    ldx, ldy = K + 8 * ldx_pad, M + ldy_pad
+    x, xbuf, _ = _x_strided(T, K, ldx, 0, seed + 1, gpu)
+    y = _y_padded(T, M, ldy, gpu)
+    what = f"{fmt} gemm {M}x{K} T{T} ldx {ldx} ldy {ldy}"
+    if g:
+        words, scales, biases = syn.affine_q4_weights([M, K], g, gen(seed))
+        wd, sd, bd = words.to(gpu), scales.to(gpu), biases.to(gpu)
+        rc = capi().gdsllm_dequant_gemm_affine_q4(ptr(wd), ptr(sd), ptr(bd), xbuf.data_ptr(), ptr(y), M, K, g, T, ldx,
+                                                  ldy, stream())
+        deq = affine_dequant_np(words, scales, biases, g).reshape(M, K)
+    else:
+        w = (syn.q4_0_weights if fmt == "q4_0" else syn.q8_0_weights)(M, K, gen(seed))
+        wd = w.to(gpu)
+        fn = capi().gdsllm_dequant_gemm_q4_0 if fmt == "q4_0" else capi().gdsllm_dequant_gemm_q8_0
+        rc = fn(ptr(wd), xbuf.data_ptr(), ptr(y), M, K, T, ldx, ldy, stream())
+        deq = (oq.dequant_q4_0 if fmt == "q4_0" else oq.dequant_q8_0)(to_np(w)).reshape(M, K)
+    torch.cuda.synchronize()
+    if fmt != "q4_0" and K % 256:
+        assert rc == 2, f"{what}: expected GDSLLM_ERR_UNSUPPORTED (2), got {rc}"
+        assert np.all(to_np(y) == SENTINEL), f"{what}: a refused call wrote y"
+        return
+    check(rc)
+    rows, pad = _y_rows(y, T, M, ldy)
+    assert np.all(pad == SENTINEL), f"{what}: written outside the output rows"
+    _gemv_close(rows, deq, to_np(x), what)
+
+
+def _h_close(hk, wgq, wuq, x, what):
+    """h = fp16(fp16(silu(g)) * u) of the gate/up launches against the
+    oracle's g and u: per element within the GEMV bound on g and u (one fp16
+    ulp plus 1e-2 of ||w_r * x||) carried through silu (slope below 1.1) and
+    the product, plus the roundings of silu and of h; relative L2 over 256
+    or more outputs."""
+    gx, ux = oq.gemv(wgq, x), oq.gemv(wuq, x)
+    gq, uq = gx.astype(np.float16), ux.astype(np.float16)
+    h_oracle = (oq.silu_fp16(gq).astype(np.float32) * uq.astype(np.float32)).astype(np.float64)
+    hk = np.asarray(hk, dtype=np.float64)
+    dg = oq.fp16_ulp(gx) + oq.GEMV_MAX_NORM * oq.row_norms(wgq, x)
+    du = oq.fp16_ulp(ux) + oq.GEMV_MAX_NORM * oq.row_norms(wuq, x)
+    sx = gx / (1.0 + np.exp(-np.clip(gx, -60, 60)))
+    ds = 1.1 * dg + oq.fp16_ulp(sx)
+    bound = np.abs(sx) * du + np.abs(ux) * ds + ds * du + 2 * oq.fp16_ulp(h_oracle)
+    bad = np.abs(hk - h_oracle) > bound
+    assert not bad.any(), f"{what}: {int(bad.sum())} h values beyond the carried GEMV tolerance"
+    if hk.size >= 256:
+        rel = float(np.linalg.norm(hk - h_oracle) / max(np.linalg.norm(h_oracle), 1e-30))
+        assert rel <= oq.GEMV_REL_L2, f"{what}: h rel L2 {rel:.3e}"
+
+
+@PROPS
+@given(fmt=st.sampled_from(["q4_0", "q8_0"]), F=st.integers(1, 600), kb=st.integers(1, 24), T=st.integers(1, 200),
+       ldh_pad=st.integers(0, 5), seed=st.integers(0, 2 ** 16))
+def test_gate_up_silu_gemm_property(gpu, fmt, F, kb, T, ldh_pad, seed):
+    """The prefill gate/up/SiLU launch: h rows of T tokens."""
+    K = 256 * kb
+    make = syn.q4_0_weights if fmt == "q4_0" else syn.q8_0_weights
+    dq = oq.dequant_q4_0 if fmt == "q4_0" else oq.dequant_q8_0
+    wg, wu = make(F, K, gen(seed)), make(F, K, gen(seed + 1))
+    x = syn.activations(T, K, gen(seed + 2))
+    ldh = F + ldh_pad
+    h = _y_padded(T, F, ldh, gpu)
+    wgd, wud, xd = wg.to(gpu), wu.to(gpu), x.to(gpu)
+    fn = (capi().gdsllm_dequant_gemm_gate_up_silu_q4_0 if fmt == "q4_0"
+          else capi().gdsllm_dequant_gemm_gate_up_silu_q8_0)
+    check(fn(ptr(wgd), ptr(wud), ptr(xd), ptr(h), F, K, T, K, ldh, stream()))
+    torch.cuda.synchronize()
+    rows, pad = _y_rows(h, T, F, ldh)
+    what = f"{fmt} gate/up/SiLU GEMM {F}x{K} T{T} ldh {ldh}"
+    assert np.all(pad == SENTINEL), f"{what}: written outside h's rows"
+    _h_close(rows, dq(to_np(wg)).reshape(F, K), dq(to_np(wu)).reshape(F, K), to_np(x), what)
+
+
+# (hidden, ffn) pairs: the row-span gather (hidden % 2048 == 0, ffn/32 in
+# {16, 32, 64}) and the general path
+MOE_DIMS = [(2048, 512), (2048, 1024), (4096, 512), (4096, 1024), (512, 256), (1024, 512), (768, 256), (2048, 256)]
+
+
+@settings(PROPS, max_examples=30)
+@given(dims=st.sampled_from(MOE_DIMS), g=st.sampled_from([32, 64, 128]), E=st.integers(1, 24),
+       k=st.integers(1, 12), bad=st.sampled_from([None, None, None, -1, "E"]), seed=st.integers(0, 2 ** 16))
+def test_moe_gather_property(gpu, dims, g, E, k, bad, seed):
+    """The top-k expert gather over drawn pools and picks (distinct experts,
+    now and then one index outside [0, E)), checked phase by phase and end to
+    end against the oracle."""
+    H, F = dims
+    k = min(k, E)
+    gate, up, down = moe_pool(E, H, F, g, seed)
+    x = syn.activations(1, H, gen(seed + 1))
+    idx = torch.randperm(E, generator=gen(seed + 2))[:k].to(torch.int32)
+    if bad is not None:
+        idx[int(seed % k)] = -1 if bad == -1 else E
+    wts = torch.softmax(torch.randn(k, generator=gen(seed + 3)), 0).to(torch.float16)
+    dev = [tuple(t.to(gpu) for t in p) for p in (gate, up, down)]
+    y, ws, hk = moe_gather(*dev, x.to(gpu), idx.to(gpu), wts.to(gpu), g, return_workspace=True)
+    if all(int(e) < 0 or int(e) >= E for e in idx):
+        assert np.all(to_np(y) == 0), "no valid expert: the output is zero"
+        return
+    check_moe(y, ws, gate, up, down, x, to_np(idx), wts, g, E, hk)

@@ -327,3 +327,83 @@ def test_moe_gather_property(gpu, dims, g, E, k, bad, seed):
         assert np.all(to_np(y) == 0), "no valid expert: the output is zero"
         return
     check_moe(y, ws, gate, up, down, x, to_np(idx), wts, g, E, hk)
+
+
+@PROPS
+@given(E=st.integers(1, 4096), k=st.integers(1, 64), n=st.integers(1, 8), ld_pad=st.integers(0, 7),
+       kind=st.sampled_from(["normal", "ties", "specials"]), seed=st.integers(0, 2 ** 16))
+def test_route_topk_property(gpu, E, k, n, ld_pad, kind, seed):
+    """On-device top-k + softmax of fp16 logit rows ld apart: the picks equal
+    the oracle's (value descending, ties to the lower index, NaN above every
+    number, -0 == +0); every weight within one fp16 ulp of the oracle's (the
+    device's exp may round the last bit differently)."""
+    k = min(k, E)
+    ld = E + ld_pad
+    rng = np.random.default_rng(seed)
+    if kind == "normal":
+        v = rng.standard_normal((n, E)).astype(np.float16)
+    elif kind == "ties":
+        v = (rng.integers(-3, 4, size=(n, E)) * 0.25).astype(np.float16)
+    else:
+        v = rng.standard_normal((n, E)).astype(np.float16)
+        specials = np.array([np.nan, np.inf, -np.inf, 0.0, -0.0, 65504.0, -65504.0], dtype=np.float16)
+        mask = rng.random((n, E)) < 0.1
+        v[mask] = rng.choice(specials, size=int(mask.sum()))
+    buf = np.zeros((n, ld), dtype=np.float16)
+    buf[:, :E] = v
+    logits = torch.from_numpy(buf).reshape(-1).to(gpu)
+    idx = torch.empty(n, k, dtype=torch.int32, device=gpu)
+    w = torch.empty(n, k, dtype=torch.float16, device=gpu)
+    check(capi().gdsllm_moe_route_topk(ptr(logits), E, n, ld, k, ptr(idx), ptr(w), stream()))
+    torch.cuda.synchronize()
+    ridx, rw = oq.route_topk(v, k)
+    what = f"route E{E} k{k} n{n} ld{ld} {kind}"
+    np.testing.assert_array_equal(to_np(idx), ridx, err_msg=what)
+    got, want = to_np(w).astype(np.float16), np.asarray(rw, dtype=np.float16)
+    same = (got.view(np.uint16) == want.view(np.uint16)) | (np.isnan(got) & np.isnan(want))
+    ulps = np.abs(got.view(np.int16).astype(np.int32) - want.view(np.int16).astype(np.int32))
+    assert np.all(same | (ulps <= 1)), f"{what}: a weight differs by more than one fp16 ulp"
+
+
+@PROPS
+@given(fmt=st.sampled_from(["q4_0", "q8_0"]), vocab=st.integers(1, 3000), hb=st.integers(1, 64),
+       n=st.integers(1, 300), seed=st.integers(0, 2 ** 16))
+def test_embed_rows_property(gpu, fmt, vocab, hb, n, seed):
+    """Row gather of a GGUF table: each row bit-identical to the whole-table
+    dequant's row, ids outside [0, vocab) give zeros."""
+    hidden = 64 * hb
+    raw = (syn.q4_0_weights if fmt == "q4_0" else syn.q8_0_weights)(vocab, hidden, gen(seed))
+    table = (oq.dequant_q4_0 if fmt == "q4_0" else oq.dequant_q8_0)(to_np(raw)).reshape(vocab, hidden)
+    ids = torch.randint(-3, vocab + 3, (n,), generator=gen(seed + 1), dtype=torch.int64)
+    src, ids_dev = raw.to(gpu), ids.to(gpu)
+    out = torch.full((n * hidden + 8,), SENTINEL, dtype=torch.float16, device=gpu)
+    fn = capi().gdsllm_embed_q4_0 if fmt == "q4_0" else capi().gdsllm_embed_q8_0
+    check(fn(ptr(src), ptr(ids_dev), n, vocab, hidden, ptr(out), stream()))
+    torch.cuda.synchronize()
+    got = to_np(out)
+    rows = got[: n * hidden].reshape(n, hidden).view(np.uint16)
+    ok_ids = (ids >= 0) & (ids < vocab)
+    want = np.zeros((n, hidden), dtype=np.uint16)
+    want[ok_ids.numpy()] = table[ids[ok_ids].numpy()].view(np.uint16)
+    assert np.array_equal(rows, want), f"{fmt} vocab {vocab} hidden {hidden} n {n}: rows differ"
+    assert np.all(got[n * hidden:] == SENTINEL), f"{fmt}: written past the last row"
+
+
+@PROPS
+@given(M=st.integers(1, 700), kc=st.integers(1, 300), B=st.integers(1, 8), ldx_pad=st.integers(0, 9),
+       ldy_pad=st.integers(0, 5), seed=st.integers(0, 2 ** 16))
+def test_int8_gemv_property(gpu, M, kc, B, ldx_pad, ldy_pad, seed):
+    """Per-column int8 weights (fast path for in_dim % 16 == 0 with aligned
+    rows, the general kernel otherwise)."""
+    K = 8 * kc
+    q, sc = syn.int8_weights(M, K, gen(seed))
+    ldx, ldy = K + ldx_pad, M + ldy_pad
+    x, xbuf, _ = _x_strided(B, K, ldx, 0, seed + 1, gpu)
+    y = _y_padded(B, M, ldy, gpu)
+    qd, sd = q.to(gpu), sc.to(gpu)
+    check(capi().gdsllm_fused_int8_gemv(ptr(qd), ptr(sd), xbuf.data_ptr(), ptr(y), M, K, B, ldx, ldy, stream()))
+    torch.cuda.synchronize()
+    rows, pad = _y_rows(y, B, M, ldy)
+    what = f"int8 {M}x{K} B{B} ldx {ldx} ldy {ldy}"
+    assert np.all(pad == SENTINEL), f"{what}: written outside the output rows"
+    _gemv_close(rows, oq.dequant_int8(to_np(q), to_np(sc)), to_np(x), what)

@@ -7,15 +7,13 @@ The dense GEMMs replace the reference's prefill route dequant -> F.linear
 replaces the per-expert loop of runtime/qwen_moe.py:475-492.
 """
 
-import ctypes
-import functools
 
 import numpy as np
 import pytest
 import torch
 
-from helpers import (affine_dequant_np, assert_gemv_close, capi, check, experts_struct, gen, oq, ptr, stream, syn,
-                     to_np)
+from helpers import (affine_dequant_np, assert_gemv_close, capi, check, check_moe_prefill, check_sort, gen, moe_prefill,
+                     oq, ptr, stream, syn, to_np)
 
 pytestmark = pytest.mark.gpu
 
@@ -219,103 +217,6 @@ def test_dequant_gemm_unsupported_shapes(gpu):
 # ------------------------------------------------------------ MoE prefill --
 
 
-def _prefill_layout(T, k, F, H, E):
-    """Byte offsets of the library's MoE-prefill workspace regions (tok, pos,
-    tiles, ntiles, h, d), 256-byte aligned, in the order the library lays them out."""
-    up = lambda v: (v + 255) & ~255  # noqa: E731
-    n = T * k
-    max_tiles = n // 32 + min(E, n) + 1
-    o, out = 0, {}
-    for name, size in (("tok", 4 * n), ("pos", 4 * n), ("tiles", 16 * max_tiles), ("ntiles", 16), ("h", 2 * n * F),
-                       ("d", 2 * n * H)):
-        out[name] = o
-        o = up(o + size)
-    out["total"] = o
-    return out
-
-
-def _moe_prefill(gate, up, down, xd, idx_d, w_d, g, T, k):
-    gs, us, ds = (experts_struct(*p, g) for p in (gate, up, down))
-    E, F, H = gs.num_experts, gs.out_dim, gs.in_dim
-    ws_bytes = capi().gdsllm_moe_prefill_workspace_size(T, k, F, H, E)
-    L = _prefill_layout(T, k, F, H, E)
-    assert ws_bytes == L["total"]
-    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=xd.device)
-    y = torch.full((T, H), 3.0, dtype=torch.float16, device=xd.device)
-    check(capi().gdsllm_moe_prefill_affine_q4(ctypes.byref(gs), ctypes.byref(us), ctypes.byref(ds), ptr(xd), H,
-                                              ptr(idx_d), ptr(w_d), T, k, ptr(y), H, ptr(ws), ws_bytes, stream()))
-    torch.cuda.synchronize()
-    n = T * k
-    part = lambda name, dt, count: ws[L[name]:L[name] + count * dt.itemsize].view(dt)  # noqa: E731
-    tok = to_np(part("tok", torch.int32, n))
-    pos = to_np(part("pos", torch.int32, n)).reshape(T, k)
-    ntiles = int(to_np(part("ntiles", torch.int32, 1))[0])
-    tiles = to_np(part("tiles", torch.int32, 4 * ntiles)).reshape(ntiles, 4)
-    hbuf = to_np(part("h", torch.float16, n * F)).reshape(n, F)
-    dbuf = to_np(part("d", torch.float16, n * H)).reshape(n, H)
-    return y, tok, pos, tiles, hbuf, dbuf
-
-
-def _check_sort(idx, tok, pos, tiles, E, BT=32):
-    """Every in-range entry (t, j) has a position p with tok[p] == t; positions
-    are a permutation of 0 .. n_valid-1; the tiles cover each expert's positions
-    in runs of at most BT."""
-    T, k = idx.shape
-    valid = (idx >= 0) & (idx < E)
-    assert (pos[~valid] == -1).all()
-    pv = pos[valid]
-    assert sorted(pv.tolist()) == list(range(int(valid.sum())))
-    for t, j in zip(*np.nonzero(valid)):
-        assert tok[pos[t, j]] == t
-    owner = np.full(int(valid.sum()), -1)
-    owner[pv] = idx[valid]
-    covered = np.zeros(len(owner), bool)
-    for e, p0, cnt, _ in tiles:
-        assert 1 <= cnt <= BT and (owner[p0:p0 + cnt] == e).all()
-        assert not covered[p0:p0 + cnt].any()
-        covered[p0:p0 + cnt] = True
-    assert covered.all()
-
-
-def _dq_fn(pool, g):
-    @functools.lru_cache(maxsize=None)
-    def f(e):
-        if e < 0 or e >= pool[0].shape[0]:
-            return None
-        w, s, b = (t[e].cpu() for t in pool)
-        return affine_dequant_np(w, s, b, g).reshape(w.shape[0], -1)
-    return lambda e: f(int(e))
-
-
-def _check_moe_prefill(y, tok, pos, hbuf, dbuf, gate, up, down, x, idx, wts, g, E, sample=None):
-    T, k = idx.shape
-    gf, uf, dn = _dq_fn(gate, g), _dq_fn(up, g), _dq_fn(down, g)
-    toks = range(T) if sample is None else sample
-    xn = to_np(x)
-    # (1) phase 2: each down row against the oracle product of the kernel's own h
-    for t in toks:
-        for j in range(k):
-            e = int(idx[t, j])
-            if gf(e) is None:
-                continue
-            p = pos[t, j]
-            assert_gemv_close(dbuf[p][None, :], dn(e), hbuf[p][None, :], f"down t{t} j{j}")
-    # (2) the combine, replayed from the kernel's down rows: bit for bit
-    want = oq.moe_prefill_combine(dbuf, pos, wts)
-    assert np.array_equal(to_np(y).view(np.uint16), want.view(np.uint16)), "combine differs from the fp16 fold"
-    # (3) h and end to end against the all-oracle prefill on the sampled tokens
-    sel = np.asarray(list(toks))
-    ref, inter = oq.moe_prefill(xn[sel], gf, uf, dn, idx[sel], wts[sel])
-    hk = np.stack([hbuf[pos[t, j]] for t in sel for j in range(k) if gf(int(idx[t, j])) is not None]).astype(np.float64)
-    hr = np.stack([inter[(r, j)][0] for r in range(len(sel)) for j in range(k) if (r, j) in inter]).astype(np.float64)
-    relh = float(np.linalg.norm(hk - hr) / np.linalg.norm(hr))
-    got = to_np(y)[sel].astype(np.float64)
-    rel = float(np.linalg.norm(got - ref.astype(np.float64)) / np.linalg.norm(ref.astype(np.float64)))
-    print(f"moe prefill: h rel L2 {relh:.2e}, expert_output rel L2 {rel:.2e}")
-    assert relh <= oq.GEMV_REL_L2, f"h rel L2 {relh:.3e}"
-    assert np.isfinite(got).all() and rel <= oq.GEMV_REL_L2, f"expert_output rel L2 {rel:.3e}"
-
-
 PREFILL_CASES = [(16, 1024, 512, 64, 4, 37), (64, 2048, 1024, 64, 10, 100), (8, 512, 256, 32, 3, 9),
                  (32, 1024, 256, 128, 8, 65), (4, 1024, 512, 64, 2, 300)]
 
@@ -330,11 +231,11 @@ def test_moe_prefill(gpu, E, H, F, g, k, T):
     idx = np.stack([np.random.default_rng(5602 + t).choice(E, k, replace=False) for t in range(T)]).astype(np.int32)
     wts = torch.softmax(torch.randn(T, k, generator=gen(5603)), -1).to(torch.float16)
     dev = [tuple(t.to(gpu) for t in p) for p in (gate, up, down)]
-    y, tok, pos, tiles, hbuf, dbuf = _moe_prefill(*dev, x.to(gpu), torch.from_numpy(idx).to(gpu), wts.to(gpu), g, T, k)
-    _check_sort(idx, tok, pos, tiles, E)
-    _check_moe_prefill(y, tok, pos, hbuf, dbuf, gate, up, down, x, idx, to_np(wts), g, E)
+    y, tok, pos, tiles, hbuf, dbuf = moe_prefill(*dev, x.to(gpu), torch.from_numpy(idx).to(gpu), wts.to(gpu), g, T, k)
+    check_sort(idx, tok, pos, tiles, E)
+    check_moe_prefill(y, tok, pos, hbuf, dbuf, gate, up, down, x, idx, to_np(wts), g, E)
     # a second run gives the same bits (positions inside an expert may differ)
-    y2 = _moe_prefill(*dev, x.to(gpu), torch.from_numpy(idx).to(gpu), wts.to(gpu), g, T, k)[0]
+    y2 = moe_prefill(*dev, x.to(gpu), torch.from_numpy(idx).to(gpu), wts.to(gpu), g, T, k)[0]
     assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
 
 
@@ -347,9 +248,9 @@ def test_moe_prefill_out_of_range_experts(gpu):
     idx[0, 1], idx[3, 0], idx[7, 2] = -1, E, 1 << 20
     wts = torch.softmax(torch.randn(T, k, generator=gen(5703)), -1).to(torch.float16)
     dev = [tuple(t.to(gpu) for t in p) for p in pools]
-    y, tok, pos, tiles, hbuf, dbuf = _moe_prefill(*dev, x.to(gpu), torch.from_numpy(idx).to(gpu), wts.to(gpu), g, T, k)
-    _check_sort(idx, tok, pos, tiles, E)
-    _check_moe_prefill(y, tok, pos, hbuf, dbuf, *pools, x, idx, to_np(wts), g, E)
+    y, tok, pos, tiles, hbuf, dbuf = moe_prefill(*dev, x.to(gpu), torch.from_numpy(idx).to(gpu), wts.to(gpu), g, T, k)
+    check_sort(idx, tok, pos, tiles, E)
+    check_moe_prefill(y, tok, pos, hbuf, dbuf, *pools, x, idx, to_np(wts), g, E)
 
 
 def test_moe_prefill_cfg2_pool_512_tokens(gpu):
@@ -363,8 +264,8 @@ def test_moe_prefill_cfg2_pool_512_tokens(gpu):
     x = syn.activations(T, H, gen(5801))
     idx = np.stack([np.random.default_rng(5802 + t).choice(E, k, replace=False) for t in range(T)]).astype(np.int32)
     wts = torch.softmax(torch.randn(T, k, generator=gen(5803)), -1).to(torch.float16)
-    y, tok, pos, tiles, hbuf, dbuf = _moe_prefill(*dev, x.to(gpu), torch.from_numpy(idx).to(gpu), wts.to(gpu), g, T, k)
-    _check_sort(idx, tok, pos, tiles, E)
+    y, tok, pos, tiles, hbuf, dbuf = moe_prefill(*dev, x.to(gpu), torch.from_numpy(idx).to(gpu), wts.to(gpu), g, T, k)
+    check_sort(idx, tok, pos, tiles, E)
     sample = sorted(np.random.default_rng(5804).choice(T, 8, replace=False).tolist())
 
     class Lazy:
@@ -376,7 +277,7 @@ def test_moe_prefill_cfg2_pool_512_tokens(gpu):
             return self.t[e].cpu()
 
     pools = [tuple(Lazy(t) for t in p) for p in dev]
-    _check_moe_prefill(y, tok, pos, hbuf, dbuf, *pools, x, idx, to_np(wts), g, E, sample=sample)
+    check_moe_prefill(y, tok, pos, hbuf, dbuf, *pools, x, idx, to_np(wts), g, E, sample=sample)
     del dev
     torch.cuda.empty_cache()
 

@@ -22,7 +22,8 @@ import torch
 from hypothesis import HealthCheck, given, settings
 from hypothesis import strategies as st
 
-from helpers import affine_dequant_np, capi, check, check_moe, gen, moe_gather, moe_pool, oq, ptr, stream, syn, to_np
+from helpers import (affine_dequant_np, capi, check, check_moe, check_moe_prefill, check_sort, gen, moe_gather,
+                     moe_pool, moe_prefill, oq, ptr, stream, syn, to_np)
 
 pytestmark = pytest.mark.gpu
 
@@ -407,3 +408,31 @@ def test_int8_gemv_property(gpu, M, kc, B, ldx_pad, ldy_pad, seed):
     what = f"int8 {M}x{K} B{B} ldx {ldx} ldy {ldy}"
     assert np.all(pad == SENTINEL), f"{what}: written outside the output rows"
     _gemv_close(rows, oq.dequant_int8(to_np(q), to_np(sc)), to_np(x), what)
+
+
+# (hidden, ffn): both multiples of 256, as the grouped prefill requires
+PREFILL_DIMS = [(512, 256), (1024, 256), (1024, 512), (2048, 512), (768, 512)]
+
+
+@settings(PROPS, max_examples=25)
+@given(dims=st.sampled_from(PREFILL_DIMS), g=st.sampled_from([32, 64, 128]), E=st.integers(1, 40),
+       k=st.integers(1, 10), T=st.integers(1, 120), bad=st.integers(0, 3), seed=st.integers(0, 2 ** 16))
+def test_moe_prefill_property(gpu, dims, g, E, k, T, bad, seed):
+    """The grouped-expert MoE prefill over drawn pools, token counts and picks
+    (distinct experts per token, `bad` entries replaced by indices outside [0,
+    E)): the device sort, each down row, the fp16 combine bit for bit, and the
+    end result against the oracle."""
+    H, F = dims
+    k = min(k, E)
+    gg = gen(seed)
+    pools = [syn.affine_q4_weights(s, g, gg) for s in ([E, F, H], [E, F, H], [E, H, F])]
+    x = syn.activations(T, H, gen(seed + 1))
+    rng = np.random.default_rng(seed + 2)
+    idx = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    for i in range(min(bad, T * k - 1)):
+        idx.flat[int(rng.integers(1, T * k))] = -1 if i % 2 else E + i
+    wts = torch.softmax(torch.randn(T, k, generator=gen(seed + 3)), -1).to(torch.float16)
+    dev = [tuple(t.to(gpu) for t in p) for p in pools]
+    y, tok, pos, tiles, hbuf, dbuf = moe_prefill(*dev, x.to(gpu), torch.from_numpy(idx).to(gpu), wts.to(gpu), g, T, k)
+    check_sort(idx, tok, pos, tiles, E)
+    check_moe_prefill(y, tok, pos, hbuf, dbuf, *pools, x, idx, to_np(wts), g, E)

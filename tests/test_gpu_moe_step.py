@@ -15,6 +15,8 @@ import ctypes
 import numpy as np
 import pytest
 import torch
+from hypothesis import HealthCheck, given, settings
+from hypothesis import strategies as st
 
 from gdsllm_amd import capi, check
 from helpers import affine_dequant_np, experts_struct, gen, moe_gather, oq, ptr, stream, syn, to_np
@@ -201,3 +203,52 @@ def test_moe_step_routed_matches_route_then_step(gpu, E, H, F, k, ties):
         top = sorted((E - 1, 5, 2, E // 2))[:min(k, 4)]
         assert idx[:len(top)].tolist() == top, "equal logits must come out lowest index first"
     np.testing.assert_array_equal(to_np(y).view(np.uint16), to_np(want).view(np.uint16))
+
+
+# Drawn layers: expert count, hidden/ffn, group size, top-k and tied router
+# rows, pools generated on the device (the properties compare two device paths
+# bit for bit, so no oracle pass is needed)
+STEP_DIMS = [(2048, 512), (4096, 512), (2048, 1024), (4096, 1024), (6144, 1024), (8192, 512)]
+
+
+@settings(max_examples=25, deadline=None, derandomize=True, database=None, print_blob=True,
+          suppress_health_check=[HealthCheck.function_scoped_fixture, HealthCheck.too_slow])
+@given(E8=st.integers(1, 32), dims=st.sampled_from(STEP_DIMS), g=st.sampled_from([32, 64, 128]),
+       k=st.integers(1, 12), ties=st.booleans(), seed=st.integers(0, 2 ** 16))
+def test_moe_step_property(gpu, E8, dims, g, k, ties, seed):
+    """Over drawn layers: the fused step is bit-identical to the separate
+    launches on the same picks, and the routed step gives the picks, weights
+    and output of router GEMV + top-k + fused step, bit for bit."""
+    E = 8 * E8
+    H, F = dims
+    k = min(k, E, 31 if F == 512 else 15)
+    gg = torch.Generator(device=gpu).manual_seed(seed)
+    routed = [syn.affine_q4_weights(s, g, gg) for s in ([E, F, H], [E, F, H], [E, H, F])]
+    shared = [_shared_stacked(syn.affine_q4_weights(s, g, gg)) for s in ([F, H], [F, H], [H, F])]
+    x = syn.activations(1, H, gen(seed + 1)).to(gpu)
+    picks = torch.randperm(E, generator=gen(seed + 2))[:k].to(torch.int32).to(gpu)
+    rw = torch.softmax(torch.randn(k, generator=gen(seed + 3)), 0).to(torch.float16).to(gpu)
+    sgw = (torch.randn(H, generator=gen(seed + 4)) * 0.02).to(torch.float16).to(gpu)
+    what = f"E{E} H{H} F{F} g{g} k{k}"
+    y = _step(routed, shared, x, picks, rw, sgw, g, k, gpu)
+    want = _separate(routed, shared, x, picks, rw, sgw, g, gpu)
+    np.testing.assert_array_equal(to_np(y).view(np.uint16), to_np(want).view(np.uint16), err_msg=what)
+
+    router = (torch.randn(E, H, generator=gen(seed + 5)) * 0.02).to(torch.float16)
+    if ties:
+        hot = _gate_row(x.cpu(), 8.0)
+        for e in {E - 1, E // 2, 0}:
+            router[e] = hot
+    router = router.to(gpu)
+    y2, idx, w = _routed_step(router, routed, shared, x, sgw, g, k, gpu)
+    logits = torch.empty(E, dtype=torch.float16, device=gpu)
+    check(capi().gdsllm_gemv_f16(ptr(router), ptr(x), ptr(logits), E, H, 1, H, E, stream()))
+    ridx = torch.empty(k, dtype=torch.int32, device=gpu)
+    rw2 = torch.empty(k, dtype=torch.float16, device=gpu)
+    check(capi().gdsllm_moe_route_topk(ptr(logits), E, 1, E, k, ptr(ridx), ptr(rw2), stream()))
+    torch.cuda.synchronize()
+    want2 = _step(routed, shared, x, ridx, rw2, sgw, g, k, gpu)
+    assert torch.equal(idx, ridx), f"{what}: picks {idx.tolist()} != {ridx.tolist()}"
+    assert torch.equal(w.view(torch.int16), rw2.view(torch.int16)), f"{what}: weights differ"
+    np.testing.assert_array_equal(to_np(y2).view(np.uint16), to_np(want2).view(np.uint16), err_msg=what)
+    del routed, shared
